@@ -1,0 +1,24 @@
+"""aiter_amd — MI355X (gfx950) scaled-GEMM hot path with aiter's API.
+
+Ops (all backed by hand-written HIP kernels in libaiter_amd.so):
+  gemm_a4w4, gemm_a4w4_asm, gemm_a4w4_blockscale(_tune)   MXFP4 x MXFP4
+  gemm_a8w4_mxfp8, gemm_a8w4_mxfp8_dynamic                MXFP8 x MXFP4
+  gemm_a16w16, tgemm.mm, gemm_a16w16_opus, gemm_a16w16_asm bf16
+  get_hip_quant / get_triton_quant(QuantType.per_1x32), quant_mxfp4_hip,
+  per_1x32_mx_quant_hip, dynamic_mxfp4_quant, dynamic_mxfp8_quant
+  shuffle_weight, shuffle_scale
+"""
+from . import dtypes
+from .gemm_common import get_padded_m
+from .gemm_op_a4w4 import (compute_gemm_SplitK, gemm_a4w4, gemm_a4w4_asm, gemm_a4w4_blockscale,
+                           gemm_a4w4_blockscale_tune, get_GEMM_config)
+from .gemm_op_a8w4 import gemm_a8w4_mxfp8, gemm_a8w4_mxfp8_dynamic
+from .gemm_op_a16w16 import gemm_a16w16_asm
+from .opus import gemm_a16w16_opus, opus_gemm_a16w16_tune, opus_gemm_workspace_init
+from .quant import (MxScaleRoundMode, QuantType, dynamic_mxfp4_quant, dynamic_mxfp8_quant, get_hip_quant,
+                    get_triton_quant, per_1x32_f4_quant_hip, per_1x32_f4_quant_triton, per_1x32_mx_quant_hip,
+                    quant_mxfp4_hip)
+from .shuffle import e8m0_shuffle, shuffle_scale, shuffle_weight
+from .tuned_gemm import TunedGemm, gemm_a16w16, get_GEMM_A16W16_config, tgemm
+
+__all__ = [n for n in dir() if not n.startswith("_")]

@@ -1,0 +1,586 @@
+// Host launchers and C-ABI entry points of the scaled-GEMM family.
+//
+// Every kernel instance has a stable name and integer id (the `kernelName` /
+// `kernelId` the tuned CSVs refer to).  Families:
+//   a4w4   : A e2m1 [M,K/2] row-major,  B e2m1 preshuffled (or row-major)
+//   a8w4   : A e4m3 [M,K] (row-major or preshuffled), B e2m1 preshuffled
+//   a16w16 : A bf16 [M,K], B bf16 [N,K] (row-major or preshuffled)
+// Each family has tile instances (LDS double-buffered, 4 waves) and skinny
+// instances (HBM streaming for small M, optional split-K over blocks).
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gemm_kernels.h"
+
+namespace aiter_amd {
+
+std::string& last_error() {
+    thread_local std::string msg;
+    return msg;
+}
+
+int device_cu_count(int dev) {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    hipDeviceProp_t prop;
+    AA_HIP(hipGetDeviceProperties(&prop, dev));
+    cache[dev] = prop.multiProcessorCount;
+    return prop.multiProcessorCount;
+}
+
+namespace {
+
+enum Family : int { kA4W4 = 0, kA8W4 = 1, kA16W16 = 2 };
+
+struct Variant {
+    bool a_pre, b_pre, out_f32;
+};
+
+using LaunchFn = void (*)(const GemmParams&, dim3, hipStream_t);
+
+struct Instance {
+    int id;
+    std::string name;
+    Family fam;
+    bool skinny;
+    int bm, bn;   // tile: block tile; skinny: bm = 16*MF rows covered, bn = 16
+    bool split;   // skinny split-K over blocks
+    Variant var;
+    LaunchFn fn;
+};
+
+template <int KA, int KB, int BM, int BN, bool AP, bool BP, bool OF>
+void launch_tile(const GemmParams& p, dim3 grid, hipStream_t s) {
+    gemm_tile_kernel<KA, KB, BM, BN, AP, BP, OF><<<grid, 256, 0, s>>>(p);
+}
+
+constexpr int kSkinnyWaves = 8;
+
+template <int KA, int MF, bool BP, bool SPLIT, bool OF>
+void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
+    gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
+}
+
+std::vector<Instance>& registry() {
+    static std::vector<Instance> reg;
+    static std::once_flag once;
+    std::call_once(once, [] {
+        int id = 0;
+        auto tile = [&](Family f, int bm, int bn, Variant v, LaunchFn fn, const char* fam) {
+            std::string nm = std::string(fam) + "_tile_" + std::to_string(bm) + "x" + std::to_string(bn);
+            if (v.a_pre) nm += "_apre";
+            if (!v.b_pre) nm += "_bplain";
+            if (v.out_f32) nm += "_f32";
+            reg.push_back({id++, nm, f, false, bm, bn, false, v, fn});
+        };
+        auto skinny = [&](Family f, int mf, bool split, Variant v, LaunchFn fn, const char* fam) {
+            std::string nm = std::string(fam) + "_skinny_m" + std::to_string(16 * mf);
+            if (split) nm += "_splitk";
+            if (v.a_pre) nm += "_apre";
+            if (!v.b_pre) nm += "_bplain";
+            if (v.out_f32) nm += "_f32";
+            reg.push_back({id++, nm, f, true, 16 * mf, 16, split, v, fn});
+        };
+        // ---- a4w4 (B preshuffled) ----
+        const Variant pre{false, true, false}, plain{false, false, false};
+        tile(kA4W4, 256, 256, pre, launch_tile<kFp4, kFp4, 256, 256, false, true, false>, "a4w4");
+        tile(kA4W4, 256, 128, pre, launch_tile<kFp4, kFp4, 256, 128, false, true, false>, "a4w4");
+        tile(kA4W4, 128, 256, pre, launch_tile<kFp4, kFp4, 128, 256, false, true, false>, "a4w4");
+        tile(kA4W4, 128, 128, pre, launch_tile<kFp4, kFp4, 128, 128, false, true, false>, "a4w4");
+        tile(kA4W4, 64, 256, pre, launch_tile<kFp4, kFp4, 64, 256, false, true, false>, "a4w4");
+        tile(kA4W4, 64, 128, pre, launch_tile<kFp4, kFp4, 64, 128, false, true, false>, "a4w4");
+        tile(kA4W4, 64, 64, pre, launch_tile<kFp4, kFp4, 64, 64, false, true, false>, "a4w4");
+        skinny(kA4W4, 1, false, pre, launch_skinny<kFp4, 1, true, false, false>, "a4w4");
+        skinny(kA4W4, 2, false, pre, launch_skinny<kFp4, 2, true, false, false>, "a4w4");
+        skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false>, "a4w4");
+        skinny(kA4W4, 1, true, pre, launch_skinny<kFp4, 1, true, true, false>, "a4w4");
+        skinny(kA4W4, 2, true, pre, launch_skinny<kFp4, 2, true, true, false>, "a4w4");
+        skinny(kA4W4, 4, true, pre, launch_skinny<kFp4, 4, true, true, false>, "a4w4");
+        // a4w4 with row-major B (bpreshuffle = 0)
+        tile(kA4W4, 256, 256, plain, launch_tile<kFp4, kFp4, 256, 256, false, false, false>, "a4w4");
+        tile(kA4W4, 128, 128, plain, launch_tile<kFp4, kFp4, 128, 128, false, false, false>, "a4w4");
+        tile(kA4W4, 64, 128, plain, launch_tile<kFp4, kFp4, 64, 128, false, false, false>, "a4w4");
+        skinny(kA4W4, 1, false, plain, launch_skinny<kFp4, 1, false, false, false>, "a4w4");
+        skinny(kA4W4, 2, false, plain, launch_skinny<kFp4, 2, false, false, false>, "a4w4");
+        skinny(kA4W4, 4, false, plain, launch_skinny<kFp4, 4, false, false, false>, "a4w4");
+        // ---- a8w4 ----
+        const Variant a8{false, true, false}, a8p{true, true, false};
+        tile(kA8W4, 128, 256, a8, launch_tile<kFp8, kFp4, 128, 256, false, true, false>, "a8w4");
+        tile(kA8W4, 128, 128, a8, launch_tile<kFp8, kFp4, 128, 128, false, true, false>, "a8w4");
+        tile(kA8W4, 64, 256, a8, launch_tile<kFp8, kFp4, 64, 256, false, true, false>, "a8w4");
+        tile(kA8W4, 64, 128, a8, launch_tile<kFp8, kFp4, 64, 128, false, true, false>, "a8w4");
+        tile(kA8W4, 128, 256, a8p, launch_tile<kFp8, kFp4, 128, 256, true, true, false>, "a8w4");
+        tile(kA8W4, 128, 128, a8p, launch_tile<kFp8, kFp4, 128, 128, true, true, false>, "a8w4");
+        tile(kA8W4, 64, 128, a8p, launch_tile<kFp8, kFp4, 64, 128, true, true, false>, "a8w4");
+        skinny(kA8W4, 1, false, a8, launch_skinny<kFp8, 1, true, false, false>, "a8w4");
+        skinny(kA8W4, 2, false, a8, launch_skinny<kFp8, 2, true, false, false>, "a8w4");
+        skinny(kA8W4, 4, false, a8, launch_skinny<kFp8, 4, true, false, false>, "a8w4");
+        skinny(kA8W4, 1, true, a8, launch_skinny<kFp8, 1, true, true, false>, "a8w4");
+        skinny(kA8W4, 2, true, a8, launch_skinny<kFp8, 2, true, true, false>, "a8w4");
+        skinny(kA8W4, 4, true, a8, launch_skinny<kFp8, 4, true, true, false>, "a8w4");
+        // ---- a16w16 ----
+        for (int of = 0; of < 2; ++of) {
+            for (int bp = 0; bp < 2; ++bp) {
+                const Variant v{false, bp != 0, of != 0};
+#define AA_T16(BM, BN)                                                                     \
+    tile(kA16W16, BM, BN, v,                                                               \
+         of ? (bp ? launch_tile<kBf16, kBf16, BM, BN, false, true, true>                   \
+                  : launch_tile<kBf16, kBf16, BM, BN, false, false, true>)                 \
+            : (bp ? launch_tile<kBf16, kBf16, BM, BN, false, true, false>                  \
+                  : launch_tile<kBf16, kBf16, BM, BN, false, false, false>),               \
+         "a16w16");
+                AA_T16(256, 256) AA_T16(256, 128) AA_T16(128, 256) AA_T16(128, 128)
+                AA_T16(64, 128) AA_T16(64, 64)
+#undef AA_T16
+#define AA_S16(MF, SP)                                                                     \
+    skinny(kA16W16, MF, SP, v,                                                             \
+           of ? (bp ? launch_skinny<kBf16, MF, true, SP, true>                             \
+                    : launch_skinny<kBf16, MF, false, SP, true>)                           \
+              : (bp ? launch_skinny<kBf16, MF, true, SP, false>                            \
+                    : launch_skinny<kBf16, MF, false, SP, false>),                         \
+           "a16w16");
+                AA_S16(1, false) AA_S16(2, false) AA_S16(4, false)
+                AA_S16(1, true) AA_S16(2, true) AA_S16(4, true)
+#undef AA_S16
+            }
+        }
+    });
+    return reg;
+}
+
+const Instance* find_by_name(const std::string& nm) {
+    for (auto& in : registry())
+        if (in.name == nm) return &in;
+    return nullptr;
+}
+
+const Instance* find_by_id(int id) {
+    auto& r = registry();
+    return (id >= 0 && id < (int)r.size()) ? &r[id] : nullptr;
+}
+
+bool variant_ok(const Instance& in, Family f, const Variant& v) {
+    return in.fam == f && in.var.a_pre == v.a_pre && in.var.b_pre == v.b_pre && in.var.out_f32 == v.out_f32;
+}
+
+// Split-K factor for a skinny launch: split only when the 16-column blocks
+// cannot cover the CUs, keeping >= 32 k-steps (8 per wave) per split.
+int skinny_splits(int n_blocks, int k_steps, int cus) {
+    int s = 1;
+    while (n_blocks * s < cus && k_steps / (s * 2) >= 32) s *= 2;
+    return s;
+}
+
+// Heuristic choice among tile instances (reference heuristic idea:
+// csrc/py_itfs_cu/asm_gemm_a4w4.cu:81-152 — fewest rounds of tiles over the
+// CUs, then higher tile compute/memory ratio).
+const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int cus, int* splits) {
+    *splits = 1;
+    const int ksteps = K / (f == kA16W16 ? 32 : 128);
+    if (M <= 64) {
+        const int mf = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+        const int nblk = (N + 15) / 16;
+        const int s = skinny_splits(nblk, ksteps, cus);
+        for (auto& in : registry())
+            if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.split == (s > 1)) {
+                *splits = s;
+                return &in;
+            }
+    }
+    const Instance* best = nullptr;
+    long best_round = 1L << 40;
+    double best_eff = 0;
+    for (auto& in : registry()) {
+        if (in.skinny || !variant_ok(in, f, v)) continue;
+        const long tiles = (long)((M + in.bm - 1) / in.bm) * ((N + in.bn - 1) / in.bn);
+        const long rounds = (tiles + cus - 1) / cus;
+        const double eff = (double)in.bm * in.bn / (in.bm + in.bn);
+        if (rounds < best_round || (rounds == best_round && eff > best_eff)) {
+            best = &in;
+            best_round = rounds;
+            best_eff = eff;
+        }
+    }
+    return best;
+}
+
+// Reference kernel names (hsa/gfx950/f4gemm manifest, "..._<tM>x<tN>E") map to
+// the tile instance of the same shape when one exists.
+const Instance* map_reference_name(const std::string& nm, Family f, const Variant& v) {
+    const size_t e = nm.rfind('E');
+    const size_t u = nm.rfind('_');
+    if (u == std::string::npos || e == std::string::npos || e < u) return nullptr;
+    const std::string dims = nm.substr(u + 1, e - u - 1);
+    const size_t x = dims.find('x');
+    if (x == std::string::npos) return nullptr;
+    const int tm = atoi(dims.substr(0, x).c_str()), tn = atoi(dims.substr(x + 1).c_str());
+    for (auto& in : registry())
+        if (!in.skinny && variant_ok(in, f, v) && in.bm == tm && in.bn == tn) return &in;
+    return nullptr;
+}
+
+// ---- per-(device, stream) f32 workspace for split-K ----------------------
+struct WsKey {
+    int dev;
+    hipStream_t st;
+    bool operator<(const WsKey& o) const { return dev != o.dev ? dev < o.dev : st < o.st; }
+};
+struct WsVal {
+    float* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+float* workspace(int dev, hipStream_t st, size_t bytes) {
+    static std::mutex mu;
+    static std::map<WsKey, WsVal> ws;
+    std::lock_guard<std::mutex> lk(mu);
+    WsVal& w = ws[{dev, st}];
+    if (w.bytes < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        AA_HIP(hipStreamIsCapturing(st, &cs));
+        AA_CHECK(cs == hipStreamCaptureStatusNone,
+                 "split-K workspace must be sized before graph capture (call gemm_workspace_reserve)");
+        if (w.ptr) {
+            AA_HIP(hipStreamSynchronize(st));
+            AA_HIP(hipFree(w.ptr));
+        }
+        AA_HIP(hipMalloc(&w.ptr, bytes));
+        w.bytes = bytes;
+    }
+    return w.ptr;
+}
+
+struct GemmCall {
+    Family fam;
+    Variant var;
+    const aiter_tensor_t *A, *B, *As, *Bs, *out, *bias;
+    float alpha, beta;
+    const char* kernel_name;
+    int kernel_id;    // < 0: use name / heuristic
+    int log2_split;   // < 0: heuristic
+};
+
+void run_gemm(const GemmCall& c, hipStream_t stream) {
+    check_tensor(c.A, "A", 2);
+    check_tensor(c.B, "B", 2);
+    check_tensor(c.out, "out", 2);
+    const bool scaled = c.fam != kA16W16;
+    const int64_t M = rows_2d(c.A), N = rows_2d(c.B);
+    int64_t K;
+    if (c.fam == kA4W4) {
+        AA_CHECK(is_byte_type(c.A->dtype) && is_byte_type(c.B->dtype), "A and B must be fp4x2/u8");
+        K = cols_2d(c.A) * 2;
+        AA_CHECK(cols_2d(c.B) * 2 == K, "B K dim ", cols_2d(c.B) * 2, " != A K dim ", K);
+    } else if (c.fam == kA8W4) {
+        AA_CHECK(is_byte_type(c.A->dtype) && is_byte_type(c.B->dtype), "A must be fp8, B fp4x2");
+        K = cols_2d(c.A);
+        AA_CHECK(cols_2d(c.B) * 2 == K, "B K dim ", cols_2d(c.B) * 2, " != A K dim ", K);
+    } else {
+        AA_CHECK(c.A->dtype == AITER_DTYPE_bf16 && c.B->dtype == AITER_DTYPE_bf16,
+                 "A and B must be bf16 (got ", dtype_name(c.A->dtype), ", ", dtype_name(c.B->dtype), ")");
+        K = cols_2d(c.A);
+        AA_CHECK(cols_2d(c.B) == K, "B K dim ", cols_2d(c.B), " != A K dim ", K);
+    }
+    AA_CHECK(c.var.out_f32 ? c.out->dtype == AITER_DTYPE_fp32 : c.out->dtype == AITER_DTYPE_bf16,
+             "unsupported output dtype ", dtype_name(c.out->dtype));
+    AA_CHECK(cols_2d(c.out) == N, "out has ", cols_2d(c.out), " columns, expected N = ", N);
+    AA_CHECK(rows_2d(c.out) >= M, "out has ", rows_2d(c.out), " rows, expected >= M = ", M);
+    const int kgran = scaled ? 256 : 64;
+    AA_CHECK(K % kgran == 0, "K = ", K, " must be a multiple of ", kgran);
+    AA_CHECK(N % 16 == 0, "N = ", N, " must be a multiple of 16");
+    if (M == 0 || N == 0) return;
+    AA_CHECK(M < (1LL << 31) && N < (1LL << 31), "M/N too large");
+
+    const int64_t elem = (c.fam == kA16W16) ? 2 : 1;
+    GemmParams p{};
+    p.A = static_cast<const uint8_t*>(c.A->ptr);
+    p.B = static_cast<const uint8_t*>(c.B->ptr);
+    p.lda = row_stride_2d(c.A, "A") * elem;
+    p.ldb = row_stride_2d(c.B, "B") * elem;
+    if (c.var.a_pre) AA_CHECK(M % 16 == 0 && p.lda == cols_2d(c.A) * elem, "preshuffled A needs M%16==0 and contiguity");
+    if (c.var.b_pre) AA_CHECK(p.ldb == cols_2d(c.B) * elem, "preshuffled B must be contiguous");
+    AA_CHECK(p.lda % 16 == 0 && p.ldb % 16 == 0 && ((uintptr_t)p.A & 15) == 0 && ((uintptr_t)p.B & 15) == 0,
+             "A/B rows must be 16-byte aligned");
+    p.D = c.out->ptr;
+    p.ldd = row_stride_2d(c.out, "out");
+    AA_CHECK(p.ldd % 4 == 0 && ((uintptr_t)p.D & 15) == 0, "out rows must be 16-byte aligned");
+    p.M = (int)M;
+    p.N = (int)N;
+    p.K = (int)K;
+    p.alpha = c.alpha;
+    p.beta = c.beta;
+    if (c.bias) {
+        check_tensor(c.bias, "bias");
+        AA_CHECK(c.bias->dtype == AITER_DTYPE_fp32, "bias must be f32");
+        AA_CHECK(cols_2d(c.bias) == N, "bias last dim must be N");
+        const int64_t br = rows_2d(c.bias);
+        AA_CHECK(br == 1 || br >= M, "bias must be [N], [1,N] or [M,N]");
+        p.bias = static_cast<const float*>(c.bias->ptr);
+        p.ld_bias = br == 1 ? 0 : row_stride_2d(c.bias, "bias");
+    }
+    if (scaled) {
+        check_tensor(c.As, "A_scale", 1);
+        check_tensor(c.Bs, "B_scale", 1);
+        const int64_t kb = K / 32;  // multiple of 8 since K % 256 == 0
+        p.As = static_cast<const uint8_t*>(c.As->ptr);
+        p.Bs = static_cast<const uint8_t*>(c.Bs->ptr);
+        p.sa_stride = c.As->ndim >= 2 ? row_stride_2d(c.As, "A_scale") : kb;
+        p.sb_stride = c.Bs->ndim >= 2 ? row_stride_2d(c.Bs, "B_scale") : kb;
+        AA_CHECK(p.sa_stride == kb && p.sb_stride == kb,
+                 "shuffled scales must be contiguous with pad8(K/32) = ", kb, " bytes per row");
+        const int64_t arows = (int64_t)c.As->numel / kb, brows = (int64_t)c.Bs->numel / kb;
+        AA_CHECK(arows >= (M + 31) / 32 * 32, "A_scale has ", arows, " rows, need >= pad32(M) = ", (M + 31) / 32 * 32);
+        AA_CHECK(brows >= (N + 31) / 32 * 32, "B_scale has ", brows, " rows, need >= pad32(N) = ", (N + 31) / 32 * 32);
+        p.sa_groups = (int)(arows / 32);
+        p.sb_groups = (int)(brows / 32);
+    }
+
+    int dev = c.A->device_id;
+    if (dev < 0) AA_HIP(hipGetDevice(&dev));
+    const int cus = device_cu_count(dev);
+
+    const Instance* inst = nullptr;
+    int splits = 1;
+    if (c.kernel_id >= 0) {
+        inst = find_by_id(c.kernel_id);
+        AA_CHECK(inst && variant_ok(*inst, c.fam, c.var), "kernel id ", c.kernel_id, " does not fit this GEMM");
+    } else if (c.kernel_name && c.kernel_name[0]) {
+        inst = find_by_name(c.kernel_name);
+        if (!inst) inst = map_reference_name(c.kernel_name, c.fam, c.var);
+        AA_CHECK(inst && variant_ok(*inst, c.fam, c.var), "unknown kernel name '", c.kernel_name, "'");
+    }
+    const int ksteps = (int)(K / (scaled ? 128 : 32));
+    if (!inst) {
+        inst = heuristic(c.fam, c.var, (int)M, (int)N, (int)K, cus, &splits);
+        AA_CHECK(inst, "no kernel instance for this GEMM");
+    } else if (inst->skinny && inst->split) {
+        splits = skinny_splits((int)((N + 15) / 16), ksteps, cus);
+    }
+    if (inst->skinny && inst->split && c.log2_split >= 0) splits = 1 << c.log2_split;
+    if (inst->skinny) AA_CHECK(M <= inst->bm, "skinny kernel ", inst->name, " covers M <= ", inst->bm);
+
+    if (!inst->skinny) {
+        p.tiles_m = (int)((M + inst->bm - 1) / inst->bm);
+        p.tiles_n = (int)((N + inst->bn - 1) / inst->bn);
+        AA_CHECK(M >= 16 || !c.var.a_pre, "preshuffled A needs M >= 16");
+        inst->fn(p, dim3(p.tiles_m * p.tiles_n), stream);
+    } else {
+        // the skinny kernels split K in k-pairs (one scale dword each)
+        const int kpairs = ksteps / 2;
+        splits = std::max(1, std::min(splits, kpairs));
+        p.k_steps_per_split = (kpairs + splits - 1) / splits;
+        splits = (kpairs + p.k_steps_per_split - 1) / p.k_steps_per_split;
+        const dim3 grid((unsigned)((N + 15) / 16), (unsigned)splits);
+        if (inst->split && splits > 1) {
+            const size_t need = (size_t)M * N * sizeof(float);
+            p.ws = workspace(dev, stream, need);
+            const int64_t n4 = (int64_t)M * N;
+            fill_zero_kernel<<<dim3((unsigned)((n4 / 4 + 255) / 256 + 1)), 256, 0, stream>>>(p.ws, n4);
+            inst->fn(p, grid, stream);
+            if (c.var.out_f32)
+                splitk_finish_kernel<true><<<dim3((unsigned)((n4 / 4 + 255) / 256)), 256, 0, stream>>>(p);
+            else
+                splitk_finish_kernel<false><<<dim3((unsigned)((n4 / 4 + 255) / 256)), 256, 0, stream>>>(p);
+        } else if (inst->split) {
+            // a split instance asked for one split runs its non-split twin
+            const Instance* twin = nullptr;
+            for (auto& in : registry())
+                if (in.skinny && !in.split && variant_ok(in, c.fam, c.var) && in.bm == inst->bm) twin = &in;
+            AA_CHECK(twin, "no non-split twin for ", inst->name);
+            p.k_steps_per_split = kpairs;
+            twin->fn(p, dim3(grid.x, 1), stream);
+        } else {
+            p.k_steps_per_split = kpairs;
+            inst->fn(p, dim3(grid.x, 1), stream);
+        }
+    }
+    AA_HIP(hipGetLastError());
+}
+
+}  // namespace
+}  // namespace aiter_amd
+
+using namespace aiter_amd;
+
+extern "C" {
+
+int aiter_ctypes_abi_version(void) { return 2; }
+
+const char* aiter_get_last_error(void) {
+    return last_error().empty() ? nullptr : last_error().c_str();
+}
+
+void aiter_clear_last_error(void) { last_error().clear(); }
+
+int getPaddedM(int M, int N, int K, int gl) {
+    (void)K;
+    int padded = M;
+    if (gl == 0) {
+        if (M <= 256) padded = (M + 15) / 16 * 16;
+        else if (M <= 1024) padded = (M + 31) / 32 * 32;
+        else if (M <= 4096) padded = (M + 63) / 64 * 64;
+        else padded = (M + 127) / 128 * 128;
+    } else if (gl == 1) {
+        if (M > 8192 && N > 4096) {
+            padded = 8192;
+        } else {
+            unsigned v = M <= 1 ? 1u : (unsigned)M;
+            unsigned p2 = 1;
+            while (p2 < v) p2 <<= 1;
+            padded = (int)p2;
+        }
+    }
+    return padded;
+}
+
+int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
+                  aiter_tensor_t* B_scale, aiter_tensor_t* out, const char* kernelName,
+                  aiter_tensor_t* bias, float alpha, float beta, int bpreshuffle, int log2_k_split,
+                  aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(A ? A->device_id : -1);
+        GemmCall c{kA4W4, {false, bpreshuffle != 0, false}, A, B, A_scale, B_scale, out, bias,
+                   alpha, beta, kernelName, -1, log2_k_split > 0 ? log2_k_split : -1};
+        run_gemm(c, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int gemm_a4w4_blockscale(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* x_scale,
+                         aiter_tensor_t* w_scale, aiter_tensor_t* Y, int splitK, int kernelId,
+                         aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(XQ ? XQ->device_id : -1);
+        GemmCall c{kA4W4, {false, true, false}, XQ, WQ, x_scale, w_scale, Y, nullptr,
+                   1.0f, 0.0f, nullptr, kernelId, splitK > 0 ? splitK : -1};
+        run_gemm(c, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int mxfp8_mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
+                         aiter_tensor_t* ScaleB, aiter_tensor_t* out, const char* kernelName,
+                         int a_preshuffle, aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(A ? A->device_id : -1);
+        // the skinny path reads A row-major only
+        GemmCall c{kA8W4, {a_preshuffle != 0, true, false}, A, B, ScaleA, ScaleB, out, nullptr,
+                   1.0f, 0.0f, kernelName, -1, -1};
+        if (a_preshuffle && rows_2d(A) <= 64) {
+            // small-M heuristic is the skinny kernel, which needs row-major A
+            AA_CHECK(!kernelName || !kernelName[0] || std::string(kernelName).find("tile") != std::string::npos,
+                     "preshuffled A with M <= 64 supports tile kernels only");
+            if (!kernelName || !kernelName[0]) c.kernel_name = "a8w4_tile_64x128_apre";
+        }
+        run_gemm(c, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
+                    aiter_tensor_t* semaphore, aiter_tensor_t* bias, int splitK,
+                    const char* kernelName, int bpreshuffle, aiter_stream_t stream) {
+    (void)semaphore;
+    return safe_call([&] {
+        DeviceGuard g(A ? A->device_id : -1);
+        int l2 = -1;
+        if (splitK > 1) {
+            l2 = 0;
+            while ((1 << (l2 + 1)) <= splitK) ++l2;
+        }
+        GemmCall c{kA16W16, {false, bpreshuffle != 0, out && out->dtype == AITER_DTYPE_fp32}, A, B,
+                   nullptr, nullptr, out, bias, 1.0f, 1.0f, kernelName, -1, l2};
+        run_gemm(c, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+static void opus_batched(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias,
+                         int kernelId, int splitK, hipStream_t st) {
+    check_tensor(XQ, "XQ", 2);
+    check_tensor(WQ, "WQ", 2);
+    check_tensor(Y, "Y", 2);
+    // [b, M, K] / [b, N, K] / [b, M, N]; a 2-D call is batch 1
+    const int nd = XQ->ndim;
+    const int64_t batch = nd == 3 ? XQ->shape[0] : 1;
+    AA_CHECK(WQ->ndim == nd && Y->ndim == nd, "XQ, WQ, Y must have the same rank");
+    AA_CHECK(nd == 2 || nd == 3, "opus a16w16 expects 2-D or 3-D tensors");
+    if (nd == 3) AA_CHECK(WQ->shape[0] == batch && Y->shape[0] == batch, "batch mismatch");
+    for (int64_t b = 0; b < batch; ++b) {
+        aiter_tensor_t a = *XQ, w = *WQ, y = *Y, bb{};
+        auto slice = [&](aiter_tensor_t& t, const aiter_tensor_t* src, size_t esz) {
+            if (nd == 3) {
+                t.ptr = static_cast<uint8_t*>(src->ptr) + b * src->strides[0] * esz;
+                t.ndim = 2;
+                t.shape[0] = src->shape[1];
+                t.shape[1] = src->shape[2];
+                t.strides[0] = src->strides[1];
+                t.strides[1] = src->strides[2];
+                t.numel = src->shape[1] * src->shape[2];
+            }
+        };
+        slice(a, XQ, 2);
+        slice(w, WQ, 2);
+        slice(y, Y, dtype_size(Y->dtype));
+        aiter_tensor_t* bptr = nullptr;
+        if (bias) {
+            bb = *bias;
+            if (bias->ndim == 2 && bias->shape[0] == batch && batch > 1) {
+                bb.ptr = static_cast<uint8_t*>(bias->ptr) + b * bias->strides[0] * 4;
+                bb.ndim = 1;
+                bb.shape[0] = bias->shape[1];
+                bb.strides[0] = bias->strides[1];
+                bb.numel = bias->shape[1];
+            }
+            bptr = &bb;
+        }
+        GemmCall c{kA16W16, {false, false, Y->dtype == AITER_DTYPE_fp32}, &a, &w, nullptr, nullptr, &y, bptr,
+                   1.0f, 1.0f, nullptr, kernelId, splitK > 0 ? splitK : -1};
+        run_gemm(c, st);
+    }
+}
+
+int opus_gemm(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias,
+              aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(XQ ? XQ->device_id : -1);
+        opus_batched(XQ, WQ, Y, bias, -1, -1, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int opus_gemm_a16w16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
+                          aiter_tensor_t* bias, int kernelId, int splitK, aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(XQ ? XQ->device_id : -1);
+        opus_batched(XQ, WQ, Y, bias, kernelId, splitK, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+// ---- library-specific introspection (used by the Python tuner) ----------
+int aiter_amd_num_kernels(void) { return (int)registry().size(); }
+
+// Writes "id,name,family,skinny,bm,bn,split,a_pre,b_pre,out_f32" for kernel
+// `id` into buf; returns -1 if id is out of range.
+int aiter_amd_kernel_info(int id, char* buf, int buflen) {
+    const Instance* in = find_by_id(id);
+    if (!in || !buf || buflen <= 0) return -1;
+    static const char* fam[] = {"a4w4", "a8w4", "a16w16"};
+    snprintf(buf, buflen, "%d,%s,%s,%d,%d,%d,%d,%d,%d,%d", in->id, in->name.c_str(), fam[in->fam],
+             (int)in->skinny, in->bm, in->bn, (int)in->split, (int)in->var.a_pre, (int)in->var.b_pre,
+             (int)in->var.out_f32);
+    return 0;
+}
+
+// Pre-size the split-K workspace of (device, stream) before graph capture.
+int gemm_workspace_reserve(int device, aiter_stream_t stream, size_t bytes) {
+    return safe_call([&] {
+        DeviceGuard g(device);
+        (void)workspace(device, reinterpret_cast<hipStream_t>(stream), bytes);
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,503 @@
+// Device code of the scaled-GEMM family (gfx950, wave64).
+//
+// Operand staging unit: the "byte-fragment" — 16 rows x 64 bytes = 1 KiB,
+// stored so that lane l holds row (l % 16), bytes [16*(l/16), 16*(l/16)+16).
+// That is exactly:
+//   * the A/B operand of v_mfma_scale_f32_16x16x128_f8f6f4 for e2m1
+//     (32 contiguous fp4 = one MX block per lane, one e8m0 scale per lane),
+//   * the A/B operand of v_mfma_f32_16x16x32_bf16 (8 contiguous bf16),
+//   * one 64-byte K window of aiter's preshuffled weight layout
+//     (shuffle_weight((16,16)): per 16-row block, 32-byte K chunks of
+//     [2 halves][16 rows][16 B]; aiter/ops/shuffle.py:192-204), which is
+//     therefore a contiguous 1 KiB read.
+// e4m3 operands use two consecutive byte-fragments per MFMA: lane l holds
+// bytes [16g, 16g+16) and [64+16g, 64+16g+16) of the 128-byte k-step
+// window (g = l/16) -- the K pairing the scaled MFMA applies between an e4m3
+// operand and an e2m1 operand laid out as above (measured on gfx950 with
+// one-hot operands).
+//
+// Scales use aiter's shuffled e8m0 layout (aiter/ops/shuffle.py:339-365):
+// one dword per lane covers rows (l%16, l%16+16) of a 32-row group and MX
+// blocks (l/16, l/16+4) of a 256-element K window; byte 2*k2+r2 is the scale
+// for K half k2 and row half r2, which is the op_sel byte of the scaled MFMA.
+#pragma once
+#include "common.h"
+
+namespace aiter_amd {
+
+enum OpKind : int { kFp4 = 4, kFp8 = 0, kBf16 = 16 };
+
+template <int KIND> struct OpTraits;
+template <> struct OpTraits<kFp4> {
+    static constexpr int frags_per_step = 1;   // byte-fragments per MFMA k-step
+    static constexpr int fmt = 4;
+    static constexpr bool scaled = true;
+};
+template <> struct OpTraits<kFp8> {
+    static constexpr int frags_per_step = 2;
+    static constexpr int fmt = 0;
+    static constexpr bool scaled = true;
+};
+template <> struct OpTraits<kBf16> {
+    static constexpr int frags_per_step = 1;
+    static constexpr int fmt = -1;
+    static constexpr bool scaled = false;
+};
+
+struct GemmParams {
+    const uint8_t* A;
+    const uint8_t* B;
+    const uint8_t* As;  // shuffled e8m0 (scaled kinds)
+    const uint8_t* Bs;
+    void* D;
+    const float* bias;
+    float* ws;           // split-K f32 partial sums [M_pad, N] (skinny split path)
+    int64_t lda, ldb;    // bytes per row (row-major) / per row of the preshuffled matrix
+    int64_t ldd;         // elements per output row
+    int64_t ld_bias;     // elements per bias row (0 = broadcast one row)
+    int64_t sa_stride, sb_stride;  // bytes per row of the scale buffers (pad8(K/32))
+    int M, N, K;
+    int sa_groups, sb_groups;      // 32-row groups present in the scale buffers
+    int tiles_m, tiles_n;
+    int k_steps_per_split;         // skinny split-K: MFMA k-steps per split
+    float alpha, beta;
+};
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers.  op_sel bytes must be immediates: the switch folds away once
+// the caller's loops are unrolled.
+// ---------------------------------------------------------------------------
+#define AA_MFMA_SC(OA, OB)                                                                 \
+    case (OA) * 4 + (OB):                                                                  \
+        return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, FA, FB, OA, sa, OB, sb);
+
+template <int FA, int FB>
+AA_DEV f32x4_t mfma_scaled(i32x8_t a, i32x8_t b, f32x4_t c, int sa, int oa, int sb, int ob) {
+    switch (oa * 4 + ob) {
+        AA_MFMA_SC(0, 0) AA_MFMA_SC(0, 1) AA_MFMA_SC(0, 2) AA_MFMA_SC(0, 3)
+        AA_MFMA_SC(1, 0) AA_MFMA_SC(1, 1) AA_MFMA_SC(1, 2) AA_MFMA_SC(1, 3)
+        AA_MFMA_SC(2, 0) AA_MFMA_SC(2, 1) AA_MFMA_SC(2, 2) AA_MFMA_SC(2, 3)
+        AA_MFMA_SC(3, 0) AA_MFMA_SC(3, 1) AA_MFMA_SC(3, 2) AA_MFMA_SC(3, 3)
+        default: __builtin_unreachable();
+    }
+}
+#undef AA_MFMA_SC
+
+AA_DEV f32x4_t mfma_bf16(i32x4_t a, i32x4_t b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// One MFMA k-step for a (B-fragment, A-fragment) pair.  src0 = B so that the
+// 16x16 result lands transposed: lane l holds C[m = l%16][n = 4*(l/16)+r],
+// i.e. four consecutive output columns of one row (an 8-byte bf16 store).
+template <int KA, int KB>
+AA_DEV f32x4_t mma_step(const i32x4_t* b, const i32x4_t* a, f32x4_t c, int sb, int ob, int sa,
+                        int oa) {
+    if constexpr (KA == kBf16) {
+        return mfma_bf16(b[0], a[0], c);
+    } else {
+        i32x8_t bv, av;
+        bv[0] = b[0][0]; bv[1] = b[0][1]; bv[2] = b[0][2]; bv[3] = b[0][3];
+        if constexpr (KB == kFp8) {
+            bv[4] = b[1][0]; bv[5] = b[1][1]; bv[6] = b[1][2]; bv[7] = b[1][3];
+        } else {
+            bv[4] = 0; bv[5] = 0; bv[6] = 0; bv[7] = 0;
+        }
+        av[0] = a[0][0]; av[1] = a[0][1]; av[2] = a[0][2]; av[3] = a[0][3];
+        if constexpr (KA == kFp8) {
+            av[4] = a[1][0]; av[5] = a[1][1]; av[6] = a[1][2]; av[7] = a[1][3];
+        } else {
+            av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
+        }
+        return mfma_scaled<OpTraits<KB>::fmt, OpTraits<KA>::fmt>(bv, av, c, sb, ob, sa, oa);
+    }
+}
+
+// XCD-aware tile order: hardware dispatches workgroup i to XCD (i % 8); the
+// remap gives each XCD a contiguous range of the grouped (GROUP_M rows)
+// raster so tiles sharing A rows / B columns share one L2.
+AA_DEV void tile_coords(int bid, int nblocks, int tiles_m, int tiles_n, int& tm, int& tn) {
+    constexpr int kXcd = 8;
+    constexpr int kGroupM = 8;
+    int pid = bid;
+    if (nblocks % kXcd == 0) pid = (bid % kXcd) * (nblocks / kXcd) + bid / kXcd;
+    const int in_group = kGroupM * tiles_n;
+    const int group = pid / in_group;
+    const int first_m = group * kGroupM;
+    const int gsize = min(tiles_m - first_m, kGroupM);
+    const int r = pid % in_group;
+    tm = first_m + r % gsize;
+    tn = r / gsize;
+}
+
+// ---------------------------------------------------------------------------
+// Epilogue store of one 16x16 fragment (transposed accumulator layout).
+// ---------------------------------------------------------------------------
+template <bool OUT_F32>
+AA_DEV void store_frag(const GemmParams& p, f32x4_t acc, int m, int n) {
+    if (m >= p.M || n >= p.N) return;
+    float v[4] = {acc[0] * p.alpha, acc[1] * p.alpha, acc[2] * p.alpha, acc[3] * p.alpha};
+    if (p.bias) {
+        const float* bp = p.bias + (int64_t)m * p.ld_bias + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] += p.beta * bp[r];
+    }
+    if constexpr (OUT_F32) {
+        float* d = static_cast<float*>(p.D) + (int64_t)m * p.ldd + n;
+        *reinterpret_cast<f32x4_t*>(d) = f32x4_t{v[0], v[1], v[2], v[3]};
+    } else {
+        uint16_t* d = static_cast<uint16_t*>(p.D) + (int64_t)m * p.ldd + n;
+        typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2_t*>(d) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Tile kernel: BM x BN block tile, 4 waves in 2x2, each (BM/2) x (BN/2).
+// One stage = 2 MFMA k-steps (256 MX elements / 64 bf16 elements), double
+// buffered in LDS through registers: global loads for stage t+1 are in
+// flight while stage t is multiplied, then written to the other LDS buffer.
+// ---------------------------------------------------------------------------
+template <int KA, int KB, int BM, int BN, bool A_PRE, bool B_PRE, bool OUT_F32>
+__global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemmParams p) {
+    constexpr int FA = OpTraits<KA>::frags_per_step;
+    constexpr int FB = OpTraits<KB>::frags_per_step;
+    constexpr bool SCALED = OpTraits<KA>::scaled;
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int MI = WM / 16, NJ = WN / 16;
+    constexpr int A_FRAGS = (BM / 16) * 2 * FA;  // byte-fragments of A per stage
+    constexpr int B_FRAGS = (BN / 16) * 2 * FB;
+    constexpr int TOT = A_FRAGS + B_FRAGS;
+    static_assert(TOT % 4 == 0, "fragments must split evenly over 4 waves");
+    constexpr int PER_WAVE = TOT / 4;
+    constexpr int STAGE_BYTES = TOT * 1024;
+    constexpr int A_KBYTES = 128 * FA;  // A bytes per row per stage
+    constexpr int B_KBYTES = 128 * FB;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * STAGE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    // ---- per-thread global source pointers of its PER_WAVE fragments
+    const uint8_t* src[PER_WAVE];
+    int64_t kstride[PER_WAVE];  // bytes to advance per stage
+#pragma unroll
+    for (int q = 0; q < PER_WAVE; ++q) {
+        const int f = wave + 4 * q;
+        if (f < A_FRAGS) {
+            const int rf = f / (2 * FA), kf = f % (2 * FA);
+            int row = m0 + rf * 16;
+            if constexpr (A_PRE) {
+                row = min(row, p.M - 16);
+                src[q] = p.A + (int64_t)row * p.lda + kf * 1024 + lane * 16;
+                kstride[q] = A_KBYTES * 16;
+            } else {
+                row = min(row + (lane & 15), p.M - 1);
+                src[q] = p.A + (int64_t)row * p.lda + kf * 64 + (lane >> 4) * 16;
+                kstride[q] = A_KBYTES;
+            }
+        } else {
+            const int g = f - A_FRAGS;
+            const int rf = g / (2 * FB), kf = g % (2 * FB);
+            int row = n0 + rf * 16;
+            if constexpr (B_PRE) {
+                row = min(row, p.N - 16);
+                src[q] = p.B + (int64_t)row * p.ldb + kf * 1024 + lane * 16;
+                kstride[q] = B_KBYTES * 16;
+            } else {
+                row = min(row + (lane & 15), p.N - 1);
+                src[q] = p.B + (int64_t)row * p.ldb + kf * 64 + (lane >> 4) * 16;
+                kstride[q] = B_KBYTES;
+            }
+        }
+    }
+
+    // ---- scale pointers: one dword per lane per 32-row group per stage
+    constexpr int SA = SCALED ? (WM / 32) : 1;
+    constexpr int SB = SCALED ? (WN / 32) : 1;
+    const uint8_t* sa_ptr[SA];
+    const uint8_t* sb_ptr[SB];
+    if constexpr (SCALED) {
+#pragma unroll
+        for (int i = 0; i < SA; ++i) {
+            const int grp = min((m0 + wm * WM) / 32 + i, p.sa_groups - 1);
+            sa_ptr[i] = p.As + (int64_t)grp * 32 * p.sa_stride + lane * 4;
+        }
+#pragma unroll
+        for (int j = 0; j < SB; ++j) {
+            const int grp = min((n0 + wn * WN) / 32 + j, p.sb_groups - 1);
+            sb_ptr[j] = p.Bs + (int64_t)grp * 32 * p.sb_stride + lane * 4;
+        }
+    }
+
+    const int stage_k = SCALED ? 256 : 64;
+    const int nstages = p.K / stage_k;
+
+    f32x4_t acc[MI][NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    i32x4_t stg[PER_WAVE];
+    int sa_cur[SA], sb_cur[SB], sa_nxt[SA], sb_nxt[SB];
+
+    auto load_stage = [&](int t) {
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q)
+            stg[q] = *reinterpret_cast<const i32x4_t*>(src[q] + (int64_t)t * kstride[q]);
+        if constexpr (SCALED) {
+#pragma unroll
+            for (int i = 0; i < SA; ++i) sa_nxt[i] = *reinterpret_cast<const int*>(sa_ptr[i] + t * 256);
+#pragma unroll
+            for (int j = 0; j < SB; ++j) sb_nxt[j] = *reinterpret_cast<const int*>(sb_ptr[j] + t * 256);
+        }
+    };
+    auto store_stage = [&](int buf) {
+        uint8_t* base = smem + buf * STAGE_BYTES;
+#pragma unroll
+        for (int q = 0; q < PER_WAVE; ++q) {
+            const int f = wave + 4 * q;
+            *reinterpret_cast<i32x4_t*>(base + f * 1024 + lane * 16) = stg[q];
+        }
+    };
+
+    load_stage(0);
+    store_stage(0);
+    if constexpr (SCALED) {
+#pragma unroll
+        for (int i = 0; i < SA; ++i) sa_cur[i] = sa_nxt[i];
+#pragma unroll
+        for (int j = 0; j < SB; ++j) sb_cur[j] = sb_nxt[j];
+    }
+    __syncthreads();
+
+    for (int t = 0; t < nstages; ++t) {
+        const int buf = t & 1;
+        if (t + 1 < nstages) load_stage(t + 1);
+        const uint8_t* abase = smem + buf * STAGE_BYTES;
+        const uint8_t* bbase = abase + A_FRAGS * 1024;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            i32x4_t af[MI][FA], bf[NJ][FB];
+#pragma unroll
+            for (int i = 0; i < MI; ++i) {
+                const int rf = wm * MI + i;
+#pragma unroll
+                for (int h = 0; h < FA; ++h)
+                    af[i][h] = *reinterpret_cast<const i32x4_t*>(abase + ((rf * 2 + ks) * FA + h) * 1024 + lane * 16);
+            }
+#pragma unroll
+            for (int j = 0; j < NJ; ++j) {
+                const int cf = wn * NJ + j;
+#pragma unroll
+                for (int h = 0; h < FB; ++h)
+                    bf[j][h] = *reinterpret_cast<const i32x4_t*>(bbase + ((cf * 2 + ks) * FB + h) * 1024 + lane * 16);
+            }
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j) {
+                    if constexpr (SCALED)
+                        acc[i][j] = mma_step<KA, KB>(bf[j], af[i], acc[i][j], sb_cur[j >> 1],
+                                                     ks * 2 + (j & 1), sa_cur[i >> 1], ks * 2 + (i & 1));
+                    else
+                        acc[i][j] = mma_step<KA, KB>(bf[j], af[i], acc[i][j], 0, 0, 0, 0);
+                }
+        }
+        if (t + 1 < nstages) {
+            // buf^1 was last read in stage t-1; every wave has passed the
+            // barrier that ended stage t-1, so it is free to overwrite.
+            store_stage(buf ^ 1);
+            if constexpr (SCALED) {
+#pragma unroll
+                for (int i = 0; i < SA; ++i) sa_cur[i] = sa_nxt[i];
+#pragma unroll
+                for (int j = 0; j < SB; ++j) sb_cur[j] = sb_nxt[j];
+            }
+            __syncthreads();
+        }
+    }
+
+    // ---- epilogue
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) {
+            const int m = m0 + wm * WM + i * 16 + (lane & 15);
+            const int n = n0 + wn * WN + j * 16 + 4 * (lane >> 4);
+            store_frag<OUT_F32>(p, acc[i][j], m, n);
+        }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny (decode) kernel: HBM-bound streaming of B for small M.
+// Block = NW waves on one 16-column B fragment.  Work unit = a k-pair (two
+// MFMA k-steps = 256 MX / 64 bf16 elements), which is exactly what one scale
+// dword covers, so every op_sel is an immediate.  Wave w takes pairs
+// w, w+NW, ... of its K split with the next pair's loads in flight while the
+// current one is multiplied; at the decode shapes every wave owns one or two
+// pairs, so all of B is requested in the first few hundred cycles.
+// Partial sums are reduced across waves through LDS; with a K split over
+// blocks (gridDim.y > 1) the block result is atomically added to an f32
+// workspace that a second kernel converts.
+// ---------------------------------------------------------------------------
+template <int KA, int MF>
+struct SkinnyPair {
+    static constexpr int FA = OpTraits<KA>::frags_per_step;
+    static constexpr bool SCALED = OpTraits<KA>::scaled;
+    static constexpr int SGRP = (MF + 1) / 2;
+    i32x4_t b[2];
+    i32x4_t a[2][MF][FA];
+    int sb;
+    int sa[SGRP];
+};
+
+template <int KA, int MF, bool B_PRE>
+AA_DEV void skinny_load(SkinnyPair<KA, MF>& d, int pr, const uint8_t* bsrc, const uint8_t* const* asrc,
+                        const bool* arow_ok, const uint8_t* sbp, const uint8_t* const* sap) {
+    using P = SkinnyPair<KA, MF>;
+    constexpr int A_STEP_BYTES = KA == kFp8 ? 128 : 64;
+    constexpr int BSTEP = B_PRE ? 1024 : 64;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int s = 2 * pr + h;
+        d.b[h] = *reinterpret_cast<const i32x4_t*>(bsrc + (int64_t)s * BSTEP);
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int f = 0; f < P::FA; ++f) {
+                const i32x4_t v = *reinterpret_cast<const i32x4_t*>(asrc[i] + (int64_t)s * A_STEP_BYTES + f * 64);
+                d.a[h][i][f] = arow_ok[i] ? v : i32x4_t{0, 0, 0, 0};
+            }
+    }
+    if constexpr (P::SCALED) {
+        d.sb = *reinterpret_cast<const int*>(sbp + (int64_t)pr * 256);
+#pragma unroll
+        for (int g = 0; g < P::SGRP; ++g) d.sa[g] = *reinterpret_cast<const int*>(sap[g] + (int64_t)pr * 256);
+    }
+}
+
+template <int KA, int MF>
+AA_DEV void skinny_mma(const SkinnyPair<KA, MF>& d, f32x4_t* acc, int bhalf) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int i = 0; i < MF; ++i) {
+            if constexpr (OpTraits<KA>::scaled) {
+                if (bhalf)
+                    acc[i] = mma_step<KA, kFp4>(&d.b[h], d.a[h][i], acc[i], d.sb, h * 2 + 1, d.sa[i >> 1],
+                                                h * 2 + (i & 1));
+                else
+                    acc[i] = mma_step<KA, kFp4>(&d.b[h], d.a[h][i], acc[i], d.sb, h * 2, d.sa[i >> 1],
+                                                h * 2 + (i & 1));
+            } else {
+                acc[i] = mma_step<KA, KA>(&d.b[h], d.a[h][i], acc[i], 0, 0, 0, 0);
+            }
+        }
+}
+
+template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
+    constexpr bool SCALED = OpTraits<KA>::scaled;
+    constexpr int KPAIR = SCALED ? 256 : 64;               // elements per k-pair
+    constexpr int SGRP = (MF + 1) / 2;                     // 32-row A scale groups
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int total_pairs = p.K / KPAIR;
+    const int p_begin = blockIdx.y * p.k_steps_per_split;   // k_steps_per_split counts pairs here
+    const int p_end = min(total_pairs, p_begin + p.k_steps_per_split);
+
+    const uint8_t* bsrc;
+    if constexpr (B_PRE)
+        bsrc = p.B + (int64_t)n0 * p.ldb + lane * 16;
+    else
+        bsrc = p.B + (int64_t)min(n0 + (lane & 15), p.N - 1) * p.ldb + (lane >> 4) * 16;
+    const uint8_t* asrc[MF];
+    bool arow_ok[MF];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+        const int row = i * 16 + (lane & 15);
+        arow_ok[i] = row < p.M;
+        asrc[i] = p.A + (int64_t)min(row, p.M - 1) * p.lda + (lane >> 4) * 16;
+    }
+    const uint8_t* sbp = nullptr;
+    const uint8_t* sap[SGRP];
+    if constexpr (SCALED) {
+        sbp = p.Bs + (int64_t)(n0 / 32) * 32 * p.sb_stride + lane * 4;
+#pragma unroll
+        for (int g = 0; g < SGRP; ++g)
+            sap[g] = p.As + (int64_t)min(g, p.sa_groups - 1) * 32 * p.sa_stride + lane * 4;
+    }
+    const int bhalf = (n0 / 16) & 1;
+
+    f32x4_t acc[MF];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+    // software pipeline: the next pair's loads are in flight while the
+    // current pair is multiplied
+    int pr = p_begin + wave;
+    if (pr < p_end) {
+        SkinnyPair<KA, MF> cur;
+        skinny_load<KA, MF, B_PRE>(cur, pr, bsrc, asrc, arow_ok, sbp, sap);
+        for (pr += NW; pr < p_end; pr += NW) {
+            SkinnyPair<KA, MF> nxt;
+            skinny_load<KA, MF, B_PRE>(nxt, pr, bsrc, asrc, arow_ok, sbp, sap);
+            skinny_mma<KA, MF>(cur, acc, bhalf);
+            cur = nxt;
+        }
+        skinny_mma<KA, MF>(cur, acc, bhalf);
+    }
+
+    __shared__ f32x4_t red[NW][MF][64];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) red[wave][i][lane] = acc[i];
+    __syncthreads();
+    for (int t = threadIdx.x; t < MF * 64; t += 64 * NW) {
+        const int i = t / 64, l = t % 64;
+        f32x4_t s = red[0][i][l];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) s += red[w][i][l];
+        const int m = i * 16 + (l & 15);
+        const int n = n0 + 4 * (l >> 4);
+        if constexpr (SPLIT) {
+            if (m < p.M && n < p.N) {
+                float* w = p.ws + (int64_t)m * p.N + n;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) atomicAdd(w + r, s[r]);
+            }
+        } else {
+            store_frag<OUT_F32>(p, s, m, n);
+        }
+    }
+}
+
+// f32 workspace -> output (+alpha, +bias) for the split-K skinny path.
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void splitk_finish_kernel(GemmParams p) {
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int64_t total = (int64_t)p.M * p.N;
+    if (idx >= total) return;
+    const int m = (int)(idx / p.N), n = (int)(idx % p.N);
+    const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.ws + idx);
+    store_frag<OUT_F32>(p, v, m, n);
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int64_t n) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i + 4 <= n) *reinterpret_cast<f32x4_t*>(p + i) = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    else
+        for (int64_t j = i; j < n; ++j) p[j] = 0.f;
+}
+
+}  // namespace aiter_amd

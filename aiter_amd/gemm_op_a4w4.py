@@ -1,0 +1,128 @@
+"""MXFP4 x MXFP4 (A4W4) GEMM with aiter's Python API
+(aiter/ops/gemm_op_a4w4.py:20-287, 581-608).
+
+D[M, N] = (A (x) A_scale) @ (B (x) B_scale)^T, A [M, K/2] fp4x2 row-major,
+B [N, K/2] fp4x2 preshuffled (``shuffle_weight``), both scales e8m0 in the
+shuffled layout (``shuffle_scale``), output bf16 allocated as [pad32(M), N]
+and returned as ``out[:M]`` like the reference.
+"""
+from __future__ import annotations
+
+import functools
+import logging
+import os
+
+import torch
+from torch import Tensor
+
+from . import dtypes
+from ._lib import call
+from .config import A4W4_KEYS, DEFAULT_A4W4_CSV, get_cu_num, get_gfx, load_tuned
+from .gemm_common import get_padded_m
+
+logger = logging.getLogger("aiter_amd")
+AITER_LOG_TUNED_CONFIG = int(os.environ.get("AITER_LOG_TUNED_CONFIG", "0"))
+
+
+@functools.lru_cache(maxsize=1024)
+def compute_gemm_SplitK(M: int, N: int, K: int, tile_m: int, tile_n: int, tile_k: int):
+    """Tuner's split-K upper bound; the reference returns 3 unconditionally
+    (aiter/ops/gemm_op_a4w4.py:20-30)."""
+    return 3
+
+
+@functools.lru_cache(maxsize=1)
+def _a4w4_table():
+    return load_tuned("AITER_CONFIG_GEMM_A4W4", DEFAULT_A4W4_CSV, A4W4_KEYS)
+
+
+@functools.lru_cache(maxsize=1024)
+def get_GEMM_config(M: int, N: int, K: int):
+    """CSV row for (gfx, cu_num, M | padded(M, gl=0) | padded(M, gl=1), N, K)
+    (aiter/ops/gemm_op_a4w4.py:33-78)."""
+    table = _a4w4_table()
+    gfx, cu_num = get_gfx(), get_cu_num()
+    for gl in (None, 0, 1):
+        pm = M if gl is None else get_padded_m(M, N, K, gl)
+        cfg = table.get((gfx, cu_num, pm, N, K))
+        if cfg is not None:
+            if AITER_LOG_TUNED_CONFIG:
+                logger.info(f"shape M:{M} N:{N} K:{K} tuned as padded_M {pm}: {cfg['kernelName']}")
+            return cfg
+    logger.debug(f"shape M:{M} N:{N} K:{K} not tuned, using the heuristic")
+    return None
+
+
+def gemm_a4w4_fake(A, B, A_scale, B_scale, bias=None, dtype=dtypes.bf16, alpha=1.0, beta=0.0,
+                   bpreshuffle=True, apreshuffle=False, global_A_scale=None, global_B_scale=None):
+    n = B.shape[0]
+    return torch.empty((*A.shape[:-1], n), dtype=dtype, device=A.device)
+
+
+def gemm_a4w4(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, bias: Tensor | None = None,
+              dtype: torch.dtype = dtypes.bf16, alpha: float | None = 1.0, beta: float | None = 0.0,
+              bpreshuffle: bool | None = True, apreshuffle: bool | None = False,
+              global_A_scale: Tensor | None = None, global_B_scale: Tensor | None = None) -> Tensor:
+    """A4W4 GEMM (aiter/ops/gemm_op_a4w4.py:147-238).  NVFP4 global scales and
+    low-precision outputs are gfx1250-only in the reference and rejected."""
+    if dtype in (dtypes.fp4x2, dtypes.fp8):
+        raise NotImplementedError("gemm_a4w4 returns one plain-dtype tensor")
+    if global_A_scale is not None or global_B_scale is not None:
+        raise NotImplementedError("NVFP4 global scales are a gfx1250 feature")
+    if apreshuffle:
+        raise NotImplementedError("preshuffled A is a gfx1250 feature of gemm_a4w4")
+    if dtype != dtypes.bf16:
+        raise NotImplementedError("gemm_a4w4 produces bf16 output")
+    m = A.numel() // A.shape[-1]
+    n = B.shape[0]
+    k = A.shape[-1] * 2
+    out = torch.empty(((m + 31) // 32 * 32, n), dtype=dtype, device=A.device)
+    cfg = get_GEMM_config(m, n, k)
+    split_k = 0
+    kernel_name = ""
+    if cfg is not None:
+        split_k = int(cfg.get("splitK", 0) or 0)
+        kernel_name = str(cfg["kernelName"])
+    gemm_a4w4_asm(A.view(m, k // 2), B, A_scale, B_scale, out, kernel_name, bias, alpha, beta,
+                  bpreshuffle, log2_k_split=split_k)
+    return out[:m].view(*A.shape[:-1], n)
+
+
+def gemm_a4w4_asm(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, out: Tensor,
+                  kernelName: str = "", bias: Tensor | None = None, alpha: float | None = 1.0,
+                  beta: float | None = 0.0, bpreshuffle: bool | None = True,
+                  log2_k_split: int | None = None) -> Tensor:
+    """ctypes entry (aiter/ops/gemm_op_a4w4.py:241-287 ->
+    csrc/py_itfs_cu/asm_gemm_a4w4.cu:158-278).  ``kernelName`` is one of this
+    library's kernel names, or a reference ASM name whose ``_<tM>x<tN>E``
+    tile maps onto the same tile here; empty selects the heuristic.
+    D = alpha * A B^T + beta * bias."""
+    call("gemm_a4w4_asm", A, B, A_scale, B_scale, out, kernelName if kernelName else None, bias,
+         float(alpha if alpha is not None else 1.0), float(beta if beta is not None else 0.0),
+         int(bpreshuffle) if bpreshuffle is not None else 1,
+         int(log2_k_split) if log2_k_split is not None else 0)
+    return out
+
+
+def gemm_a4w4_blockscale(XQ: Tensor, WQ: Tensor, x_scale: Tensor, w_scale: Tensor, Out: Tensor,
+                         splitK: int = 0, kernelName: str = "") -> Tensor:
+    """CK-instance entry (csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale.cu:69-93).
+    A kernel name of this library selects that instance; other names use the
+    heuristic choice (as the reference's empty-name default)."""
+    from ._lib import kernel_table
+
+    kid = -1
+    if kernelName:
+        for row in kernel_table():
+            if row[1] == kernelName:
+                kid = row[0]
+    call("gemm_a4w4_blockscale", XQ, WQ, x_scale, w_scale, Out, int(splitK), int(kid))
+    return Out
+
+
+def gemm_a4w4_blockscale_tune(XQ: Tensor, WQ: Tensor, x_scale: Tensor, w_scale: Tensor, Out: Tensor,
+                              kernelId: int = 0, splitK: int = 0) -> Tensor:
+    """Tuning entry with an explicit kernel id
+    (csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale_tune.cu:58-90)."""
+    call("gemm_a4w4_blockscale", XQ, WQ, x_scale, w_scale, Out, int(splitK), int(kernelId))
+    return Out

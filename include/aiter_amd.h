@@ -1,0 +1,146 @@
+/*
+ * aiter_amd — C ABI of the MI355X (gfx950) scaled-GEMM hot path.
+ *
+ * Every entry point is `extern "C"`, takes plain POD tensor descriptors
+ * (`aiter_tensor_t*`), scalars and a trailing `hipStream_t`, returns 0 on
+ * success and -1 on error (message via `aiter_get_last_error`).  No C++
+ * exception crosses the boundary and the library never frees caller memory.
+ * The argument order and meaning follow the reference's ctypes convention
+ * (aiter/jit/core.py:1252-1555): Tensor -> aiter_tensor_t*, Optional[Tensor]
+ * -> NULL, str -> const char* (Optional -> NULL), bool -> int, float -> float.
+ *
+ * Citations (file:line) name the reference entry point each symbol replaces.
+ */
+#ifndef AITER_AMD_H
+#define AITER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Opaque HIP stream handle (hipStream_t). */
+typedef struct ihipStream_t* aiter_stream_t;
+
+/* Dtype ids, same order as AiterDtype in csrc/include/aiter_enum.h:40-56. */
+typedef enum {
+    AITER_DTYPE_fp8 = 0,      /* e4m3fn */
+    AITER_DTYPE_fp8_e8m0 = 1, /* e8m0 block scale */
+    AITER_DTYPE_fp16 = 2,
+    AITER_DTYPE_bf16 = 3,
+    AITER_DTYPE_fp32 = 4,
+    AITER_DTYPE_i4x2 = 5,
+    AITER_DTYPE_fp4x2 = 6,    /* two e2m1 per byte, even element low nibble */
+    AITER_DTYPE_u32 = 7,
+    AITER_DTYPE_i32 = 8,
+    AITER_DTYPE_i16 = 9,
+    AITER_DTYPE_i8 = 10,
+    AITER_DTYPE_u8 = 11,
+    AITER_DTYPE_i64 = 12,
+    AITER_DTYPE_u64 = 13,
+} AiterDtype;
+
+/* POD tensor descriptor, layout of csrc/include/aiter_tensor.h:8-17
+ * (aiter/utility/aiter_types.py:68-77).  Strides are in elements; for fp4x2
+ * one element is one byte (two e2m1 values). */
+typedef struct aiter_tensor_t {
+    void* ptr;
+    size_t numel;
+    int ndim;
+    int64_t shape[8];
+    int64_t strides[8];
+    int dtype; /* AiterDtype */
+    int device_id;
+} aiter_tensor_t;
+
+/* ---- error ABI: csrc/include/aiter_ctypes_error.h:60-71 ---------------- */
+int aiter_ctypes_abi_version(void); /* returns 2, as the reference */
+const char* aiter_get_last_error(void);
+void aiter_clear_last_error(void);
+
+/* ---- dispatch helper: csrc/py_itfs_cu/gemm_common.cu:12-41 ------------- */
+int getPaddedM(int M, int N, int K, int gl);
+
+/* ---- A4W4: csrc/py_itfs_cu/asm_gemm_a4w4.cu:158-172 -------------------
+ * D[M,N] bf16 = alpha * (A (x) A_scale) (B (x) B_scale)^T + beta * bias.
+ * A [M,K/2] fp4x2 row-major; B [N,K/2] fp4x2 preshuffled (bpreshuffle=1,
+ * shuffle_weight layout (16,16)) or row-major (bpreshuffle=0);
+ * A_scale [>=pad32(M), >=K/32] / B_scale [>=pad32(N), >=K/32] e8m0 in the
+ * shuffled MFMA layout; out [>=M, N] bf16 (aiter allocates pad32(M) rows);
+ * bias optional f32 [N], [1,N] or [M,N].  kernelName selects a kernel id
+ * from this library's table ("" or NULL = heuristic); log2_k_split < 0 lets
+ * the heuristic choose the split-K factor. */
+int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
+                  aiter_tensor_t* B_scale, aiter_tensor_t* out, const char* kernelName,
+                  aiter_tensor_t* bias, float alpha, float beta, int bpreshuffle,
+                  int log2_k_split, aiter_stream_t stream);
+
+/* ---- A4W4 blockscale (the CK-instance entry):
+ * csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale.cu:69-93 and the tune
+ * entry csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale_tune.cu:58-90.
+ * Same tensors as gemm_a4w4_asm with B preshuffled; kernelId < 0 means the
+ * heuristic choice, splitK is log2 of the K split. */
+int gemm_a4w4_blockscale(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* x_scale,
+                         aiter_tensor_t* w_scale, aiter_tensor_t* Y, int splitK,
+                         int kernelId, aiter_stream_t stream);
+
+/* ---- MXFP8 x MXFP4: aiter/ops/gemm_op_a8w4.py:18-31 (gfx1250 ASM entry
+ * csrc/py_itfs_cu/asm_mxfp8fp4gemm.cu), implemented here for gfx950.
+ * A [M,K] e4m3fn (row-major, or shuffle_weight layout when a_preshuffle=1),
+ * B [N,K/2] fp4x2 preshuffled, ScaleA/ScaleB shuffled e8m0, out [M,N] bf16. */
+int mxfp8_mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
+                         aiter_tensor_t* ScaleB, aiter_tensor_t* out, const char* kernelName,
+                         int a_preshuffle, aiter_stream_t stream);
+
+/* ---- bf16 A16W16: csrc/py_itfs_cu/asm_gemm_a16w16.cu:192-205 ----------
+ * out[M,N] (bf16 or f32) = A[M,K] @ B[N,K]^T (+ bias f32 [N]).  B row-major
+ * or preshuffled (bpreshuffle=1, shuffle_weight (16,16)).  `semaphore` is
+ * accepted for signature compatibility and unused (split-K partials go to a
+ * library-owned per-stream workspace). */
+int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
+                    aiter_tensor_t* semaphore, aiter_tensor_t* bias, int splitK,
+                    const char* kernelName, int bpreshuffle, aiter_stream_t stream);
+
+/* ---- opus a16w16: csrc/opus_gemm/opus_gemm.cu:133-209 (heuristic) and
+ * :294-350 (explicit kernel id).  XQ [b,M,K], WQ [b,N,K] bf16, Y [b,M,N]
+ * bf16 or f32, bias f32 [N] or [b,N] or NULL. */
+int opus_gemm(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
+              aiter_tensor_t* bias, aiter_stream_t stream);
+int opus_gemm_a16w16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
+                          aiter_tensor_t* bias, int kernelId, int splitK,
+                          aiter_stream_t stream);
+
+/* ---- quantisers ---------------------------------------------------------
+ * dynamic_per_group_scaled_quant: csrc/kernels/quant_kernels.cu:837-962.
+ * x [M,K] bf16/fp16/f32 -> out [M,K/2] fp4x2 or [M,K] fp8, scales e8m0
+ * (RoundUp, [M,K/32] plain or shuffled [pad256(M), pad8(K/32)]).  num_rows
+ * (optional i32 device scalar) limits the rows processed to
+ * num_rows*num_rows_factor. */
+int dynamic_per_group_scaled_quant(aiter_tensor_t* out, aiter_tensor_t* input,
+                                   aiter_tensor_t* scales, int group_size, int shuffle_scale,
+                                   aiter_tensor_t* num_rows, int num_rows_factor,
+                                   aiter_stream_t stream);
+
+/* quant_mxfp4: csrc/kernels/quant_mxfp4.cu:233-300 (4 round modes, optional
+ * e8m0 shuffle and fused shuffle_weight of the packed output).  a16w4 /
+ * gate_up layouts are MoE-only and rejected. */
+int quant_mxfp4(aiter_tensor_t* x, aiter_tensor_t* out_packed, aiter_tensor_t* out_scale,
+                int group_size, int round_mode, int e8m0_shuffle, int a16w4_shuffle,
+                int gate_up, int shuffle_weight, aiter_stream_t stream);
+
+/* dynamic_mxfp4_quant (Even mode, Triton kernel of
+ * aiter/utility/fp4_utils.py:373-597) and dynamic_mxfp8_quant (Even mode,
+ * aiter/ops/triton/quant/quant.py:235-297), as HIP kernels.  The fp4 scale
+ * buffer is [pad256(M), pad8(K/32)] when shuffle=1 (rows pad32(M).. untouched,
+ * rows M..pad32(M) and columns K/32..pad8 written as 0), else [M, K/32]. */
+int dynamic_mxfp4_quant(aiter_tensor_t* x, aiter_tensor_t* x_fp4, aiter_tensor_t* scale,
+                        int shuffle, aiter_stream_t stream);
+int dynamic_mxfp8_quant(aiter_tensor_t* x, aiter_tensor_t* y, aiter_tensor_t* scale,
+                        int shuffle, aiter_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* AITER_AMD_H */

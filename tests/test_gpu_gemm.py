@@ -1,0 +1,278 @@
+"""GPU parity of the GEMMs against the CPU oracle (dequantise -> f32 matmul ->
+bf16; op_tests/test_gemm_a4w4.py:23-39), tolerance rtol = atol = 1e-2 on every
+element.  Inputs are quantised by the oracle so these tests exercise the GEMM
+kernels alone; the quantisers have their own bit-exact tests.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mx_oracle as O
+from tests.conftest import announce
+from tests.mx_inputs import allclose_report, bf16_operand, mxfp4_operand, mxfp8_operand
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_np(t: torch.Tensor) -> np.ndarray:
+    return t.float().cpu().numpy()
+
+
+def _a4w4_case(m, n, k, seed=0):
+    a_q, a_s, a_ss = mxfp4_operand(m, k, seed, "triton")
+    b_q, b_s, b_ss = mxfp4_operand(n, k, seed + 1, "triton")
+    ref = O.bf16_bits_to_f32(O.gemm_a4w4_ref(a_q, b_q, a_s, b_s))
+    return a_q, a_ss, b_q, b_ss, ref
+
+
+def _dev(x, cuda):
+    return torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
+
+
+A4W4_SHAPES = [(1, 256, 256), (5, 512, 512), (16, 1024, 1024), (32, 7168, 2048), (33, 640, 1280),
+               (64, 7168, 2048), (65, 256, 512), (128, 1024, 1024), (256, 512, 2048), (300, 1040, 768),
+               (512, 512, 512)]
+
+
+@pytest.mark.parametrize("m,n,k", A4W4_SHAPES)
+def test_gemm_a4w4_heuristic(cuda, m, n, k):
+    import aiter_amd
+
+    announce(f"gemm_a4w4 {m}x{n}x{k}")
+    a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k)
+    out = aiter_amd.gemm_a4w4(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda),
+                              _dev(b_ss, cuda))
+    torch.cuda.synchronize()
+    assert out.shape == (m, n)
+    ok, msg = allclose_report(_bf16_np(out), ref)
+    assert ok, msg
+
+
+def _kernels(family, skinny=None, b_pre=True, a_pre=False, out_f32=False):
+    from aiter_amd._lib import kernel_table
+
+    return [r for r in kernel_table() if r[2] == family and r[8] == b_pre and r[7] == a_pre and r[9] == out_f32
+            and (skinny is None or r[3] == skinny)]
+
+
+def _kernel_names(family, **kw):
+    try:
+        return [r[1] for r in _kernels(family, **kw)]
+    except RuntimeError:
+        return []
+
+
+@pytest.mark.parametrize("name", _kernel_names("a4w4"))
+def test_gemm_a4w4_every_instance(cuda, name):
+    """Every A4W4 instance (tile and skinny, incl. split-K) on a ragged shape."""
+    import aiter_amd
+    from aiter_amd._lib import kernel_table
+
+    row = [r for r in kernel_table() if r[1] == name][0]
+    skinny, bm = row[3], row[4]
+    m = min(bm, 48) if skinny else 200
+    if skinny:
+        m = max(1, bm - 3)
+    n, k = 1024 + 48, 2048
+    announce(f"a4w4 instance {name} {m}x{n}x{k}")
+    a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=3)
+    out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda),
+                            _dev(b_ss, cuda), out, kernelName=name, log2_k_split=2 if row[6] else 0)
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out[:m]), ref)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("m", [1, 32, 96])
+def test_gemm_a4w4_row_major_b(cuda, m):
+    import aiter_amd
+
+    n, k = 512, 1024
+    announce(f"a4w4 bpreshuffle=0 {m}x{n}x{k}")
+    a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=9)
+    out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(b_q, cuda), _dev(a_ss, cuda), _dev(b_ss, cuda), out,
+                            bpreshuffle=False)
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out[:m]), ref)
+    assert ok, msg
+
+
+def test_gemm_a4w4_bias_alpha_beta(cuda):
+    """D = alpha * A B^T + beta * bias (csrc/py_itfs_cu/asm_gemm_a4w4.cu:154)."""
+    import aiter_amd
+
+    m, n, k = 64, 512, 512
+    announce("a4w4 alpha/beta/bias")
+    a_q, a_ss, b_q, b_ss, _ = _a4w4_case(m, n, k, seed=4)
+    bias = np.random.default_rng(5).standard_normal((1, n)).astype(np.float32)
+    a = O.dequant_mxfp4(a_q, O.unshuffle_scale(a_ss, m, k // 32))
+    b = O.dequant_mxfp4(b_q, O.unshuffle_scale(b_ss, n, k // 32))
+    ref = O.bf16_bits_to_f32(O.f32_to_bf16_bits(0.5 * (a @ b.T) + 2.0 * bias))
+    for name in ("a4w4_tile_64x128", "a4w4_skinny_m64"):
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+        aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda),
+                                _dev(b_ss, cuda), out, kernelName=name, bias=_dev(bias, cuda), alpha=0.5,
+                                beta=2.0)
+        torch.cuda.synchronize()
+        ok, msg = allclose_report(_bf16_np(out), ref)
+        assert ok, f"{name}: {msg}"
+
+
+def test_gemm_a4w4_full_size_spot_check(cuda):
+    """M=N=K=8192 (BASELINE prefill config): 256 random (m, n) outputs
+    against the oracle's f32 dot products of the dequantised rows."""
+    import aiter_amd
+
+    m = n = k = 8192
+    announce("a4w4 8192^3 spot check")
+    g = torch.Generator(device="cpu").manual_seed(0)
+    x = torch.randn((m, k), generator=g, dtype=torch.float32).to(torch.bfloat16).to(cuda)
+    w = torch.randn((n, k), generator=g, dtype=torch.float32).to(torch.bfloat16).to(cuda)
+    xq, xs = aiter_amd.dynamic_mxfp4_quant(x, shuffle=True)
+    wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+    out = aiter_amd.gemm_a4w4(xq, aiter_amd.shuffle_weight(wq), xs, ws)
+    torch.cuda.synchronize()
+    rs = np.random.default_rng(1)
+    rows = rs.choice(m, 16, replace=False)
+    cols = rs.choice(n, 16, replace=False)
+    a_q = xq.view(torch.uint8)[rows].cpu().numpy()
+    b_q = wq.view(torch.uint8)[cols].cpu().numpy()
+    xs_np = xs.view(torch.uint8).cpu().numpy()
+    ws_np = ws.view(torch.uint8).cpu().numpy()
+    a_s = O.unshuffle_scale(xs_np, m, k // 32)[rows]
+    b_s = O.unshuffle_scale(ws_np, n, k // 32)[cols]
+    ref = O.bf16_bits_to_f32(O.gemm_a4w4_ref(a_q, b_q, a_s, b_s))
+    got = out[torch.from_numpy(rows).to(cuda)][:, torch.from_numpy(cols).to(cuda)].float().cpu().numpy()
+    ok, msg = allclose_report(got, ref)
+    assert ok, msg
+
+
+# ----------------------------------------------------------------------------- a8w4
+A8W4_SHAPES = [(1, 256, 512), (17, 512, 1024), (64, 7168, 2048), (100, 640, 512), (256, 1024, 2048)]
+
+
+def _a8w4_case(m, n, k, seed=0):
+    a_q, a_s, a_ss = mxfp8_operand(m, k, seed)
+    b_q, b_s, b_ss = mxfp4_operand(n, k, seed + 1, "triton")
+    ref = O.bf16_bits_to_f32(O.gemm_a8w4_ref(a_q, b_q, a_s, b_s))
+    return a_q, a_ss, b_q, b_ss, ref
+
+
+@pytest.mark.parametrize("m,n,k", A8W4_SHAPES)
+def test_gemm_a8w4(cuda, m, n, k):
+    import aiter_amd
+
+    announce(f"gemm_a8w4_mxfp8 {m}x{n}x{k}")
+    a_q, a_ss, b_q, b_ss, ref = _a8w4_case(m, n, k)
+    a = _dev(a_q, cuda).view(torch.float8_e4m3fn)
+    out = aiter_amd.gemm_a8w4_mxfp8(a, _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda), _dev(b_ss, cuda),
+                                    a_preshuffle=False)
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out), ref)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("name", _kernel_names("a8w4") + _kernel_names("a8w4", a_pre=True))
+def test_gemm_a8w4_every_instance(cuda, name):
+    import aiter_amd
+    from aiter_amd._lib import kernel_table
+
+    row = [r for r in kernel_table() if r[1] == name][0]
+    skinny, bm, a_pre = row[3], row[4], row[7]
+    m = max(1, bm - 5) if skinny else 192
+    n, k = 768, 1024
+    announce(f"a8w4 instance {name} {m}x{n}x{k}")
+    a_q, a_ss, b_q, b_ss, ref = _a8w4_case(m, n, k, seed=2)
+    a_in = O.shuffle_weight(a_q) if a_pre else a_q
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+    from aiter_amd._lib import call
+
+    call("mxfp8_mxfp4_gemm_asm", _dev(a_in, cuda).view(torch.float8_e4m3fn), _dev(O.shuffle_weight(b_q), cuda),
+         _dev(a_ss, cuda), _dev(b_ss, cuda), out, name, int(a_pre))
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out), ref)
+    assert ok, msg
+
+
+def test_gemm_a8w4_dynamic_quant(cuda):
+    """bf16 activation -> fused dynamic MXFP8 quant -> GEMM."""
+    import aiter_amd
+
+    m, n, k = 256, 512, 2048
+    announce("a8w4 dynamic quant")
+    x = np.random.default_rng(0).standard_normal((m, k)).astype(np.float32)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    b_q, b_s, b_ss = mxfp4_operand(n, k, 1, "triton")
+    aq, as_ = O.quant_mxfp8(xb.float().numpy(), O.EVEN)
+    ref = O.bf16_bits_to_f32(O.gemm_a8w4_ref(aq, b_q, as_, b_s))
+    out = aiter_amd.gemm_a8w4_mxfp8_dynamic(xb.to(cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(b_ss, cuda))
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out), ref)
+    assert ok, msg
+
+
+# ----------------------------------------------------------------------------- bf16
+BF16_SHAPES = [(1, 256, 256), (7, 512, 1024), (32, 1024, 512), (64, 4096, 1024), (100, 640, 320),
+               (256, 512, 1024), (513, 1024, 768)]
+
+
+@pytest.mark.parametrize("m,n,k", BF16_SHAPES)
+def test_gemm_a16w16(cuda, m, n, k):
+    import aiter_amd
+
+    announce(f"gemm_a16w16 {m}x{n}x{k}")
+    a = bf16_operand(m, k, 0)
+    b = bf16_operand(n, k, 1)
+    ref = O.bf16_bits_to_f32(O.gemm_a16w16_ref(a, b))
+    at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+    bt = _dev(b.view(np.int16), cuda).view(torch.bfloat16)
+    out = aiter_amd.gemm_a16w16(at, bt)
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out), ref)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("name", _kernel_names("a16w16") + _kernel_names("a16w16", b_pre=False)
+                         + _kernel_names("a16w16", out_f32=True) + _kernel_names("a16w16", b_pre=False, out_f32=True))
+def test_gemm_a16w16_every_instance(cuda, name):
+    import aiter_amd
+    from aiter_amd._lib import kernel_table
+
+    row = [r for r in kernel_table() if r[1] == name][0]
+    skinny, bm, b_pre, out_f32 = row[3], row[4], row[8], row[9]
+    m = max(1, bm - 7) if skinny else 150
+    n, k = 528, 1024
+    announce(f"a16w16 instance {name} {m}x{n}x{k}")
+    a = bf16_operand(m, k, 5)
+    b = bf16_operand(n, k, 6)
+    bias = np.random.default_rng(8).standard_normal(n).astype(np.float32)
+    af, bf = O.bf16_bits_to_f32(a), O.bf16_bits_to_f32(b)
+    c = af @ bf.T + bias
+    ref = c if out_f32 else O.bf16_bits_to_f32(O.f32_to_bf16_bits(c))
+    bt_np = O.shuffle_weight(b) if b_pre else b
+    at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+    bt = _dev(bt_np.view(np.int16), cuda).view(torch.bfloat16)
+    out = torch.empty((m, n), dtype=torch.float32 if out_f32 else torch.bfloat16, device=cuda)
+    aiter_amd.gemm_a16w16_asm(at, bt, out, bias=_dev(bias, cuda), splitK=4 if row[6] else 0, kernelName=name,
+                              bpreshuffle=b_pre)
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(out.float().cpu().numpy(), ref)
+    assert ok, msg
+
+
+def test_gemm_a16w16_opus_batched(cuda):
+    import aiter_amd
+
+    announce("gemm_a16w16_opus batched")
+    b_, m, n, k = 3, 64, 256, 512
+    rs = np.random.default_rng(3)
+    A = torch.from_numpy(rs.standard_normal((b_, m, k)).astype(np.float32)).to(torch.bfloat16)
+    B = torch.from_numpy(rs.standard_normal((b_, n, k)).astype(np.float32)).to(torch.bfloat16)
+    bias = torch.from_numpy(rs.standard_normal((b_, n)).astype(np.float32))
+    ref = torch.bmm(A.float(), B.float().transpose(1, 2).contiguous()) + bias[:, None, :]
+    out = aiter_amd.gemm_a16w16_opus(A.to(cuda), B.to(cuda), bias.to(cuda))
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(out.float().cpu().numpy(), O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.numpy())))
+    assert ok, msg
