@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "gemm_kernels.h"
+#include "gemm_mx32.h"
 
 namespace aiter_amd {
 
@@ -64,6 +65,11 @@ void launch_tile(const GemmParams& p, dim3 grid, hipStream_t s) {
 
 constexpr int kSkinnyWaves = 8;
 
+template <int KA, int BM, int BN, int WMW>
+void launch_mx32(const GemmParams& p, dim3 grid, hipStream_t s) {
+    gemm_mx32_kernel<KA, BM, BN, WMW, false><<<grid, 256, 0, s>>>(p);
+}
+
 template <int KA, int MF, bool BP, bool SPLIT, bool OF>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
@@ -89,15 +95,14 @@ std::vector<Instance>& registry() {
             if (v.out_f32) nm += "_f32";
             reg.push_back({id++, nm, f, true, 16 * mf, 16, split, v, fn});
         };
-        // ---- a4w4 (B preshuffled) ----
+        // ---- a4w4 (B preshuffled): 32x32x64 tile kernels ----
         const Variant pre{false, true, false}, plain{false, false, false};
-        tile(kA4W4, 256, 256, pre, launch_tile<kFp4, kFp4, 256, 256, false, true, false>, "a4w4");
-        tile(kA4W4, 256, 128, pre, launch_tile<kFp4, kFp4, 256, 128, false, true, false>, "a4w4");
-        tile(kA4W4, 128, 256, pre, launch_tile<kFp4, kFp4, 128, 256, false, true, false>, "a4w4");
-        tile(kA4W4, 128, 128, pre, launch_tile<kFp4, kFp4, 128, 128, false, true, false>, "a4w4");
-        tile(kA4W4, 64, 256, pre, launch_tile<kFp4, kFp4, 64, 256, false, true, false>, "a4w4");
-        tile(kA4W4, 64, 128, pre, launch_tile<kFp4, kFp4, 64, 128, false, true, false>, "a4w4");
-        tile(kA4W4, 64, 64, pre, launch_tile<kFp4, kFp4, 64, 64, false, true, false>, "a4w4");
+        tile(kA4W4, 256, 256, pre, launch_mx32<kFp4, 256, 256, 2>, "a4w4");
+        tile(kA4W4, 256, 128, pre, launch_mx32<kFp4, 256, 128, 2>, "a4w4");
+        tile(kA4W4, 128, 256, pre, launch_mx32<kFp4, 128, 256, 2>, "a4w4");
+        tile(kA4W4, 128, 128, pre, launch_mx32<kFp4, 128, 128, 2>, "a4w4");
+        tile(kA4W4, 64, 256, pre, launch_mx32<kFp4, 64, 256, 1>, "a4w4");
+        tile(kA4W4, 64, 128, pre, launch_mx32<kFp4, 64, 128, 1>, "a4w4");
         skinny(kA4W4, 1, false, pre, launch_skinny<kFp4, 1, true, false, false>, "a4w4");
         skinny(kA4W4, 2, false, pre, launch_skinny<kFp4, 2, true, false, false>, "a4w4");
         skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false>, "a4w4");
@@ -105,7 +110,6 @@ std::vector<Instance>& registry() {
         skinny(kA4W4, 2, true, pre, launch_skinny<kFp4, 2, true, true, false>, "a4w4");
         skinny(kA4W4, 4, true, pre, launch_skinny<kFp4, 4, true, true, false>, "a4w4");
         // a4w4 with row-major B (bpreshuffle = 0)
-        tile(kA4W4, 256, 256, plain, launch_tile<kFp4, kFp4, 256, 256, false, false, false>, "a4w4");
         tile(kA4W4, 128, 128, plain, launch_tile<kFp4, kFp4, 128, 128, false, false, false>, "a4w4");
         tile(kA4W4, 64, 128, plain, launch_tile<kFp4, kFp4, 64, 128, false, false, false>, "a4w4");
         skinny(kA4W4, 1, false, plain, launch_skinny<kFp4, 1, false, false, false>, "a4w4");
@@ -113,10 +117,10 @@ std::vector<Instance>& registry() {
         skinny(kA4W4, 4, false, plain, launch_skinny<kFp4, 4, false, false, false>, "a4w4");
         // ---- a8w4 ----
         const Variant a8{false, true, false}, a8p{true, true, false};
-        tile(kA8W4, 128, 256, a8, launch_tile<kFp8, kFp4, 128, 256, false, true, false>, "a8w4");
-        tile(kA8W4, 128, 128, a8, launch_tile<kFp8, kFp4, 128, 128, false, true, false>, "a8w4");
-        tile(kA8W4, 64, 256, a8, launch_tile<kFp8, kFp4, 64, 256, false, true, false>, "a8w4");
-        tile(kA8W4, 64, 128, a8, launch_tile<kFp8, kFp4, 64, 128, false, true, false>, "a8w4");
+        tile(kA8W4, 128, 256, a8, launch_mx32<kFp8, 128, 256, 2>, "a8w4");
+        tile(kA8W4, 128, 128, a8, launch_mx32<kFp8, 128, 128, 2>, "a8w4");
+        tile(kA8W4, 64, 256, a8, launch_mx32<kFp8, 64, 256, 1>, "a8w4");
+        tile(kA8W4, 64, 128, a8, launch_mx32<kFp8, 64, 128, 1>, "a8w4");
         tile(kA8W4, 128, 256, a8p, launch_tile<kFp8, kFp4, 128, 256, true, true, false>, "a8w4");
         tile(kA8W4, 128, 128, a8p, launch_tile<kFp8, kFp4, 128, 128, true, true, false>, "a8w4");
         tile(kA8W4, 64, 128, a8p, launch_tile<kFp8, kFp4, 64, 128, true, true, false>, "a8w4");

@@ -1,0 +1,281 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X scaled-GEMM hot path (one GPU).
+
+Headline (``value``): MXFP4 x MXFP4 (A4W4) GEMM at M=N=K=8192 (BASELINE.json
+configs[2]) in TFLOP/s: A, B drawn N(0,1) from a seed, quantised per 1x32 to
+MXFP4 (e2m1 + e8m0, Even rounding as the reference test/tuner), B
+preshuffled, bf16 output.  One step = one ``gemm_a4w4`` call on inputs
+resident in HBM.  The K timed steps are captured in a HIP graph and replayed
+once between two synchronisations (launch overhead is not part of a step).
+
+Also reported on the same JSON line:
+* ``decode``: the bandwidth-bound configs[1] (M in {1,8,16,32,64}, N=7168,
+  K=2048), cold-cache (B/scales rotated over >512 MiB) and warm, GB/s incl.
+  scales and % of 8 TB/s;
+* ``extra``: bf16 A16W16 8192x8192x8192, MXFP8xMXFP4 4096x7168x16384 and the
+  dynamic quantiser;
+* ``roofline`` of the dominant kernel (A4W4 tile kernel) from HIP events on the
+  launch stream; ``traffic`` is the HBM bytes/launch measured with rocprofv3
+  PMC counters (profiles/), or null when no such measurement is committed;
+* ``cpu_baseline``: the CPU oracle (dequantise -> f32 matmul, the reference's
+  ``run_torch`` of op_tests/test_gemm_a4w4.py:23-39) on a bounded row sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MXFP4 = 10100.0   # TFLOP/s dense (MI355X)
+PEAK_MXFP8 = 5000.0
+PEAK_BF16 = 2500.0
+PEAK_HBM = 8000.0      # GB/s
+REF_A4W4_8192 = 5089.97  # TFLOP/s, aiter/configs/a4w4_blockscale_tuned_gemm.csv:1284
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def quantised_operands(m, n, k, seed, dev):
+    import aiter_amd
+
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    a = torch.randn((m, k), generator=g, dtype=torch.float32).to(dev)
+    b = torch.randn((n, k), generator=g, dtype=torch.float32).to(dev)
+    aq, as_ = aiter_amd.dynamic_mxfp4_quant(a, shuffle=True)
+    bq, bs = aiter_amd.dynamic_mxfp4_quant(b, shuffle=True)
+    del a, b
+    return aq, as_, aiter_amd.shuffle_weight(bq), bs
+
+
+def time_graph(fn, steps, warmup):
+    """Capture `steps` calls of fn() in a HIP graph, replay once, return the
+    average seconds per call measured by HIP events on the launch stream."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # one eager call on the capture stream (lazy state)
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for _ in range(steps):
+                fn()
+    torch.cuda.synchronize()
+    g.replay()  # warm replay
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def a4w4_bytes(m, n, k):
+    """Algorithmic HBM bytes incl. scales: A, B (1/2 B/elem), both e8m0 scale
+    tensors (1 B per 32 elems), bf16 C."""
+    return m * k // 2 + n * k // 2 + m * k // 32 + n * k // 32 + 2 * m * n
+
+
+def bench_prefill(steps, warmup, dev):
+    import aiter_amd
+
+    m = n = k = 8192
+    aq, as_, bq, bs = quantised_operands(m, n, k, 0, dev)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
+
+    sec = time_graph(step, steps, warmup)
+    flop = 2.0 * m * n * k
+    return sec, flop / sec / 1e12
+
+
+def bench_decode(dev, steps=50):
+    import aiter_amd
+
+    res = []
+    n, k = 7168, 2048
+    g = torch.Generator(device="cpu").manual_seed(1)
+    b = torch.randn((n, k), generator=g).to(dev)
+    bq, bs = aiter_amd.dynamic_mxfp4_quant(b, shuffle=True)
+    bq = aiter_amd.shuffle_weight(bq)
+    per = bq.numel() + bs.numel()
+    copies = max(2, (600 << 20) // per)  # rotate > 512 MiB (defeats L2 + 256 MiB MALL)
+    bqs = [bq.clone() for _ in range(copies)]
+    bss = [bs.clone() for _ in range(copies)]
+    for m in (1, 8, 16, 32, 64):
+        a = torch.randn((m, k), generator=g).to(dev)
+        aq, as_ = aiter_amd.dynamic_mxfp4_quant(a, shuffle=True)
+        out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=dev)
+        it = {"i": 0}
+
+        def cold():
+            i = it["i"] % copies
+            it["i"] += 1
+            aiter_amd.gemm_a4w4_asm(aq, bqs[i], as_, bss[i], out)
+
+        def warm():
+            aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
+
+        t_cold = time_graph(cold, min(steps, copies), 3)
+        t_warm = time_graph(warm, steps, 3)
+        byts = a4w4_bytes(m, n, k)
+        ref_bw = (m * k / 2 + n * k / 2 + 2 * m * n)  # reference `bw` formula (scales excluded)
+        res.append({
+            "M": m, "N": n, "K": k,
+            "us_cold": round(t_cold * 1e6, 3), "us_warm": round(t_warm * 1e6, 3),
+            "GBps_cold": round(byts / t_cold / 1e9, 1), "GBps_warm": round(byts / t_warm / 1e9, 1),
+            "hbm_frac_cold": round(byts / t_cold / 1e9 / PEAK_HBM, 4),
+            "ref_formula_GBps_cold": round(ref_bw / t_cold / 1e9, 1),
+        })
+        log(f"decode M={m}: cold {t_cold*1e6:.2f} us ({byts/t_cold/1e9:.0f} GB/s), warm {t_warm*1e6:.2f} us")
+    return res
+
+
+def bench_extra(dev):
+    import aiter_amd
+
+    out = {}
+    # bf16 A16W16 M=N=K=8192
+    m = n = k = 8192
+    g = torch.Generator(device="cpu").manual_seed(2)
+    a = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
+    b = torch.randn((n, k), generator=g).to(torch.bfloat16).to(dev)
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    sema = torch.empty(0, dtype=torch.uint32, device=dev)
+    t = time_graph(lambda: aiter_amd.gemm_a16w16_asm(a, b, c), 10, 2)
+    out["bf16_8192x8192x8192"] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1),
+                                  "frac_bf16_peak": round(2 * m * n * k / t / 1e12 / PEAK_BF16, 4)}
+    del a, b, c
+    # MXFP8 x MXFP4 M=4096 N=7168 K=16384 (+ dynamic quant of the bf16 activation)
+    m, n, k = 4096, 7168, 16384
+    x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
+    w = torch.randn((n, k), generator=g).to(dev)
+    wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+    wq = aiter_amd.shuffle_weight(wq)
+    del w
+    xq, xs = aiter_amd.dynamic_mxfp8_quant(x, shuffle=True)
+    t = time_graph(lambda: aiter_amd.gemm_a8w4_mxfp8(xq, wq, xs, ws, a_preshuffle=False), 10, 2)
+    tq = time_graph(lambda: aiter_amd.dynamic_mxfp8_quant(x, shuffle=True), 20, 2)
+    out["a8w4_4096x7168x16384"] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1),
+                                   "frac_mxfp8_peak": round(2 * m * n * k / t / 1e12 / PEAK_MXFP8, 4),
+                                   "quant_us": round(tq * 1e6, 1),
+                                   "quant_GBps": round(m * k * (2 + 1 + 1 / 32) / tq / 1e9, 1)}
+    # MXFP4 activation quant 8192 x 8192 bf16
+    xa = torch.randn((8192, 8192), generator=g).to(torch.bfloat16).to(dev)
+    tq = time_graph(lambda: aiter_amd.per_1x32_mx_quant_hip(xa, shuffle=True), 20, 2)
+    out["mxfp4_quant_8192x8192"] = {"us": round(tq * 1e6, 1),
+                                    "GBps": round(8192 * 8192 * (2 + 0.5 + 1 / 32) / tq / 1e9, 1)}
+    return out
+
+
+def cpu_baseline(budget_s=12.0):
+    """Oracle (numpy) dequantise + f32 matmul on a row sample of the 8192^3
+    A4W4 problem, scaled to TFLOP/s."""
+    from oracle import mx_oracle as O
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [os.cpu_count()])
+    except Exception:
+        threads = os.cpu_count()
+    n = k = 8192
+    rs = np.random.default_rng(0)
+    # already-quantised operands (random e2m1 bytes, e8m0 scales around 2^0):
+    # the timed CPU path is the reference's dequantise + f32 matmul
+    bq = rs.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    bsc = rs.integers(120, 134, (n, k // 32), dtype=np.uint8)
+    rows = 512
+    total_flop = 0.0
+    total_t = 0.0
+    runs = 0
+    while total_t < budget_s and runs < 8:
+        aq = rs.integers(0, 256, (rows, k // 2), dtype=np.uint8)
+        asc = rs.integers(120, 134, (rows, k // 32), dtype=np.uint8)
+        t0 = time.perf_counter()
+        O.gemm_a4w4_ref(aq, bq, asc, bsc)
+        dt = time.perf_counter() - t0
+        total_t += dt
+        total_flop += 2.0 * rows * n * k
+        runs += 1
+    return {"value": round(total_flop / total_t / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads),
+            "kind": "port",
+            "sample": f"{runs} run(s) of M={rows} rows x N=K=8192 (dequantise A and B + f32 matmul + bf16), "
+                      f"{total_t:.1f} s"}
+
+
+def traffic_from_profiles():
+    p = os.path.join(ROOT, "profiles", "a4w4_8192_traffic.json")
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--quick", action="store_true", help="headline only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda", 0)
+    import aiter_amd  # noqa: F401  (fails loudly if the HIP library is missing)
+
+    log("prefill A4W4 8192^3")
+    sec, tflops = bench_prefill(args.steps, args.warmup, dev)
+    log(f"prefill: {sec*1e6:.1f} us/step, {tflops:.0f} TFLOP/s")
+    decode = [] if args.quick else bench_decode(dev)
+    extra = {} if args.quick else bench_extra(dev)
+    cpu = None if (args.no_cpu or args.quick) else cpu_baseline()
+    m = n = k = 8192
+    line = {
+        "metric": "TFLOP/s and % dense MXFP4/bf16 peak (M=8192); HBM GB/s % peak at M<=32",
+        "value": round(tflops, 1),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": round(tflops / REF_A4W4_8192, 4),
+        "dtype": "mxfp4",
+        "data": "synthetic",
+        "config": {"workload": "A4W4 MXFP4xMXFP4 GEMM, M=N=K=8192, preshuffled B, e8m0 per-1x32 scales, bf16 out "
+                               "(BASELINE configs[2])", "M": m, "N": n, "K": k},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_MXFP4, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_MXFP4, 4), "traffic": traffic_from_profiles()},
+        "cpu_baseline": cpu,
+        "decode": decode,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
