@@ -38,6 +38,7 @@ PEAK_MXFP4 = 10100.0   # TFLOP/s dense (MI355X)
 PEAK_MXFP8 = 5000.0
 PEAK_BF16 = 2500.0
 PEAK_HBM = 8000.0      # GB/s
+COPY_BYTES = 1 << 30    # calibration copy of the traffic counter runs
 REF_A4W4_8192 = 5089.97  # TFLOP/s, aiter/configs/a4w4_blockscale_tuned_gemm.csv:1284
 
 
@@ -185,7 +186,7 @@ def bench_extra(dev):
     return out
 
 
-def cpu_baseline(budget_s=12.0):
+def cpu_baseline(budget_s=10.0):
     """Oracle (numpy) dequantise + f32 matmul on a row sample of the 8192^3
     A4W4 problem, scaled to TFLOP/s."""
     from oracle import mx_oracle as O
@@ -205,7 +206,7 @@ def cpu_baseline(budget_s=12.0):
     total_flop = 0.0
     total_t = 0.0
     runs = 0
-    while total_t < budget_s and runs < 8:
+    while total_t < budget_s and runs < 64:
         aq = rs.integers(0, 256, (rows, k // 2), dtype=np.uint8)
         asc = rs.integers(120, 134, (rows, k // 32), dtype=np.uint8)
         t0 = time.perf_counter()
@@ -218,6 +219,27 @@ def cpu_baseline(budget_s=12.0):
             "kind": "port",
             "sample": f"{runs} run(s) of M={rows} rows x N=K=8192 (dequantise A and B + f32 matmul + bf16), "
                       f"{total_t:.1f} s"}
+
+
+def pmc_workload(dev):
+    """Launches for the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE /
+    WRITE_SIZE): three plain device copies of COPY_BYTES (the calibration
+    kernel: it must read and write exactly COPY_BYTES each), then three
+    launches of the headline A4W4 8192^3 GEMM, each on a cold L2 (the copy
+    in between evicts it)."""
+    import aiter_amd
+
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    aq, as_, bq, bs = quantised_operands(8192, 8192, 8192, 0, dev)
+    out = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        dst.copy_(src)
+    for _ in range(3):
+        dst.copy_(src)
+        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
+    torch.cuda.synchronize()
+    log(f"pmc workload done: copy {COPY_BYTES} B x6, a4w4 8192^3 x3")
 
 
 def traffic_from_profiles():
@@ -235,6 +257,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--pmc", action="store_true",
+                    help="only the launches of the HBM-traffic counter runs (copy calibration + A4W4 8192^3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -245,6 +269,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     import aiter_amd  # noqa: F401  (fails loudly if the HIP library is missing)
+    if args.pmc:
+        pmc_workload(dev)
+        return
 
     log("prefill A4W4 8192^3")
     sec, tflops = bench_prefill(args.steps, args.warmup, dev)

@@ -140,6 +140,24 @@ int dynamic_mxfp4_quant(aiter_tensor_t* x, aiter_tensor_t* x_fp4, aiter_tensor_t
 int dynamic_mxfp8_quant(aiter_tensor_t* x, aiter_tensor_t* y, aiter_tensor_t* scale,
                         int shuffle, aiter_stream_t stream);
 
+/* ---- library introspection and workspace --------------------------------
+ * The reference keeps its kernel list in per-arch CSVs next to its ASM code
+ * objects (hsa/gfx950/f4gemm/f4gemm_bf16_per1x32Fp4.csv) and the CK instance
+ * list in generated headers; the tuner enumerates those.  Here the table is
+ * compiled into the library and read through these two calls:
+ * aiter_amd_num_kernels() -> number of kernel ids (ids are 0..n-1);
+ * aiter_amd_kernel_info(id, buf, len) writes
+ * "id,name,family,skinny,bm,bn,split,a_pre,b_pre,out_f32" (0 or -1). */
+int aiter_amd_num_kernels(void);
+int aiter_amd_kernel_info(int id, char* buf, int buflen);
+
+/* Pre-sizes the split-K fp32 workspace owned by (device, stream) to at least
+ * `bytes`, so that a later HIP-graph capture never needs to allocate.  The
+ * reference's counterpart is the caller-provided semaphore / workspace
+ * tensor of csrc/py_itfs_cu/asm_gemm_a16w16.cu:192-205 and
+ * aiter/ops/opus/gemm_op_opus.py (opus_gemm_workspace_init). */
+int gemm_workspace_reserve(int device, aiter_stream_t stream, size_t bytes);
+
 #ifdef __cplusplus
 }
 #endif
