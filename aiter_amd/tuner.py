@@ -1,0 +1,321 @@
+"""Shape-keyed dispatch tuner for the A4W4, A8W4 and bf16 GEMMs.
+
+Role of the reference's tuners (csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale_tune.py:101-381,
+csrc/gemm_a16w16/gemm_a16w16_tune.py:400-1070, aiter/utility/base_tuner.py,
+aiter/utility/mp_tuner.py:367-709): for every untuned shape, build seeded
+inputs, run each kernel of this library that accepts the shape (and each
+split-K factor of the split instances), reject candidates whose output
+differs from an fp32 reference of the dequantised operands by more than
+rtol = atol = 1e-2 on more than ``max_err_ratio`` of the elements, time the
+rest, and write the fastest as one row of the reference's tuned-CSV schema:
+
+* a4w4 / a8w4: ``gfx,cu_num,M,N,K,kernelId,splitK,us,kernelName,tflops,bw,errRatio``
+  (``splitK`` = log2 of the K split; ``bw`` = the reference's formula,
+  A and B at 1/2 byte per element, C at 2 bytes, scales excluded,
+  aiter/utility/base_tuner.py:1597-1615);
+* bf16: ``gfx,cu_num,M,N,K,bias,dtype,outdtype,scaleAB,bpreshuffle,libtype,
+  solidx,splitK,us,kernelName,err_ratio,tflops,bw`` with libtype
+  ``aiter_amd`` and solidx = kernel id (``splitK`` = number of K splits).
+
+Timing: each candidate runs ``iters`` times inside one HIP graph, cycling
+over enough copies of the weight operand (> 512 MiB in total, capped at 64
+copies) that every call streams its weights from HBM as in serving, and the
+graph replay is timed with HIP events on the launch stream.
+
+    python -m aiter_amd.tuner --family a4w4 -i untuned.csv -o tuned.csv
+    python -m aiter_amd.tuner --family a16w16 --sweep -o bf16_tuned_gemm.csv
+"""
+from __future__ import annotations
+
+import argparse
+import math
+import os
+import sys
+import time
+
+import pandas as pd
+import torch
+
+from . import dtypes
+from ._lib import call, kernel_table
+from .config import A4W4_COLUMNS, BF16_COLUMNS, get_cu_num, get_gfx
+from .quant import dynamic_mxfp4_quant, dynamic_mxfp8_quant
+from .shuffle import shuffle_weight
+
+E2M1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
+ROTATE_BYTES = 600 << 20
+MAX_COPIES = 64
+
+# BASELINE dispatch sweep: (N, K) x M, plus the decode / prefill / mixed shapes
+SWEEP_NK = [(4096, 4096), (14336, 4096), (4096, 14336), (28672, 8192), (8192, 28672)]
+SWEEP_M = [1, 32, 256, 2048, 8192]
+EXTRA_A4W4 = [(m, 7168, 2048) for m in (1, 8, 16, 32, 64)] + [(8192, 8192, 8192), (8192, 2048, 16384)]
+EXTRA_A8W4 = [(256, 7168, 16384), (4096, 7168, 16384)]
+
+
+def sweep_shapes(family: str):
+    shapes = [(m, n, k) for (n, k) in SWEEP_NK for m in SWEEP_M]
+    if family == "a4w4":
+        shapes += EXTRA_A4W4
+    elif family == "a8w4":
+        shapes = [(m, n, k) for (n, k) in SWEEP_NK for m in SWEEP_M] + EXTRA_A8W4
+    seen, out = set(), []
+    for s in shapes:
+        if s not in seen:
+            seen.add(s)
+            out.append(s)
+    return out
+
+
+# ---------------------------------------------------------------- references
+def _dequant_fp4(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """fp4x2 [R, K/2] + plain e8m0 [R, K/32] -> f32 [R, K] (aiter/utility/fp4_utils.py:25-52,213-221)."""
+    lut = torch.tensor(E2M1, dtype=torch.float32, device=q.device)
+    q = q.view(torch.uint8)
+    codes = torch.stack((q & 0xF, q >> 4), dim=-1).reshape(q.shape[0], -1).long()
+    scale = torch.exp2(s.view(torch.uint8).float() - 127.0).repeat_interleave(32, dim=1)
+    return lut[codes] * scale
+
+
+def _dequant_fp8(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    scale = torch.exp2(s.view(torch.uint8).float() - 127.0).repeat_interleave(32, dim=1)
+    return q.view(dtypes.fp8).float() * scale
+
+
+def err_ratio(out: torch.Tensor, ref: torch.Tensor, rtol=1e-2, atol=1e-2) -> float:
+    """Fraction of elements outside atol + rtol*|ref| (aiter/test_common.py:479-490)."""
+    bad = (out.float() - ref).abs() > atol + rtol * ref.abs()
+    return bad.float().mean().item()
+
+
+# ---------------------------------------------------------------- timing
+def time_rotated(fn, n_copies: int, iters: int) -> float:
+    """Average seconds per call of ``fn(i)`` (i = rotation index), captured
+    ``iters`` times in one HIP graph and replayed after a warm replay."""
+    for i in range(min(3, n_copies)):
+        fn(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        fn(0)
+        s.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(iters):
+                fn(i % n_copies)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(s):
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / iters
+
+
+def _copies(per_call_bytes: int) -> int:
+    return max(1, min(MAX_COPIES, math.ceil(ROTATE_BYTES / max(1, per_call_bytes))))
+
+
+# ---------------------------------------------------------------- candidates
+def candidates(family: str, M: int, bpreshuffle: bool = True, out_f32: bool = False):
+    """(kernel id, name, log2 split) triples of this library for the shape."""
+    out = []
+    for (kid, name, fam, skinny, bm, bn, split, a_pre, b_pre, of32) in kernel_table():
+        if fam != family or a_pre or b_pre != bpreshuffle or of32 != out_f32:
+            continue
+        if skinny and M > bm:
+            continue
+        if not skinny and M <= 16 and bm > 64:
+            continue  # a 128/256-row tile for a handful of rows is never the fastest
+        if split:
+            for l2 in (0, 1, 2, 3):  # 0 = the library's own split choice
+                out.append((kid, name, l2))
+        else:
+            out.append((kid, name, 0))
+    return out
+
+
+def _log(msg):
+    print(f"[tune] {msg}", flush=True)
+
+
+def tune_mx(family: str, M: int, N: int, K: int, iters: int, max_err_ratio: float, seed: int = 0):
+    """Best row for one A4W4 (family a4w4) or A8W4 (family a8w4) shape."""
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    a = torch.randn((M, K), generator=g).to(dev)
+    b = torch.randn((N, K), generator=g).to(dev)
+    bq, bs_plain = dynamic_mxfp4_quant(b, shuffle=False)
+    _, bs = dynamic_mxfp4_quant(b, shuffle=True)
+    if family == "a4w4":
+        aq, as_plain = dynamic_mxfp4_quant(a, shuffle=False)
+        _, as_ = dynamic_mxfp4_quant(a, shuffle=True)
+        deq_a = _dequant_fp4(aq, as_plain)
+        a_bytes = M * K // 2
+    else:
+        aq, as_plain = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=False)
+        _, as_ = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=True)
+        deq_a = _dequant_fp8(aq, as_plain)
+        a_bytes = M * K
+    prev_tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = deq_a @ _dequant_fp4(bq, bs_plain).t()
+    torch.backends.cuda.matmul.allow_tf32 = prev_tf32
+    del a, b, deq_a
+    bqs = shuffle_weight(bq)
+    n_copies = _copies(bqs.numel() + bs.numel())
+    wq = [bqs] + [bqs.clone() for _ in range(n_copies - 1)]
+    ws = [bs] + [bs.clone() for _ in range(n_copies - 1)]
+    pad_m = (M + 31) // 32 * 32
+    out = torch.empty((pad_m, N), dtype=dtypes.bf16, device=dev)
+    best = None
+    for kid, name, l2 in candidates(family, M):
+        if family == "a4w4":
+            def run(i, kid=kid, l2=l2):
+                call("gemm_a4w4_blockscale", aq, wq[i], as_, ws[i], out, l2, kid)
+        else:
+            def run(i, kid=kid, l2=l2, name=name):
+                call("mxfp8_mxfp4_gemm_asm", aq, wq[i], as_, ws[i], out, name, 0)
+            if l2:
+                continue  # the MXFP8 entry takes no split argument
+        try:
+            out.zero_()
+            run(0)
+            torch.cuda.synchronize()
+        except RuntimeError as e:
+            _log(f"  skip {name}: {e}")
+            continue
+        er = err_ratio(out[:M], ref)
+        if er > max_err_ratio:
+            _log(f"  reject {name} split {l2}: errRatio {er:.4f}")
+            continue
+        t = time_rotated(run, n_copies, iters)
+        if best is None or t < best[0]:
+            best = (t, kid, name, l2, er)
+    del wq, ws
+    if best is None:
+        raise RuntimeError(f"no kernel passes {family} M={M} N={N} K={K}")
+    t, kid, name, l2, er = best
+    us = t * 1e6
+    tflops = 2.0 * M * N * K / t / 1e12
+    bw = (a_bytes + N * K / 2 + 2 * M * N) / t / 1e9
+    return {"gfx": get_gfx(), "cu_num": get_cu_num(), "M": M, "N": N, "K": K, "kernelId": kid, "splitK": l2,
+            "us": round(us, 4), "kernelName": name, "tflops": round(tflops, 2), "bw": round(bw, 2),
+            "errRatio": round(er, 6)}
+
+
+def tune_bf16(M: int, N: int, K: int, bias: bool, otype: torch.dtype, bpreshuffle: bool, iters: int,
+              max_err_ratio: float, seed: int = 0):
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    a = torch.randn((M, K), generator=g).to(dtypes.bf16).to(dev)
+    b = torch.randn((N, K), generator=g).to(dtypes.bf16).to(dev)
+    bias_t = torch.randn((N,), generator=g).to(dev) if bias else None
+    prev_tf32 = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ref = a.float() @ b.float().t()
+    torch.backends.cuda.matmul.allow_tf32 = prev_tf32
+    if bias_t is not None:
+        ref = ref + bias_t
+    bw_ = shuffle_weight(b) if bpreshuffle else b
+    n_copies = _copies(bw_.numel() * 2)
+    wb = [bw_] + [bw_.clone() for _ in range(n_copies - 1)]
+    out = torch.empty((M, N), dtype=otype, device=dev)
+    sema = torch.empty(0, dtype=torch.uint32, device=dev)
+    best = None
+    for kid, name, l2 in candidates("a16w16", M, bpreshuffle, otype == torch.float32):
+        split = (1 << l2) if l2 else 0
+
+        def run(i, name=name, split=split):
+            call("gemm_a16w16_asm", a, wb[i], out, sema, bias_t, split, name, int(bpreshuffle))
+        try:
+            out.zero_()
+            run(0)
+            torch.cuda.synchronize()
+        except RuntimeError as e:
+            _log(f"  skip {name}: {e}")
+            continue
+        er = err_ratio(out, ref)
+        if er > max_err_ratio:
+            _log(f"  reject {name} split {split}: errRatio {er:.4f}")
+            continue
+        t = time_rotated(run, n_copies, iters)
+        if best is None or t < best[0]:
+            best = (t, kid, name, split, er)
+    del wb
+    if best is None:
+        raise RuntimeError(f"no kernel passes bf16 M={M} N={N} K={K}")
+    t, kid, name, split, er = best
+    return {"gfx": get_gfx(), "cu_num": get_cu_num(), "M": M, "N": N, "K": K, "bias": bias,
+            "dtype": str(dtypes.bf16), "outdtype": str(otype), "scaleAB": False, "bpreshuffle": bpreshuffle,
+            "libtype": "aiter_amd", "solidx": kid, "splitK": split, "us": round(t * 1e6, 4), "kernelName": name,
+            "err_ratio": round(er, 6), "tflops": round(2.0 * M * N * K / t / 1e12, 2),
+            "bw": round(2.0 * (M * K + N * K + M * N) / t / 1e9, 2)}
+
+
+# ---------------------------------------------------------------- driver
+def _read_untuned(path: str, family: str):
+    df = pd.read_csv(path, skipinitialspace=True)
+    rows = []
+    for _, r in df.iterrows():
+        if family == "a16w16":
+            rows.append((int(r["M"]), int(r["N"]), int(r["K"]), str(r.get("bias", False)) == "True",
+                         str(r.get("outdtype", "torch.bfloat16")), str(r.get("bpreshuffle", False)) == "True"))
+        else:
+            rows.append((int(r["M"]), int(r["N"]), int(r["K"])))
+    return rows
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--family", choices=["a4w4", "a8w4", "a16w16"], required=True)
+    ap.add_argument("-i", "--untune_file", default=None, help="untuned CSV (M,N,K[,bias,dtype,outdtype,...])")
+    ap.add_argument("--sweep", action="store_true", help="tune the built-in benchmark shape sweep")
+    ap.add_argument("-o", "--tune_file", required=True)
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--errRatio", type=float, default=0.05, help="max fraction of elements off tolerance")
+    ap.add_argument("--append", action="store_true", help="keep rows of an existing output for other keys")
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        print("the tuner needs a GPU", file=sys.stderr)
+        return 2
+    if args.untune_file:
+        shapes = _read_untuned(args.untune_file, args.family)
+    elif args.sweep:
+        shapes = sweep_shapes("a4w4" if args.family == "a16w16" else args.family)
+        if args.family == "a16w16":
+            shapes = [(m, n, k, False, "torch.bfloat16", False) for (m, n, k) in shapes]
+    else:
+        ap.error("give -i untuned.csv or --sweep")
+    rows = []
+    t0 = time.time()
+    for s in shapes:
+        _log(f"{args.family} {s}")
+        if args.family == "a16w16":
+            m, n, k, bias, otype, bpre = s
+            row = tune_bf16(m, n, k, bias, torch.float32 if "float32" in otype else dtypes.bf16, bpre,
+                            args.iters, args.errRatio)
+        else:
+            row = tune_mx(args.family, *s, iters=args.iters, max_err_ratio=args.errRatio)
+        _log(f"  -> {row['kernelName']} split {row['splitK']} {row['us']} us {row['tflops']} TFLOP/s")
+        rows.append(row)
+        torch.cuda.empty_cache()
+    cols = BF16_COLUMNS if args.family == "a16w16" else A4W4_COLUMNS
+    df = pd.DataFrame(rows, columns=cols)
+    if args.append and os.path.exists(args.tune_file):
+        old = pd.read_csv(args.tune_file)
+        keys = cols[:10] if args.family == "a16w16" else cols[:5]
+        df = pd.concat([old, df], ignore_index=True).drop_duplicates(subset=keys, keep="last")
+    os.makedirs(os.path.dirname(os.path.abspath(args.tune_file)), exist_ok=True)
+    df.to_csv(args.tune_file, index=False)
+    _log(f"wrote {len(df)} rows to {args.tune_file} in {time.time() - t0:.0f} s")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
