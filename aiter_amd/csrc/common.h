@@ -146,8 +146,11 @@ AA_DEV uint32_t f32_to_bf16_rne(float f) {
     return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
 }
 
+// two floats -> packed bf16 pair (v_cvt_pk_bf16_f32: round to nearest even)
 AA_DEV uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
 AA_DEV float bf16_bits_to_f32(uint32_t b) { return __builtin_bit_cast(float, b << 16); }

@@ -17,6 +17,7 @@
 
 #include "gemm_kernels.h"
 #include "gemm_mx32.h"
+#include "gemm_flat.h"
 
 namespace aiter_amd {
 
@@ -70,6 +71,11 @@ void launch_mx32(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_mx32_kernel<KA, BM, BN, WMW, false><<<grid, 256, 0, s>>>(p);
 }
 
+template <int KA, int BM>
+void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
+    gemm_flat_kernel<KA, BM, false><<<grid, 256, 0, s>>>(p);
+}
+
 template <int KA, int MF, bool BP, bool SPLIT, bool OF>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
@@ -95,11 +101,13 @@ std::vector<Instance>& registry() {
             if (v.out_f32) nm += "_f32";
             reg.push_back({id++, nm, f, true, 16 * mf, 16, split, v, fn});
         };
-        // ---- a4w4 (B preshuffled): 32x32x64 tile kernels ----
+        // ---- a4w4 (B preshuffled): 32x32x64 tile kernels; the 256-column
+        // tiles read B straight into registers (gemm_flat.h), the others stage
+        // A and B through LDS (gemm_mx32.h) ----
         const Variant pre{false, true, false}, plain{false, false, false};
-        tile(kA4W4, 256, 256, pre, launch_mx32<kFp4, 256, 256, 2>, "a4w4");
+        tile(kA4W4, 256, 256, pre, launch_flat<kFp4, 256>, "a4w4");
         tile(kA4W4, 256, 128, pre, launch_mx32<kFp4, 256, 128, 2>, "a4w4");
-        tile(kA4W4, 128, 256, pre, launch_mx32<kFp4, 128, 256, 2>, "a4w4");
+        tile(kA4W4, 128, 256, pre, launch_flat<kFp4, 128>, "a4w4");
         tile(kA4W4, 128, 128, pre, launch_mx32<kFp4, 128, 128, 2>, "a4w4");
         tile(kA4W4, 64, 256, pre, launch_mx32<kFp4, 64, 256, 1>, "a4w4");
         tile(kA4W4, 64, 128, pre, launch_mx32<kFp4, 64, 128, 1>, "a4w4");
@@ -117,7 +125,7 @@ std::vector<Instance>& registry() {
         skinny(kA4W4, 4, false, plain, launch_skinny<kFp4, 4, false, false, false>, "a4w4");
         // ---- a8w4 ----
         const Variant a8{false, true, false}, a8p{true, true, false};
-        tile(kA8W4, 128, 256, a8, launch_mx32<kFp8, 128, 256, 2>, "a8w4");
+        tile(kA8W4, 128, 256, a8, launch_flat<kFp8, 128>, "a8w4");
         tile(kA8W4, 128, 128, a8, launch_mx32<kFp8, 128, 128, 2>, "a8w4");
         tile(kA8W4, 64, 256, a8, launch_mx32<kFp8, 64, 256, 1>, "a8w4");
         tile(kA8W4, 64, 128, a8, launch_mx32<kFp8, 64, 128, 1>, "a8w4");
@@ -315,7 +323,8 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
              "A/B rows must be 16-byte aligned");
     p.D = c.out->ptr;
     p.ldd = row_stride_2d(c.out, "out");
-    AA_CHECK(p.ldd % 4 == 0 && ((uintptr_t)p.D & 15) == 0, "out rows must be 16-byte aligned");
+    AA_CHECK((p.ldd * (c.var.out_f32 ? 4 : 2)) % 16 == 0 && ((uintptr_t)p.D & 15) == 0,
+             "out rows must be 16-byte aligned");
     p.M = (int)M;
     p.N = (int)N;
     p.K = (int)K;
@@ -329,6 +338,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         AA_CHECK(br == 1 || br >= M, "bias must be [N], [1,N] or [M,N]");
         p.bias = static_cast<const float*>(c.bias->ptr);
         p.ld_bias = br == 1 ? 0 : row_stride_2d(c.bias, "bias");
+        AA_CHECK(p.ld_bias % 4 == 0 && ((uintptr_t)p.bias & 15) == 0, "bias rows must be 16-byte aligned");
     }
     if (scaled) {
         check_tensor(c.As, "A_scale", 1);

@@ -1,0 +1,308 @@
+// MX tile kernel with B read straight into registers ("flat" B), for tiles
+// 256 columns wide.  v_mfma_scale_f32_32x32x64_f8f6f4 on gfx950.
+//
+// Why: aiter's preshuffled B (shuffle_weight (16,16)) stores every 16-row
+// block so that one 16-byte load per lane is exactly the B operand of one
+// 32x32x64 MFMA (rows l%32, bytes [16*(l/32), +16) of a 32-byte K window).
+// B therefore needs no LDS staging: each wave loads its own 64 columns into
+// VGPRs two 256-element stages ahead of use.  Only A (row-major, so it needs
+// re-laying) and the e8m0 scales pass through LDS, in a ring of up to 4
+// stages, which leaves up to 3 stages (~6000 MFMA cycles) to hide the
+// global-memory latency of A.
+//
+// Work split: 4 waves side by side along N (1 x 4), wave w owns columns
+// [64w, 64w+64) of the tile and every row, so no B byte is loaded twice and
+// every wave reads the same A fragments from LDS.
+//
+// Per 256-element stage and workgroup:
+//   A  : BM rows x 128 B (fp4) or 256 B (fp8), copied global -> LDS with
+//        buffer_load ... lds in 1 KiB chunks of 8 rows x 128 B; 16-byte pieces
+//        XOR-swizzled by row so the reads of one k-step are bank-conflict free;
+//   B  : per wave 2 tiles x 4 k-steps of buffer_load_dwordx4 into VGPRs;
+//   scales: 4 chunks of 4 groups x 256 B (A groups, then B groups), one
+//        chunk per wave (a spare chunk is filled with zeros).
+// Loads past the end of A, B or K go through range-checked buffer descriptors
+// and return zeros, so the loop is a single basic block with no bounds
+// branches (which keeps the accumulators in AGPRs); a stage past the end of K
+// contributes exactly zero (zero operands, scale byte 0).
+#pragma once
+#include "gemm_mx32.h"
+
+namespace aiter_amd {
+
+template <int KA, int BM>
+struct FlatCfg {
+    static constexpr int FA = (KA == kFp8) ? 2 : 1;   // 128-byte halves of an A row per stage
+    static constexpr int A_CH = (BM / 8) * FA;        // A chunks per stage
+    static constexpr int STAGE_KB = A_CH + 4;         // + 4 scale chunks
+    static constexpr int NS = (160 / STAGE_KB) > 4 ? 4 : (160 / STAGE_KB);
+};
+
+template <int KA, int BM, bool OUT_F32>
+__global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
+    using Cfg = FlatCfg<KA, BM>;
+    constexpr int BN = 256;
+    constexpr int NS = Cfg::NS;
+    constexpr int FA = Cfg::FA;
+    constexpr int MA = BM / 32;           // 32-row A tiles per wave (all rows of the tile)
+    constexpr int NB = 2;                 // 32-column B tiles per wave
+    constexpr int A_CH = Cfg::A_CH;
+    constexpr int AG = BM / 32;           // A scale groups in the tile
+    constexpr int SCA = (AG + 3) / 4;     // A scale chunks
+    static_assert(SCA + 2 <= 4, "scale chunks: one per wave");
+    static_assert(NS >= 2, "two LDS stages minimum");
+    static_assert(A_CH % 4 == 0, "A chunks split over 4 waves");
+    constexpr int NA = A_CH / 4;          // A DMAs per wave per stage
+    constexpr int NDMA = NA + 1;          // + one scale chunk
+    constexpr int NBL = NB * 4;           // B loads per wave per stage
+    constexpr int STAGE_BYTES = Cfg::STAGE_KB * 1024;
+    constexpr int A_ROW_BYTES = 128 * FA;
+
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
+
+    int tm, tn;
+    tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int nstages = p.K / 256;
+
+    // ---- A: chunk c = half*(BM/8) + 8-row block; lane l -> row l/8, stored piece l%8
+    //      holding global 16-byte piece (l%8) ^ swz(row), swz(r) = (r>>1)&7
+    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.A + (int64_t)m0 * p.lda, (int64_t)(p.M - m0) * p.lda);
+    int a_off[NA];
+#pragma unroll
+    for (int q = 0; q < NA; ++q) {
+        const int c = wave + 4 * q;
+        const int half = c / (BM / 8), rb = c % (BM / 8);
+        const int r = rb * 8 + (lane >> 3);
+        a_off[q] = r * (int)p.lda + half * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16);
+    }
+    // ---- B (preshuffled (16,16)): tile j of wave w = 16-row blocks 4w+2j, 4w+2j+1;
+    //      k-step s of stage t at blk*16*ldb + (4t+s)*512 + (l/32)*256 + (l%16)*16
+    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.B + (int64_t)n0 * p.ldb, (int64_t)(p.N - n0) * p.ldb);
+    int b_off[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int blk = 4 * wave + 2 * j + ((lane >> 4) & 1);
+        b_off[j] = blk * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
+    }
+    // ---- scales: wave w copies chunk w (A chunks first, then the 2 B chunks)
+    const int ga0 = m0 / 32, gb0 = n0 / 32;
+    const __amdgpu_buffer_rsrc_t sa_rsrc =
+        make_rsrc(p.As + (int64_t)ga0 * 32 * p.sa_stride, (int64_t)(p.sa_groups - ga0) * 32 * p.sa_stride);
+    const __amdgpu_buffer_rsrc_t sb_rsrc =
+        make_rsrc(p.Bs + (int64_t)gb0 * 32 * p.sb_stride, (int64_t)(p.sb_groups - gb0) * 32 * p.sb_stride);
+    const __amdgpu_buffer_rsrc_t null_rsrc = make_rsrc(p.A, 0);
+    const bool sc_is_a = wave < SCA;
+    const bool sc_is_b = wave >= SCA && wave < SCA + 2;
+    const int sc_chunk = sc_is_a ? wave : (sc_is_b ? wave - SCA : 0);
+    const int sc_off = (4 * sc_chunk + (lane >> 4)) * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + (lane & 15) * 16;
+    const __amdgpu_buffer_rsrc_t sc_rsrc = sc_is_a ? sa_rsrc : (sc_is_b ? sb_rsrc : null_rsrc);
+
+    auto dma_stage = [&](int t) {
+        const bool live = t < nstages;
+        const __amdgpu_buffer_rsrc_t ra = live ? a_rsrc : null_rsrc;
+        const __amdgpu_buffer_rsrc_t rs = live ? sc_rsrc : null_rsrc;
+        uint8_t* base = smem + (t % NS) * STAGE_BYTES;
+#pragma unroll
+        for (int q = 0; q < NA; ++q) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], t * A_ROW_BYTES);
+        dma16(rs, base + (A_CH + wave) * 1024, sc_off, t * 256);
+    };
+    auto load_b = [&](int t, int j, int s) -> i32x4_t {
+        const __amdgpu_buffer_rsrc_t rb = t < nstages ? b_rsrc : null_rsrc;
+        return __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + s * 512, t * 2048, 0);
+    };
+
+    const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;
+    const int sshift = 8 * ((lane >> 4) & 1);
+
+    f32x16v_t acc[MA][NB];
+#pragma unroll
+    for (int i = 0; i < MA; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = f32x16v_t{};
+
+    i32x4_t af[2][MA][FA];
+    i32x4_t bq[2][NB][4];          // [stage parity][tile][k-step]
+    int sa_raw[MA][2], sb_raw[NB][2];
+
+    const int ar = lane & 31;
+    const int a_lane_off = (ar >> 3) * 1024 + (ar & 7) * 128;
+    const int a_swz = (ar >> 1) & 7;
+    auto read_a = [&](int t, int s, int slot) {
+        const uint8_t* base = smem + (t % NS) * STAGE_BYTES;
+#pragma unroll
+        for (int i = 0; i < MA; ++i)
+#pragma unroll
+            for (int h = 0; h < FA; ++h) {
+                const int piece = (FA == 1) ? (2 * s + (lane >> 5)) : ((4 * s + 2 * h + (lane >> 5)) & 7);
+                const int hh = (FA == 1) ? 0 : ((4 * s + 2 * h) >> 3);
+                af[slot][i][h] = *reinterpret_cast<const i32x4_t*>(
+                    base + (hh * (BM / 8) + i * 4) * 1024 + a_lane_off + ((piece ^ a_swz) * 16));
+            }
+    };
+    auto read_scales = [&](int t) {
+        const uint8_t* base = smem + (t % NS) * STAGE_BYTES + A_CH * 1024 + pos0;
+#pragma unroll
+        for (int i = 0; i < MA; ++i) {
+            sa_raw[i][0] = *reinterpret_cast<const int*>(base + i * 256);
+            sa_raw[i][1] = *reinterpret_cast<const int*>(base + i * 256 + 128);
+        }
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const uint8_t* g = base + SCA * 1024 + (2 * wave + j) * 256;
+            sb_raw[j][0] = *reinterpret_cast<const int*>(g);
+            sb_raw[j][1] = *reinterpret_cast<const int*>(g + 128);
+        }
+    };
+    struct StepScales {
+        int a[MA], b[NB];
+    };
+    auto step_scales = [&](int s) {
+        StepScales sc;
+        const int shift = sshift + 16 * (s >> 1);
+#pragma unroll
+        for (int i = 0; i < MA; ++i) sc.a[i] = sa_raw[i][s & 1] >> shift;
+#pragma unroll
+        for (int j = 0; j < NB; ++j) sc.b[j] = sb_raw[j][s & 1] >> shift;
+        return sc;
+    };
+    auto mma = [&](int aslot, int bpar, int s, const StepScales& sc) {
+#pragma unroll
+        for (int i = 0; i < MA; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                i32x8_t bv, av;
+                bv[0] = bq[bpar][j][s][0]; bv[1] = bq[bpar][j][s][1];
+                bv[2] = bq[bpar][j][s][2]; bv[3] = bq[bpar][j][s][3];
+                bv[4] = 0; bv[5] = 0; bv[6] = 0; bv[7] = 0;
+                av[0] = af[aslot][i][0][0]; av[1] = af[aslot][i][0][1];
+                av[2] = af[aslot][i][0][2]; av[3] = af[aslot][i][0][3];
+                if constexpr (FA == 2) {
+                    av[4] = af[aslot][i][1][0]; av[5] = af[aslot][i][1][1];
+                    av[6] = af[aslot][i][1][2]; av[7] = af[aslot][i][1][3];
+                } else {
+                    av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
+                }
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], 4,
+                                                                            OpTraits<KA>::fmt, 0, sc.b[j], 0, sc.a[i]);
+            }
+    };
+    // B of stage t+2, k-step s, into the registers k-step s of stage t just used
+    auto prefetch_b = [&](int t, int bpar, int s) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bq[bpar][j][s] = load_b(t + 2, j, s);
+    };
+
+    // Each k-step is its own scheduling region (sched_barrier fences): the LDS
+    // reads of the next k-step, this k-step's MFMAs, a third of the next-but-two
+    // stage's A copies and the B loads of stage t+2 into the registers this
+    // k-step has just consumed.  The LDS reads therefore have a whole k-step
+    // (16 MFMAs) of latency budget and the compiler's lgkmcnt waits never stall.
+    constexpr int DMA_PART = (NDMA + 2) / 3;
+    auto dma_part = [&](int t, int part) {
+        const bool live = t < nstages;
+        const __amdgpu_buffer_rsrc_t ra = live ? a_rsrc : null_rsrc;
+        const __amdgpu_buffer_rsrc_t rs = live ? sc_rsrc : null_rsrc;
+        uint8_t* base = smem + (t % NS) * STAGE_BYTES;
+#pragma unroll
+        for (int q = part * DMA_PART; q < (part + 1) * DMA_PART && q < NDMA; ++q) {
+            if (q < NA) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], t * A_ROW_BYTES);
+            else dma16(rs, base + (A_CH + wave) * 1024, sc_off, t * 256);
+        }
+    };
+    // loads issued after the last A copy of stage t+1 and before the wait at
+    // the end of iteration t (all of them from later iterations)
+    constexpr int LOADS_ITER = NDMA + NBL;
+    constexpr int WAIT_N = NS >= 3 ? (NS - 3) * LOADS_ITER + NDMA + 3 * NB : 0;
+    static_assert(WAIT_N < 64, "vmcnt range");
+    auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+    // order inside a k-step region: one LDS read after each of the first RD
+    // MFMAs, the region's global loads after the last MFMAs
+    constexpr int RD = MA * FA;
+    constexpr int MF = MA * NB;
+    auto pace = [&](int vmem) {
+#pragma unroll
+        for (int k = 0; k < MF; ++k) {
+            if (k < RD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
+            if (k >= MF - vmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM
+        }
+    };
+
+    // stage t of the main loop; bpar = t & 1 selects the B registers
+    auto stage = [&](int t, int bpar) {
+        read_a(t, 1, 1);
+        dma_part(t + NS - 1, 0);
+        mma(0, bpar, 0, step_scales(0));
+        prefetch_b(t, bpar, 0);
+        pace(NB + DMA_PART);
+        fence();
+        read_a(t, 2, 0);
+        dma_part(t + NS - 1, 1);
+        mma(1, bpar, 1, step_scales(1));
+        prefetch_b(t, bpar, 1);
+        pace(NB + DMA_PART);
+        fence();
+        read_a(t, 3, 1);
+        dma_part(t + NS - 1, 2);
+        mma(0, bpar, 2, step_scales(2));
+        prefetch_b(t, bpar, 2);
+        pace(NB + NDMA - 2 * DMA_PART);
+        const StepScales sc3 = step_scales(3);
+        fence();
+        // stage t+1 published: own copies landed and own LDS reads of stage t
+        // done (waitcnt), then everyone's (barrier).  No workgroup memory fence:
+        // it would also wait for the copies of later stages still in flight.
+        wait_vmcnt_lgkm0<WAIT_N>();
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        fence();
+        read_a(t + 1, 0, 0);
+        read_scales(t + 1);
+        mma(1, bpar, 3, sc3);
+        prefetch_b(t, bpar, 3);
+        pace(NB);
+        fence();
+    };
+
+    // prologue: B stages 0, 1 first, then A stages 0..NS-2 (so that at the loop
+    // head at least as many loads follow each B load as in the steady state,
+    // and the compiler's B waits there stay as loose as in the loop); wait for A 0
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bq[0][j][s] = load_b(0, j, s);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) bq[1][j][s] = load_b(1, j, s);
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t) dma_stage(t);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_vmcnt<(NS - 2) * NDMA>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    read_scales(0);
+    read_a(0, 0, 0);
+
+    // the loop runs an even number of stages; an odd last stage is a zero stage
+    for (int t = 0; t < nstages; t += 2) {
+        stage(t, 0);
+        stage(t + 1, 1);
+    }
+
+    // ---- epilogue through LDS (the ring is free once every copy has landed)
+    static_assert(!OUT_F32, "the flat kernel writes bf16");
+    static_assert(BM * BN * 2 <= NS * STAGE_BYTES, "epilogue fits the ring");
+    wait_vmcnt<0>();
+    __syncthreads();
+    store_block_bf16<MA, NB>(p, acc, smem + wave * (BM * 128), lane, m0, n0 + wave * 64);
+}
+
+}  // namespace aiter_amd

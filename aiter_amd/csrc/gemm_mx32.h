@@ -15,18 +15,17 @@
 //
 // Data movement per 256-element K stage (4 k-steps):
 //   * A and B are copied global -> LDS by buffer_load ... lds (no VGPR
-//     staging).  One instruction moves one 1 KiB operand chunk: lane l's 16
-//     bytes land at chunk + 16*l, so the per-lane global address is simply the
-//     operand element the MFMA lane needs (row-major A: row l%32, byte
-//     16*(l/32) of the k-step window; preshuffled B: four contiguous 256-byte
-//     runs of the (16,16) layout).  Rows beyond M/N read as 0 (buffer range).
-//   * Two LDS stages: the DMA of stage t+1 is in flight while stage t is
-//     multiplied; one vmcnt(0) + barrier per stage.
-//   * Operand chunks of k-step s+1 are read from LDS while the MFMAs of k-step
-//     s run.
-//   * Scales: per 32-row group two dwords per lane per stage, gathered from
-//     aiter's shuffled e8m0 layout one stage ahead and shifted by
-//     8*((l>>4)&1) at use, so one uniform op_sel (0 or 2) picks the byte.
+//     staging).  One instruction moves one 1 KiB chunk: lane l's 16 bytes land
+//     at chunk + 16*l.  A is staged as whole 128-byte row pieces (8 rows per
+//     chunk, 16-byte pieces XOR-swizzled by row, bank-conflict-free reads);
+//     preshuffled B is already in MFMA operand order (four 256-byte runs per
+//     chunk).  Rows beyond M/N read as 0 (buffer range check).
+//   * Scales: one chunk of 4 groups x 256 bytes per wave and stage, read as
+//     two dwords per lane and group and shifted by 8*((l>>4)&1) + 16*(s>>1)
+//     at use, so op_sel stays 0.
+//   * A ring of NS stages (as many as fit 160 KiB, at most 4); one vmcnt wait
+//     and barrier per stage; LDS reads of k-step s+1 overlap the MFMAs of s.
+//   * Epilogue through LDS (store_block_bf16): whole output rows per store.
 #pragma once
 #include "gemm_kernels.h"
 
@@ -64,6 +63,62 @@ template <int N>
 AA_DEV void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt range");
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): own copies up to the N newest have landed and
+// every LDS access of this wave has completed
+template <int N>
+AA_DEV void wait_vmcnt_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// Epilogue of a wave's (32*MA) x (32*NB) block of 32x32 MFMA accumulators
+// (lane l holds C[m = l%32][n = 8q + 4(l/32) + r] of each tile) written as
+// bf16, D = alpha*acc + beta*bias.  Stored directly, each global store would
+// touch 32 rows; instead the block goes through the wave's own LDS scratch
+// `cb` (32*MA * 64*NB bytes), 16-byte pieces XOR-swizzled by row so that both
+// the 8-byte writes and the 16-byte reads spread over the banks, and leaves as
+// whole rows of 64*NB bytes.  (mb, nb) is the block's global origin.
+template <int MA, int NB>
+AA_DEV void store_block_bf16(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb,
+                             int nb) {
+    constexpr int RB = 64 * NB;                 // bytes per block row
+    constexpr int P = RB / 16;                  // 16-byte pieces per row
+    constexpr int SWM = (P < 8 ? P : 8) - 1;    // swizzle mask
+    constexpr int RSH = RB < 128 ? 1 : 0;       // two 64-byte rows share a 128-byte bank line
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int i = 0; i < MA; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int r = i * 32 + (lane & 31);
+                const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
+                float v[4] = {acc[i][j][4 * q] * p.alpha, acc[i][j][4 * q + 1] * p.alpha,
+                              acc[i][j][4 * q + 2] * p.alpha, acc[i][j][4 * q + 3] * p.alpha};
+                if (p.bias) {
+                    const int m = min(mb + r, p.M - 1), n = min(nb + nl, p.N - 4);
+                    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
+                }
+                const int piece = (nl >> 3) ^ ((r >> RSH) & SWM);
+                *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (nl & 7) * 2) =
+                    u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            }
+    // the block is the wave's own: its LDS accesses complete in order
+    constexpr int ROWS_PER = 64 / P;            // rows per read instruction
+    const int pc = lane % P;
+    const int n_out = nb + pc * 8;
+#pragma unroll 4
+    for (int rr = 0; rr < 32 * MA; rr += ROWS_PER) {
+        const int r = rr + lane / P;
+        const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
+        if (mb + r < p.M && n_out < p.N)
+            *reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(p.D) + (int64_t)(mb + r) * p.ldd + n_out) = v;
+    }
 }
 
 // LDS ring depth that fits 160 KiB for a tile
@@ -289,18 +344,12 @@ __global__ __launch_bounds__(256, 1) void gemm_mx32_kernel(GemmParams p) {
         pace(0);
     }
 
-    // ---- epilogue: lane holds C[m = l%32][n = 8q + 4(l/32) + r]
-#pragma unroll
-    for (int i = 0; i < MA; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int m = m0 + wm * WM + i * 32 + (lane & 31);
-                const int n = n0 + wn * WN + j * 32 + 8 * q + 4 * (lane >> 5);
-                const f32x4_t v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-                store_frag<OUT_F32>(p, v, m, n);
-            }
+    // ---- epilogue through LDS (the ring is free once every copy has landed)
+    static_assert(!OUT_F32, "the MX tile kernel writes bf16");
+    static_assert(BM * BN * 2 <= NS * STAGE_BYTES, "epilogue fits the ring");
+    wait_vmcnt<0>();
+    __syncthreads();
+    store_block_bf16<MA, NB>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
 }
 
 }  // namespace aiter_amd

@@ -276,3 +276,35 @@ def test_gemm_a16w16_opus_batched(cuda):
     torch.cuda.synchronize()
     ok, msg = allclose_report(out.float().cpu().numpy(), O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref.numpy())))
     assert ok, msg
+
+
+TILE_K_CASES = [(300, 528, 256), (257, 512, 768), (64, 272, 2304), (520, 784, 1280)]
+
+
+@pytest.mark.parametrize("m,n,k", TILE_K_CASES)
+def test_tile_instances_odd_stage_counts(cuda, m, n, k):
+    """Every A4W4 / A8W4 tile instance with K/256 = 1, 3, 9, 5 (odd stage
+    counts, a single stage) on ragged M and N, called twice in a row with
+    different data (stale LDS or registers from the first call must not leak
+    into the second)."""
+    import aiter_amd
+    from aiter_amd._lib import call
+
+    for fam in ("a4w4", "a8w4"):
+        for row in _kernels(fam, skinny=False):
+            name = row[1]
+            for seed in (11, 12):
+                announce(f"{fam} tile {name} {m}x{n}x{k} seed {seed}")
+                if fam == "a4w4":
+                    a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=seed)
+                    out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
+                    aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda),
+                                            _dev(b_ss, cuda), out, kernelName=name)
+                else:
+                    a_q, a_ss, b_q, b_ss, ref = _a8w4_case(m, n, k, seed=seed)
+                    out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+                    call("mxfp8_mxfp4_gemm_asm", _dev(a_q, cuda).view(torch.float8_e4m3fn),
+                         _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda), _dev(b_ss, cuda), out, name, 0)
+                torch.cuda.synchronize()
+                ok, msg = allclose_report(_bf16_np(out[:m]), ref)
+                assert ok, f"{name}: {msg}"
