@@ -312,6 +312,10 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     AA_CHECK(M < (1LL << 31) && N < (1LL << 31), "M/N too large");
 
     const int64_t elem = (c.fam == kA16W16) ? 2 : 1;
+    // the MX kernels address A, B and the scales through 32-bit buffer offsets
+    if (scaled)
+        AA_CHECK(M * row_stride_2d(c.A, "A") < (1LL << 31) && N * row_stride_2d(c.B, "B") < (1LL << 31),
+                 "A and B must each be smaller than 2 GiB");
     GemmParams p{};
     p.A = static_cast<const uint8_t*>(c.A->ptr);
     p.B = static_cast<const uint8_t*>(c.B->ptr);
@@ -325,6 +329,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     p.ldd = row_stride_2d(c.out, "out");
     AA_CHECK((p.ldd * (c.var.out_f32 ? 4 : 2)) % 16 == 0 && ((uintptr_t)p.D & 15) == 0,
              "out rows must be 16-byte aligned");
+    AA_CHECK(M * p.ldd * (c.var.out_f32 ? 4 : 2) < (1LL << 31), "out must be smaller than 2 GiB");
     p.M = (int)M;
     p.N = (int)N;
     p.K = (int)K;

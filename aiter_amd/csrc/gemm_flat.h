@@ -26,6 +26,8 @@
 // branches (which keeps the accumulators in AGPRs); a stage past the end of K
 // contributes exactly zero (zero operands, scale byte 0).
 #pragma once
+#include <type_traits>
+
 #include "gemm_mx32.h"
 
 namespace aiter_amd {
@@ -116,7 +118,11 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     };
 
     const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;
-    const int sshift = 8 * ((lane >> 4) & 1);
+    // per group, lane l needs bytes h and 2+h (h = (l>>4)&1) of the window's
+    // two scale dwords d0 (k-steps 0, 2) and d1 (k-steps 1, 3); v_perm packs
+    // them as [d0.h, d0.(2+h), d1.h, d1.(2+h)] so that k-step s takes byte
+    // {0, 2, 1, 3}[s] through the MFMA's op_sel, the same for every lane
+    const unsigned sc_perm = 0x06040200u + ((lane >> 4) & 1) * 0x01010101u;
 
     f32x16v_t acc[MA][NB];
 #pragma unroll
@@ -126,7 +132,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
 
     i32x4_t af[2][MA][FA];
     i32x4_t bq[2][NB][4];          // [stage parity][tile][k-step]
-    int sa_raw[MA][2], sb_raw[NB][2];
+    int sa_pk[MA], sb_pk[NB];      // packed scale bytes of the stage being multiplied
 
     const int ar = lane & 31;
     const int a_lane_off = (ar >> 3) * 1024 + (ar & 7) * 128;
@@ -143,33 +149,26 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
                     base + (hh * (BM / 8) + i * 4) * 1024 + a_lane_off + ((piece ^ a_swz) * 16));
             }
     };
-    auto read_scales = [&](int t) {
+    auto read_scales = [&](int t, int (&pa)[MA], int (&pb)[NB]) {
         const uint8_t* base = smem + (t % NS) * STAGE_BYTES + A_CH * 1024 + pos0;
 #pragma unroll
         for (int i = 0; i < MA; ++i) {
-            sa_raw[i][0] = *reinterpret_cast<const int*>(base + i * 256);
-            sa_raw[i][1] = *reinterpret_cast<const int*>(base + i * 256 + 128);
+            const unsigned d0 = *reinterpret_cast<const unsigned*>(base + i * 256);
+            const unsigned d1 = *reinterpret_cast<const unsigned*>(base + i * 256 + 128);
+            pa[i] = (int)__builtin_amdgcn_perm(d1, d0, sc_perm);
         }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const uint8_t* g = base + SCA * 1024 + (2 * wave + j) * 256;
-            sb_raw[j][0] = *reinterpret_cast<const int*>(g);
-            sb_raw[j][1] = *reinterpret_cast<const int*>(g + 128);
+            const unsigned d0 = *reinterpret_cast<const unsigned*>(g);
+            const unsigned d1 = *reinterpret_cast<const unsigned*>(g + 128);
+            pb[j] = (int)__builtin_amdgcn_perm(d1, d0, sc_perm);
         }
     };
-    struct StepScales {
-        int a[MA], b[NB];
-    };
-    auto step_scales = [&](int s) {
-        StepScales sc;
-        const int shift = sshift + 16 * (s >> 1);
-#pragma unroll
-        for (int i = 0; i < MA; ++i) sc.a[i] = sa_raw[i][s & 1] >> shift;
-#pragma unroll
-        for (int j = 0; j < NB; ++j) sc.b[j] = sb_raw[j][s & 1] >> shift;
-        return sc;
-    };
-    auto mma = [&](int aslot, int bpar, int s, const StepScales& sc) {
+    // k-step S of the stage; scale byte {0, 2, 1, 3}[S] of the packed scales
+    auto mma = [&](int aslot, int bpar, auto sel, const int (&pa)[MA], const int (&pb)[NB]) {
+        constexpr int s = decltype(sel)::value;
+        constexpr int osel = (s == 0) ? 0 : (s == 1) ? 2 : (s == 2) ? 1 : 3;
 #pragma unroll
         for (int i = 0; i < MA; ++i)
 #pragma unroll
@@ -187,7 +186,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
                     av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
                 }
                 acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], 4,
-                                                                            OpTraits<KA>::fmt, 0, sc.b[j], 0, sc.a[i]);
+                                                                            OpTraits<KA>::fmt, osel, pb[j], osel, pa[i]);
             }
     };
     // B of stage t+2, k-step s, into the registers k-step s of stage t just used
@@ -234,24 +233,27 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
 
     // stage t of the main loop; bpar = t & 1 selects the B registers
     auto stage = [&](int t, int bpar) {
+        using S0 = std::integral_constant<int, 0>;
+        using S1 = std::integral_constant<int, 1>;
+        using S2 = std::integral_constant<int, 2>;
+        using S3 = std::integral_constant<int, 3>;
         read_a(t, 1, 1);
         dma_part(t + NS - 1, 0);
-        mma(0, bpar, 0, step_scales(0));
+        mma(0, bpar, S0{}, sa_pk, sb_pk);
         prefetch_b(t, bpar, 0);
         pace(NB + DMA_PART);
         fence();
         read_a(t, 2, 0);
         dma_part(t + NS - 1, 1);
-        mma(1, bpar, 1, step_scales(1));
+        mma(1, bpar, S1{}, sa_pk, sb_pk);
         prefetch_b(t, bpar, 1);
         pace(NB + DMA_PART);
         fence();
         read_a(t, 3, 1);
         dma_part(t + NS - 1, 2);
-        mma(0, bpar, 2, step_scales(2));
+        mma(0, bpar, S2{}, sa_pk, sb_pk);
         prefetch_b(t, bpar, 2);
         pace(NB + NDMA - 2 * DMA_PART);
-        const StepScales sc3 = step_scales(3);
         fence();
         // stage t+1 published: own copies landed and own LDS reads of stage t
         // done (waitcnt), then everyone's (barrier).  No workgroup memory fence:
@@ -262,9 +264,14 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
         asm volatile("" ::: "memory");
         fence();
         read_a(t + 1, 0, 0);
-        read_scales(t + 1);
-        mma(1, bpar, 3, sc3);
+        int na[MA], nb[NB];
+        read_scales(t + 1, na, nb);
+        mma(1, bpar, S3{}, sa_pk, sb_pk);
         prefetch_b(t, bpar, 3);
+#pragma unroll
+        for (int i = 0; i < MA; ++i) sa_pk[i] = na[i];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) sb_pk[j] = nb[j];
         pace(NB);
         fence();
     };
@@ -288,7 +295,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    read_scales(0);
+    read_scales(0, sa_pk, sb_pk);
     read_a(0, 0, 0);
 
     // the loop runs an even number of stages; an odd last stage is a zero stage
@@ -302,7 +309,10 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     static_assert(BM * BN * 2 <= NS * STAGE_BYTES, "epilogue fits the ring");
     wait_vmcnt<0>();
     __syncthreads();
-    store_block_bf16<MA, NB>(p, acc, smem + wave * (BM * 128), lane, m0, n0 + wave * 64);
+    if (p.bias)
+        store_block_bf16<MA, NB, MA, true>(p, acc, smem + wave * (BM * 128), lane, m0, n0 + wave * 64);
+    else
+        store_block_bf16<MA, NB, MA, false>(p, acc, smem + wave * (BM * 128), lane, m0, n0 + wave * 64);
 }
 
 }  // namespace aiter_amd

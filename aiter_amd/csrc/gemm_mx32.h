@@ -77,47 +77,62 @@ AA_DEV void wait_vmcnt_lgkm0() {
 // (lane l holds C[m = l%32][n = 8q + 4(l/32) + r] of each tile) written as
 // bf16, D = alpha*acc + beta*bias.  Stored directly, each global store would
 // touch 32 rows; instead the block goes through the wave's own LDS scratch
-// `cb` (32*MA * 64*NB bytes), 16-byte pieces XOR-swizzled by row so that both
-// the 8-byte writes and the 16-byte reads spread over the banks, and leaves as
-// whole rows of 64*NB bytes.  (mb, nb) is the block's global origin.
-template <int MA, int NB>
+// `cb`, MP row tiles (32*MP rows x 64*NB bytes) per pass, 16-byte pieces
+// XOR-swizzled by row so that both the 8-byte writes and the 16-byte reads
+// spread over the banks, and leaves as whole rows of 64*NB bytes.  (mb, nb)
+// is the block's global origin.  Branch-free: stores go through a
+// range-checked descriptor of D (rows >= M fall outside it, columns >= N get
+// an offset outside it) and bias reads are clamped into the bias tensor.
+template <int MA, int NB, int MP, bool HAS_BIAS>
 AA_DEV void store_block_bf16(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb,
                              int nb) {
+    static_assert(MA % MP == 0, "whole passes");
     constexpr int RB = 64 * NB;                 // bytes per block row
     constexpr int P = RB / 16;                  // 16-byte pieces per row
     constexpr int SWM = (P < 8 ? P : 8) - 1;    // swizzle mask
     constexpr int RSH = RB < 128 ? 1 : 0;       // two 64-byte rows share a 128-byte bank line
-    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
-#pragma unroll
-    for (int i = 0; i < MA; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int r = i * 32 + (lane & 31);
-                const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
-                float v[4] = {acc[i][j][4 * q] * p.alpha, acc[i][j][4 * q + 1] * p.alpha,
-                              acc[i][j][4 * q + 2] * p.alpha, acc[i][j][4 * q + 3] * p.alpha};
-                if (p.bias) {
-                    const int m = min(mb + r, p.M - 1), n = min(nb + nl, p.N - 4);
-                    const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
-                }
-                const int piece = (nl >> 3) ^ ((r >> RSH) & SWM);
-                *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (nl & 7) * 2) =
-                    u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            }
-    // the block is the wave's own: its LDS accesses complete in order
     constexpr int ROWS_PER = 64 / P;            // rows per read instruction
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    // opaque copy of the lane index: keeps the compiler from hoisting this
+    // epilogue's address arithmetic out of an enclosing tile loop (where it
+    // would stay live, in registers, across the whole main loop)
+    asm volatile("" : "+v"(lane));
+    const __amdgpu_buffer_rsrc_t d_rsrc = make_rsrc(p.D, (int64_t)p.M * p.ldd * 2);
     const int pc = lane % P;
     const int n_out = nb + pc * 8;
-#pragma unroll 4
-    for (int rr = 0; rr < 32 * MA; rr += ROWS_PER) {
-        const int r = rr + lane / P;
-        const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
-        if (mb + r < p.M && n_out < p.N)
-            *reinterpret_cast<i32x4_t*>(static_cast<uint16_t*>(p.D) + (int64_t)(mb + r) * p.ldd + n_out) = v;
+    const int col_off = n_out < p.N ? n_out * 2 : 0x7fffffff;   // outside D when past N
+#pragma unroll
+    for (int i0 = 0; i0 < MA; i0 += MP) {
+#pragma unroll
+        for (int i = 0; i < MP; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = i * 32 + (lane & 31);
+                    const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
+                    const f32x16v_t& a = acc[i0 + i][j];
+                    float v[4] = {a[4 * q] * p.alpha, a[4 * q + 1] * p.alpha, a[4 * q + 2] * p.alpha,
+                                  a[4 * q + 3] * p.alpha};
+                    if constexpr (HAS_BIAS) {
+                        const int m = min(mb + i0 * 32 + r, p.M - 1), n = min(nb + nl, p.N - 4);
+                        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
+                    }
+                    const int piece = (nl >> 3) ^ ((r >> RSH) & SWM);
+                    *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (nl & 7) * 2) =
+                        u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                }
+        // the scratch is the wave's own: its LDS accesses complete in order
+#pragma unroll
+        for (int rr = 0; rr < 32 * MP; rr += ROWS_PER) {
+            const int r = rr + lane / P;
+            const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
+            const int m = mb + i0 * 32 + r;
+            const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * 2 + col_off;
+            __builtin_amdgcn_raw_buffer_store_b128(v, d_rsrc, off, 0, 0);
+        }
     }
 }
 
@@ -349,7 +364,10 @@ __global__ __launch_bounds__(256, 1) void gemm_mx32_kernel(GemmParams p) {
     static_assert(BM * BN * 2 <= NS * STAGE_BYTES, "epilogue fits the ring");
     wait_vmcnt<0>();
     __syncthreads();
-    store_block_bf16<MA, NB>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
+    if (p.bias)
+        store_block_bf16<MA, NB, MA, true>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
+    else
+        store_block_bf16<MA, NB, MA, false>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
 }
 
 }  // namespace aiter_amd

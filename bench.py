@@ -4,9 +4,12 @@
 Headline (``value``): MXFP4 x MXFP4 (A4W4) GEMM at M=N=K=8192 (BASELINE.json
 configs[2]) in TFLOP/s: A, B drawn N(0,1) from a seed, quantised per 1x32 to
 MXFP4 (e2m1 + e8m0, Even rounding as the reference test/tuner), B
-preshuffled, bf16 output.  One step = one ``gemm_a4w4`` call on inputs
-resident in HBM.  The K timed steps are captured in a HIP graph and replayed
-once between two synchronisations (launch overhead is not part of a step).
+preshuffled, bf16 output.  One step = one ``gemm_a4w4_asm`` call (the entry
+``gemm_a4w4`` dispatches to) on inputs resident in HBM, into a preallocated
+output.  The K timed steps are captured in a HIP graph and replayed once
+between two synchronisations (launch overhead is not part of a step), after
+W warm-up steps replayed through the same graph for at least one second
+(the clocks ramp up under load).
 
 Also reported on the same JSON line:
 * ``decode``: the bandwidth-bound configs[1] (M in {1,8,16,32,64}, N=7168,
@@ -58,24 +61,31 @@ def quantised_operands(m, n, k, seed, dev):
     return aq, as_, aiter_amd.shuffle_weight(bq), bs
 
 
-def time_graph(fn, steps, warmup):
-    """Capture `steps` calls of fn() in a HIP graph, replay once, return the
-    average seconds per call measured by HIP events on the launch stream."""
-    for _ in range(warmup):
-        fn()
+def time_graph(fn, steps, warmup, min_warm_s=0.3):
+    """Capture `steps` calls of fn() in a HIP graph and time one replay with
+    HIP events on the launch stream; returns seconds per call.
+
+    Warm-up: `warmup` calls, replayed through the same graph (whole replays,
+    at least one), continued until `min_warm_s` of GPU work has run.  MI355X
+    raises its clocks over the first few hundred milliseconds of load, so a
+    cold measurement reads up to 20% slow."""
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        fn()  # one eager call on the capture stream (lazy state)
+        fn()  # one eager call on the capture stream (lazy state, workspaces)
         s.synchronize()
         with torch.cuda.graph(g, stream=s):
             for _ in range(steps):
                 fn()
     torch.cuda.synchronize()
-    g.replay()  # warm replay
-    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    done = 0
+    while done < max(warmup, 1) or time.perf_counter() - t0 < min_warm_s:
+        g.replay()
+        done += steps
+        torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(s):
@@ -102,7 +112,7 @@ def bench_prefill(steps, warmup, dev):
     def step():
         aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
 
-    sec = time_graph(step, steps, warmup)
+    sec = time_graph(step, steps, warmup, min_warm_s=1.0)
     flop = 2.0 * m * n * k
     return sec, flop / sec / 1e12
 
@@ -253,8 +263,8 @@ def traffic_from_profiles():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--pmc", action="store_true",

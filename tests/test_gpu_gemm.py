@@ -308,3 +308,22 @@ def test_tile_instances_odd_stage_counts(cuda, m, n, k):
                 torch.cuda.synchronize()
                 ok, msg = allclose_report(_bf16_np(out[:m]), ref)
                 assert ok, f"{name}: {msg}"
+
+
+@pytest.mark.parametrize("m,n,k", [(8192, 2048, 512), (2048, 8192, 512), (4608, 4096, 256)])
+def test_tile_instances_more_tiles_than_cus(cuda, m, n, k):
+    """Every A4W4 tile instance on grids of 512-2304 tiles (more tiles than
+    CUs, and tile counts that are multiples of the 8 XCDs, which turns on the
+    XCD-aware tile order): every tile must be written."""
+    import aiter_amd
+
+    a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=21)
+    b_dev = _dev(O.shuffle_weight(b_q), cuda)
+    for row in _kernels("a4w4", skinny=False):
+        name = row[1]
+        announce(f"a4w4 tile {name} {m}x{n}x{k} (many tiles)")
+        out = torch.zeros(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
+        aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), b_dev, _dev(a_ss, cuda), _dev(b_ss, cuda), out, kernelName=name)
+        torch.cuda.synchronize()
+        ok, msg = allclose_report(_bf16_np(out[:m]), ref)
+        assert ok, f"{name}: {msg}"
