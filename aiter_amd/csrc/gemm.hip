@@ -18,6 +18,7 @@
 #include "gemm_kernels.h"
 #include "gemm_mx32.h"
 #include "gemm_flat.h"
+#include "gemm_t32.h"
 
 namespace aiter_amd {
 
@@ -71,9 +72,14 @@ void launch_mx32(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_mx32_kernel<KA, BM, BN, WMW, false><<<grid, 256, 0, s>>>(p);
 }
 
-template <int KA, int BM>
+template <int KA, int BM, bool OF = false>
 void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_flat_kernel<KA, BM, false><<<grid, 256, 0, s>>>(p);
+    gemm_flat_kernel<KA, BM, OF><<<grid, 256, 0, s>>>(p);
+}
+
+template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false>
+void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
+    gemm_t32_kernel<KA, BP, BM, BN, WMW, OF><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, int MF, bool BP, bool SPLIT, bool OF>
@@ -106,11 +112,11 @@ std::vector<Instance>& registry() {
         // A and B through LDS (gemm_mx32.h) ----
         const Variant pre{false, true, false}, plain{false, false, false};
         tile(kA4W4, 256, 256, pre, launch_flat<kFp4, 256>, "a4w4");
-        tile(kA4W4, 256, 128, pre, launch_mx32<kFp4, 256, 128, 2>, "a4w4");
+        tile(kA4W4, 256, 128, pre, launch_t32<kFp4, true, 256, 128, 2>, "a4w4");
         tile(kA4W4, 128, 256, pre, launch_flat<kFp4, 128>, "a4w4");
-        tile(kA4W4, 128, 128, pre, launch_mx32<kFp4, 128, 128, 2>, "a4w4");
-        tile(kA4W4, 64, 256, pre, launch_mx32<kFp4, 64, 256, 1>, "a4w4");
-        tile(kA4W4, 64, 128, pre, launch_mx32<kFp4, 64, 128, 1>, "a4w4");
+        tile(kA4W4, 128, 128, pre, launch_t32<kFp4, true, 128, 128, 2>, "a4w4");
+        tile(kA4W4, 64, 256, pre, launch_t32<kFp4, true, 64, 256, 1>, "a4w4");
+        tile(kA4W4, 64, 128, pre, launch_t32<kFp4, true, 64, 128, 1>, "a4w4");
         skinny(kA4W4, 1, false, pre, launch_skinny<kFp4, 1, true, false, false>, "a4w4");
         skinny(kA4W4, 2, false, pre, launch_skinny<kFp4, 2, true, false, false>, "a4w4");
         skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false>, "a4w4");
@@ -118,17 +124,17 @@ std::vector<Instance>& registry() {
         skinny(kA4W4, 2, true, pre, launch_skinny<kFp4, 2, true, true, false>, "a4w4");
         skinny(kA4W4, 4, true, pre, launch_skinny<kFp4, 4, true, true, false>, "a4w4");
         // a4w4 with row-major B (bpreshuffle = 0)
-        tile(kA4W4, 128, 128, plain, launch_tile<kFp4, kFp4, 128, 128, false, false, false>, "a4w4");
-        tile(kA4W4, 64, 128, plain, launch_tile<kFp4, kFp4, 64, 128, false, false, false>, "a4w4");
+        tile(kA4W4, 128, 128, plain, launch_t32<kFp4, false, 128, 128, 2>, "a4w4");
+        tile(kA4W4, 64, 128, plain, launch_t32<kFp4, false, 64, 128, 1>, "a4w4");
         skinny(kA4W4, 1, false, plain, launch_skinny<kFp4, 1, false, false, false>, "a4w4");
         skinny(kA4W4, 2, false, plain, launch_skinny<kFp4, 2, false, false, false>, "a4w4");
         skinny(kA4W4, 4, false, plain, launch_skinny<kFp4, 4, false, false, false>, "a4w4");
         // ---- a8w4 ----
         const Variant a8{false, true, false}, a8p{true, true, false};
         tile(kA8W4, 128, 256, a8, launch_flat<kFp8, 128>, "a8w4");
-        tile(kA8W4, 128, 128, a8, launch_mx32<kFp8, 128, 128, 2>, "a8w4");
-        tile(kA8W4, 64, 256, a8, launch_mx32<kFp8, 64, 256, 1>, "a8w4");
-        tile(kA8W4, 64, 128, a8, launch_mx32<kFp8, 64, 128, 1>, "a8w4");
+        tile(kA8W4, 128, 128, a8, launch_t32<kFp8, true, 128, 128, 2>, "a8w4");
+        tile(kA8W4, 64, 256, a8, launch_t32<kFp8, true, 64, 256, 1>, "a8w4");
+        tile(kA8W4, 64, 128, a8, launch_t32<kFp8, true, 64, 128, 1>, "a8w4");
         tile(kA8W4, 128, 256, a8p, launch_tile<kFp8, kFp4, 128, 256, true, true, false>, "a8w4");
         tile(kA8W4, 128, 128, a8p, launch_tile<kFp8, kFp4, 128, 128, true, true, false>, "a8w4");
         tile(kA8W4, 64, 128, a8p, launch_tile<kFp8, kFp4, 64, 128, true, true, false>, "a8w4");
@@ -142,15 +148,18 @@ std::vector<Instance>& registry() {
         for (int of = 0; of < 2; ++of) {
             for (int bp = 0; bp < 2; ++bp) {
                 const Variant v{false, bp != 0, of != 0};
-#define AA_T16(BM, BN)                                                                     \
+// bf16 tiles: the 256-wide preshuffled ones read B straight into registers
+#define AA_T16(BM, BN, WMW)                                                                \
     tile(kA16W16, BM, BN, v,                                                               \
-         of ? (bp ? launch_tile<kBf16, kBf16, BM, BN, false, true, true>                   \
-                  : launch_tile<kBf16, kBf16, BM, BN, false, false, true>)                 \
-            : (bp ? launch_tile<kBf16, kBf16, BM, BN, false, true, false>                  \
-                  : launch_tile<kBf16, kBf16, BM, BN, false, false, false>),               \
+         of ? (bp ? ((BN == 256 && BM >= 128) ? launch_flat<kBf16, (BM >= 128 ? BM : 128), true>  \
+                                              : launch_t32<kBf16, true, BM, BN, WMW, true>)       \
+                  : launch_t32<kBf16, false, BM, BN, WMW, true>)                                  \
+            : (bp ? ((BN == 256 && BM >= 128) ? launch_flat<kBf16, (BM >= 128 ? BM : 128), false> \
+                                              : launch_t32<kBf16, true, BM, BN, WMW, false>)      \
+                  : launch_t32<kBf16, false, BM, BN, WMW, false>),                                \
          "a16w16");
-                AA_T16(256, 256) AA_T16(256, 128) AA_T16(128, 256) AA_T16(128, 128)
-                AA_T16(64, 128) AA_T16(64, 64)
+                AA_T16(256, 256, 2) AA_T16(256, 128, 2) AA_T16(128, 256, 2) AA_T16(128, 128, 2)
+                AA_T16(64, 128, 1) AA_T16(64, 64, 2)
 #undef AA_T16
 #define AA_S16(MF, SP)                                                                     \
     skinny(kA16W16, MF, SP, v,                                                             \
@@ -197,8 +206,8 @@ int skinny_splits(int n_blocks, int k_steps, int cus) {
 const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int cus, int* splits) {
     *splits = 1;
     const int ksteps = K / (f == kA16W16 ? 32 : 128);
-    if (M <= 64) {
-        const int mf = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+    if (M <= 32) {
+        const int mf = M <= 16 ? 1 : 2;
         const int nblk = (N + 15) / 16;
         const int s = skinny_splits(nblk, ksteps, cus);
         for (auto& in : registry())

@@ -1,5 +1,8 @@
-// MX tile kernel with B read straight into registers ("flat" B), for tiles
-// 256 columns wide.  v_mfma_scale_f32_32x32x64_f8f6f4 on gfx950.
+// Tile kernel with B read straight into registers ("flat" B), for tiles 256
+// columns wide: MX (v_mfma_scale_f32_32x32x64_f8f6f4, e8m0 scales) and bf16
+// (v_mfma_f32_32x32x16_bf16).  In bytes both have the same operand layout and
+// the same preshuffled-B layout, so a stage is 128 bytes of every row either
+// way (256 MX or 64 bf16 elements); bf16 simply has no scales.
 //
 // Why: aiter's preshuffled B (shuffle_weight (16,16)) stores every 16-row
 // block so that one 16-byte load per lane is exactly the B operand of one
@@ -34,10 +37,12 @@ namespace aiter_amd {
 
 template <int KA, int BM>
 struct FlatCfg {
+    static constexpr bool MX = KA != kBf16;
     static constexpr int FA = (KA == kFp8) ? 2 : 1;   // 128-byte halves of an A row per stage
     static constexpr int A_CH = (BM / 8) * FA;        // A chunks per stage
-    static constexpr int STAGE_KB = A_CH + 4;         // + 4 scale chunks
+    static constexpr int STAGE_KB = A_CH + (MX ? 4 : 0);   // + 4 scale chunks (MX)
     static constexpr int NS = (160 / STAGE_KB) > 4 ? 4 : (160 / STAGE_KB);
+    static constexpr int K_STAGE = MX ? 256 : 64;     // K elements per stage (128 bytes of a row)
 };
 
 template <int KA, int BM, bool OUT_F32>
@@ -49,13 +54,14 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     constexpr int MA = BM / 32;           // 32-row A tiles per wave (all rows of the tile)
     constexpr int NB = 2;                 // 32-column B tiles per wave
     constexpr int A_CH = Cfg::A_CH;
+    constexpr bool MX = Cfg::MX;
     constexpr int AG = BM / 32;           // A scale groups in the tile
     constexpr int SCA = (AG + 3) / 4;     // A scale chunks
     static_assert(SCA + 2 <= 4, "scale chunks: one per wave");
     static_assert(NS >= 2, "two LDS stages minimum");
     static_assert(A_CH % 4 == 0, "A chunks split over 4 waves");
     constexpr int NA = A_CH / 4;          // A DMAs per wave per stage
-    constexpr int NDMA = NA + 1;          // + one scale chunk
+    constexpr int NDMA = NA + (MX ? 1 : 0);   // + one scale chunk (MX)
     constexpr int NBL = NB * 4;           // B loads per wave per stage
     constexpr int STAGE_BYTES = Cfg::STAGE_KB * 1024;
     constexpr int A_ROW_BYTES = 128 * FA;
@@ -68,7 +74,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int nstages = p.K / 256;
+    const int nstages = p.K / Cfg::K_STAGE;
 
     // ---- A: chunk c = half*(BM/8) + 8-row block; lane l -> row l/8, stored piece l%8
     //      holding global 16-byte piece (l%8) ^ swz(row), swz(r) = (r>>1)&7
@@ -110,7 +116,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
         uint8_t* base = smem + (t % NS) * STAGE_BYTES;
 #pragma unroll
         for (int q = 0; q < NA; ++q) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], t * A_ROW_BYTES);
-        dma16(rs, base + (A_CH + wave) * 1024, sc_off, t * 256);
+        if constexpr (MX) dma16(rs, base + (A_CH + wave) * 1024, sc_off, t * 256);
     };
     auto load_b = [&](int t, int j, int s) -> i32x4_t {
         const __amdgpu_buffer_rsrc_t rb = t < nstages ? b_rsrc : null_rsrc;
@@ -132,7 +138,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
 
     i32x4_t af[2][MA][FA];
     i32x4_t bq[2][NB][4];          // [stage parity][tile][k-step]
-    int sa_pk[MA], sb_pk[NB];      // packed scale bytes of the stage being multiplied
+    int sa_pk[MA] = {}, sb_pk[NB] = {};   // packed scale bytes of the stage being multiplied
 
     const int ar = lane & 31;
     const int a_lane_off = (ar >> 3) * 1024 + (ar & 7) * 128;
@@ -150,6 +156,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
             }
     };
     auto read_scales = [&](int t, int (&pa)[MA], int (&pb)[NB]) {
+        if constexpr (!MX) return;
         const uint8_t* base = smem + (t % NS) * STAGE_BYTES + A_CH * 1024 + pos0;
 #pragma unroll
         for (int i = 0; i < MA; ++i) {
@@ -172,22 +179,9 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < MA; ++i)
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                i32x8_t bv, av;
-                bv[0] = bq[bpar][j][s][0]; bv[1] = bq[bpar][j][s][1];
-                bv[2] = bq[bpar][j][s][2]; bv[3] = bq[bpar][j][s][3];
-                bv[4] = 0; bv[5] = 0; bv[6] = 0; bv[7] = 0;
-                av[0] = af[aslot][i][0][0]; av[1] = af[aslot][i][0][1];
-                av[2] = af[aslot][i][0][2]; av[3] = af[aslot][i][0][3];
-                if constexpr (FA == 2) {
-                    av[4] = af[aslot][i][1][0]; av[5] = af[aslot][i][1][1];
-                    av[6] = af[aslot][i][1][2]; av[7] = af[aslot][i][1][3];
-                } else {
-                    av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
-                }
-                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, acc[i][j], 4,
-                                                                            OpTraits<KA>::fmt, osel, pb[j], osel, pa[i]);
-            }
+            for (int j = 0; j < NB; ++j)
+                acc[i][j] = mma32<KA, osel>(bq[bpar][j][s], af[aslot][i][0], af[aslot][i][FA - 1], acc[i][j], pa[i],
+                                            pb[j]);
     };
     // B of stage t+2, k-step s, into the registers k-step s of stage t just used
     auto prefetch_b = [&](int t, int bpar, int s) {
@@ -268,10 +262,12 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
         read_scales(t + 1, na, nb);
         mma(1, bpar, S3{}, sa_pk, sb_pk);
         prefetch_b(t, bpar, 3);
+        if constexpr (MX) {
 #pragma unroll
-        for (int i = 0; i < MA; ++i) sa_pk[i] = na[i];
+            for (int i = 0; i < MA; ++i) sa_pk[i] = na[i];
 #pragma unroll
-        for (int j = 0; j < NB; ++j) sb_pk[j] = nb[j];
+            for (int j = 0; j < NB; ++j) sb_pk[j] = nb[j];
+        }
         pace(NB);
         fence();
     };
@@ -305,14 +301,13 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     }
 
     // ---- epilogue through LDS (the ring is free once every copy has landed)
-    static_assert(!OUT_F32, "the flat kernel writes bf16");
-    static_assert(BM * BN * 2 <= NS * STAGE_BYTES, "epilogue fits the ring");
+    constexpr int EB = OUT_F32 ? 4 : 2;
+    constexpr int WAVE_SCRATCH = NS * STAGE_BYTES / 4;
+    constexpr int EP_MP = (MA * 32 * 64 * EB <= WAVE_SCRATCH) ? MA : MA / 2;
+    static_assert(MA % EP_MP == 0 && EP_MP * 32 * 64 * EB <= WAVE_SCRATCH, "epilogue pass fits the ring");
     wait_vmcnt<0>();
     __syncthreads();
-    if (p.bias)
-        store_block_bf16<MA, NB, MA, true>(p, acc, smem + wave * (BM * 128), lane, m0, n0 + wave * 64);
-    else
-        store_block_bf16<MA, NB, MA, false>(p, acc, smem + wave * (BM * 128), lane, m0, n0 + wave * 64);
+    store_block_any<MA, NB, EP_MP, OUT_F32>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0, n0 + wave * 64);
 }
 
 }  // namespace aiter_amd

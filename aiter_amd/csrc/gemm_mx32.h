@@ -73,34 +73,58 @@ AA_DEV void wait_vmcnt_lgkm0() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
 }
 
+// One k-step of a 32x32 MFMA tile: src0 = B fragment (16 bytes per lane),
+// src1 = A fragment(s) (two 16-byte halves for e4m3), packed scale bytes with
+// op_sel OSEL for the MX kinds.  Result lane l holds C[m = l%32][n = 8q + 4(l/32) + r].
+template <int KA, int OSEL>
+AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f32x16v_t c, int sa, int sb) {
+    if constexpr (KA == kBf16) {
+        typedef __bf16 bf16x8v_t __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v_t, b), __builtin_bit_cast(bf16x8v_t, a0),
+                                                       c, 0, 0, 0);
+    } else {
+        i32x8_t bv, av;
+        bv[0] = b[0]; bv[1] = b[1]; bv[2] = b[2]; bv[3] = b[3];
+        bv[4] = 0; bv[5] = 0; bv[6] = 0; bv[7] = 0;
+        av[0] = a0[0]; av[1] = a0[1]; av[2] = a0[2]; av[3] = a0[3];
+        if constexpr (KA == kFp8) {
+            av[4] = a1[0]; av[5] = a1[1]; av[6] = a1[2]; av[7] = a1[3];
+        } else {
+            av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
+        }
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, c, 4, OpTraits<KA>::fmt, OSEL, sb, OSEL, sa);
+    }
+}
+
 // Epilogue of a wave's (32*MA) x (32*NB) block of 32x32 MFMA accumulators
 // (lane l holds C[m = l%32][n = 8q + 4(l/32) + r] of each tile) written as
-// bf16, D = alpha*acc + beta*bias.  Stored directly, each global store would
-// touch 32 rows; instead the block goes through the wave's own LDS scratch
-// `cb`, MP row tiles (32*MP rows x 64*NB bytes) per pass, 16-byte pieces
-// XOR-swizzled by row so that both the 8-byte writes and the 16-byte reads
-// spread over the banks, and leaves as whole rows of 64*NB bytes.  (mb, nb)
-// is the block's global origin.  Branch-free: stores go through a
-// range-checked descriptor of D (rows >= M fall outside it, columns >= N get
-// an offset outside it) and bias reads are clamped into the bias tensor.
-template <int MA, int NB, int MP, bool HAS_BIAS>
-AA_DEV void store_block_bf16(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb,
-                             int nb) {
+// bf16 or f32, D = alpha*acc + beta*bias.  Stored directly, each global store
+// would touch 32 rows; instead the block goes through the wave's own LDS
+// scratch `cb`, MP row tiles (32*MP rows x 32*NB elements) per pass, 16-byte
+// pieces XOR-swizzled by row so that both the writes and the 16-byte reads
+// spread over the banks, and leaves as whole rows.  (mb, nb) is the block's
+// global origin.  Branch-free: stores go through a range-checked descriptor
+// of D (rows >= M fall outside it, columns >= N get an offset outside it) and
+// bias reads are clamped into the bias tensor.  SCALED = false skips the
+// alpha multiply (alpha == 1, no bias).
+template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false>
+AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     static_assert(MA % MP == 0, "whole passes");
-    constexpr int RB = 64 * NB;                 // bytes per block row
+    constexpr int EB = OUT_F32 ? 4 : 2;         // output bytes per element
+    constexpr int RB = 32 * NB * EB;            // bytes per block row
     constexpr int P = RB / 16;                  // 16-byte pieces per row
+    static_assert(P <= 64, "one row per read instruction at most");
     constexpr int SWM = (P < 8 ? P : 8) - 1;    // swizzle mask
     constexpr int RSH = RB < 128 ? 1 : 0;       // two 64-byte rows share a 128-byte bank line
     constexpr int ROWS_PER = 64 / P;            // rows per read instruction
     typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
     // opaque copy of the lane index: keeps the compiler from hoisting this
-    // epilogue's address arithmetic out of an enclosing tile loop (where it
-    // would stay live, in registers, across the whole main loop)
+    // epilogue's address arithmetic out of an enclosing loop
     asm volatile("" : "+v"(lane));
-    const __amdgpu_buffer_rsrc_t d_rsrc = make_rsrc(p.D, (int64_t)p.M * p.ldd * 2);
+    const __amdgpu_buffer_rsrc_t d_rsrc = make_rsrc(p.D, (int64_t)p.M * p.ldd * EB);
     const int pc = lane % P;
-    const int n_out = nb + pc * 8;
-    const int col_off = n_out < p.N ? n_out * 2 : 0x7fffffff;   // outside D when past N
+    const int n_out = nb + pc * (16 / EB);
+    const int col_off = n_out < p.N ? n_out * EB : 0x7fffffff;   // outside D when past N
 #pragma unroll
     for (int i0 = 0; i0 < MA; i0 += MP) {
 #pragma unroll
@@ -112,17 +136,25 @@ AA_DEV void store_block_bf16(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint
                     const int r = i * 32 + (lane & 31);
                     const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
                     const f32x16v_t& a = acc[i0 + i][j];
-                    float v[4] = {a[4 * q] * p.alpha, a[4 * q + 1] * p.alpha, a[4 * q + 2] * p.alpha,
-                                  a[4 * q + 3] * p.alpha};
+                    float v[4] = {a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                    if constexpr (SCALED) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] *= p.alpha;
+                    }
                     if constexpr (HAS_BIAS) {
                         const int m = min(mb + i0 * 32 + r, p.M - 1), n = min(nb + nl, p.N - 4);
                         const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
                     }
-                    const int piece = (nl >> 3) ^ ((r >> RSH) & SWM);
-                    *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (nl & 7) * 2) =
-                        u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    const int byte = nl * EB;
+                    const int piece = (byte >> 4) ^ ((r >> RSH) & SWM);
+                    if constexpr (OUT_F32) {
+                        *reinterpret_cast<f32x4_t*>(cb + r * RB + piece * 16) = f32x4_t{v[0], v[1], v[2], v[3]};
+                    } else {
+                        *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (byte & 15)) =
+                            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    }
                 }
         // the scratch is the wave's own: its LDS accesses complete in order
 #pragma unroll
@@ -130,10 +162,21 @@ AA_DEV void store_block_bf16(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint
             const int r = rr + lane / P;
             const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
             const int m = mb + i0 * 32 + r;
-            const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * 2 + col_off;
+            const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * EB + col_off;
             __builtin_amdgcn_raw_buffer_store_b128(v, d_rsrc, off, 0, 0);
         }
     }
+}
+
+// the three epilogue flavours picked at run time (uniform branch)
+template <int MA, int NB, int MP, bool OUT_F32>
+AA_DEV void store_block_any(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
+    if (p.bias)
+        store_block<MA, NB, MP, true, true, OUT_F32>(p, acc, cb, lane, mb, nb);
+    else if (p.alpha != 1.0f)
+        store_block<MA, NB, MP, false, true, OUT_F32>(p, acc, cb, lane, mb, nb);
+    else
+        store_block<MA, NB, MP, false, false, OUT_F32>(p, acc, cb, lane, mb, nb);
 }
 
 // LDS ring depth that fits 160 KiB for a tile
@@ -364,10 +407,7 @@ __global__ __launch_bounds__(256, 1) void gemm_mx32_kernel(GemmParams p) {
     static_assert(BM * BN * 2 <= NS * STAGE_BYTES, "epilogue fits the ring");
     wait_vmcnt<0>();
     __syncthreads();
-    if (p.bias)
-        store_block_bf16<MA, NB, MA, true>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
-    else
-        store_block_bf16<MA, NB, MA, false>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
+    store_block_any<MA, NB, MA, false>(p, acc, smem + wave * (WM * WN * 2), lane, m0 + wm * WM, n0 + wn * WN);
 }
 
 }  // namespace aiter_amd

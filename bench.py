@@ -136,20 +136,26 @@ def bench_decode(dev, steps=50):
         out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=dev)
         it = {"i": 0}
 
+        # the kernel gemm_a4w4 dispatches to (tuned table, else the heuristic),
+        # called on a preallocated output
+        cfg = aiter_amd.get_GEMM_config(m, n, k)
+        kname = str(cfg["kernelName"]) if cfg else ""
+        l2 = int(cfg.get("splitK", 0) or 0) if cfg else 0
+
         def cold():
             i = it["i"] % copies
             it["i"] += 1
-            aiter_amd.gemm_a4w4_asm(aq, bqs[i], as_, bss[i], out)
+            aiter_amd.gemm_a4w4_asm(aq, bqs[i], as_, bss[i], out, kernelName=kname, log2_k_split=l2)
 
         def warm():
-            aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
+            aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out, kernelName=kname, log2_k_split=l2)
 
         t_cold = time_graph(cold, min(steps, copies), 3)
         t_warm = time_graph(warm, steps, 3)
         byts = a4w4_bytes(m, n, k)
         ref_bw = (m * k / 2 + n * k / 2 + 2 * m * n)  # reference `bw` formula (scales excluded)
         res.append({
-            "M": m, "N": n, "K": k,
+            "M": m, "N": n, "K": k, "kernel": kname or "heuristic",
             "us_cold": round(t_cold * 1e6, 3), "us_warm": round(t_warm * 1e6, 3),
             "GBps_cold": round(byts / t_cold / 1e9, 1), "GBps_warm": round(byts / t_warm / 1e9, 1),
             "hbm_frac_cold": round(byts / t_cold / 1e9 / PEAK_HBM, 4),
