@@ -16,7 +16,7 @@
 #include <vector>
 
 #include "gemm_kernels.h"
-#include "gemm_mx32.h"
+#include "mfma32.h"
 #include "gemm_flat.h"
 #include "gemm_t32.h"
 
@@ -67,10 +67,6 @@ void launch_tile(const GemmParams& p, dim3 grid, hipStream_t s) {
 
 constexpr int kSkinnyWaves = 8;
 
-template <int KA, int BM, int BN, int WMW>
-void launch_mx32(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_mx32_kernel<KA, BM, BN, WMW, false><<<grid, 256, 0, s>>>(p);
-}
 
 template <int KA, int BM, bool OF = false>
 void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
@@ -109,7 +105,7 @@ std::vector<Instance>& registry() {
         };
         // ---- a4w4 (B preshuffled): 32x32x64 tile kernels; the 256-column
         // tiles read B straight into registers (gemm_flat.h), the others stage
-        // A and B through LDS (gemm_mx32.h) ----
+        // A and B through LDS (gemm_t32.h) ----
         const Variant pre{false, true, false}, plain{false, false, false};
         tile(kA4W4, 256, 256, pre, launch_flat<kFp4, 256>, "a4w4");
         tile(kA4W4, 256, 128, pre, launch_t32<kFp4, true, 256, 128, 2>, "a4w4");

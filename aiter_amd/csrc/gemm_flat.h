@@ -31,7 +31,7 @@
 #pragma once
 #include <type_traits>
 
-#include "gemm_mx32.h"
+#include "mfma32.h"
 
 namespace aiter_amd {
 

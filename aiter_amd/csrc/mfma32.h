@@ -1,0 +1,156 @@
+// Shared pieces of the gfx950 32x32 MFMA tile kernels (gemm_flat.h,
+// gemm_t32.h): the k-step MFMA wrapper for e2m1 / e4m3 (scaled, e8m0) and
+// bf16, buffer descriptors with hardware range checks, global -> LDS copies,
+// explicit wait counters and the LDS-staged epilogue.
+//
+// Measured on MI355X: v_mfma_scale_f32_32x32x64_f8f6f4 issues once per 32
+// cycles for e2m1 x e2m1 (twice the e2m1 rate of the 16x16x128 form) and once
+// per 64 cycles with an e4m3 operand; v_mfma_f32_32x32x16_bf16 once per 32.
+// Operand layout (bytes are the same for all three): lane l holds row l%32
+// and bytes [16*(l/32), +16) of a 32-byte K window (e4m3: also the same 16
+// bytes of the following window); result lane l holds
+// C[src1 row = l%32][src0 row = 8q + 4(l/32) + r], r < 4, q < 4.  Scales: lane
+// l supplies the e8m0 byte of (row l%32, block 2s + l/32) for k-step s of a
+// 256-element window, selected from a 32-bit register by op_sel (byte 0..3).
+#pragma once
+#include "gemm_kernels.h"
+
+namespace aiter_amd {
+
+typedef float f32x16v_t __attribute__((ext_vector_type(16)));
+#define AA_LDS __attribute__((address_space(3)))
+
+
+AA_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+    // raw buffer, dword format; loads at offsets >= bytes return 0
+    const int n = (int)(bytes > 0x7ffffff0LL ? 0x7ffffff0LL : (bytes < 0 ? 0 : bytes));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, n, 0x00020000);
+}
+
+// global -> LDS copy of one 1 KiB chunk (16 bytes per lane, lane order)
+AA_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_chunk, int voff, int soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AA_LDS void*)lds_chunk, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt with only the vmcnt field constrained (expcnt/lgkmcnt left at max)
+template <int N>
+AA_DEV void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// s_waitcnt vmcnt(N) lgkmcnt(0): own copies up to the N newest have landed and
+// every LDS access of this wave has completed
+template <int N>
+AA_DEV void wait_vmcnt_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4));
+}
+
+// One k-step of a 32x32 MFMA tile: src0 = B fragment (16 bytes per lane),
+// src1 = A fragment(s) (two 16-byte halves for e4m3), packed scale bytes with
+// op_sel OSEL for the MX kinds.  Result lane l holds C[m = l%32][n = 8q + 4(l/32) + r].
+template <int KA, int OSEL>
+AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f32x16v_t c, int sa, int sb) {
+    if constexpr (KA == kBf16) {
+        typedef __bf16 bf16x8v_t __attribute__((ext_vector_type(8)));
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v_t, b), __builtin_bit_cast(bf16x8v_t, a0),
+                                                       c, 0, 0, 0);
+    } else {
+        i32x8_t bv, av;
+        bv[0] = b[0]; bv[1] = b[1]; bv[2] = b[2]; bv[3] = b[3];
+        bv[4] = 0; bv[5] = 0; bv[6] = 0; bv[7] = 0;
+        av[0] = a0[0]; av[1] = a0[1]; av[2] = a0[2]; av[3] = a0[3];
+        if constexpr (KA == kFp8) {
+            av[4] = a1[0]; av[5] = a1[1]; av[6] = a1[2]; av[7] = a1[3];
+        } else {
+            av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
+        }
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, c, 4, OpTraits<KA>::fmt, OSEL, sb, OSEL, sa);
+    }
+}
+
+// Epilogue of a wave's (32*MA) x (32*NB) block of 32x32 MFMA accumulators
+// (lane l holds C[m = l%32][n = 8q + 4(l/32) + r] of each tile) written as
+// bf16 or f32, D = alpha*acc + beta*bias.  Stored directly, each global store
+// would touch 32 rows; instead the block goes through the wave's own LDS
+// scratch `cb`, MP row tiles (32*MP rows x 32*NB elements) per pass, 16-byte
+// pieces XOR-swizzled by row so that both the writes and the 16-byte reads
+// spread over the banks, and leaves as whole rows.  (mb, nb) is the block's
+// global origin.  Branch-free: stores go through a range-checked descriptor
+// of D (rows >= M fall outside it, columns >= N get an offset outside it) and
+// bias reads are clamped into the bias tensor.  SCALED = false skips the
+// alpha multiply (alpha == 1, no bias).
+template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false>
+AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
+    static_assert(MA % MP == 0, "whole passes");
+    constexpr int EB = OUT_F32 ? 4 : 2;         // output bytes per element
+    constexpr int RB = 32 * NB * EB;            // bytes per block row
+    constexpr int P = RB / 16;                  // 16-byte pieces per row
+    static_assert(P <= 64, "one row per read instruction at most");
+    constexpr int SWM = (P < 8 ? P : 8) - 1;    // swizzle mask
+    constexpr int RSH = RB < 128 ? 1 : 0;       // two 64-byte rows share a 128-byte bank line
+    constexpr int ROWS_PER = 64 / P;            // rows per read instruction
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    // opaque copy of the lane index: keeps the compiler from hoisting this
+    // epilogue's address arithmetic out of an enclosing loop
+    asm volatile("" : "+v"(lane));
+    const __amdgpu_buffer_rsrc_t d_rsrc = make_rsrc(p.D, (int64_t)p.M * p.ldd * EB);
+    const int pc = lane % P;
+    const int n_out = nb + pc * (16 / EB);
+    const int col_off = n_out < p.N ? n_out * EB : 0x7fffffff;   // outside D when past N
+#pragma unroll
+    for (int i0 = 0; i0 < MA; i0 += MP) {
+#pragma unroll
+        for (int i = 0; i < MP; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int r = i * 32 + (lane & 31);
+                    const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
+                    const f32x16v_t& a = acc[i0 + i][j];
+                    float v[4] = {a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                    if constexpr (SCALED) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] *= p.alpha;
+                    }
+                    if constexpr (HAS_BIAS) {
+                        const int m = min(mb + i0 * 32 + r, p.M - 1), n = min(nb + nl, p.N - 4);
+                        const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
+                    }
+                    const int byte = nl * EB;
+                    const int piece = (byte >> 4) ^ ((r >> RSH) & SWM);
+                    if constexpr (OUT_F32) {
+                        *reinterpret_cast<f32x4_t*>(cb + r * RB + piece * 16) = f32x4_t{v[0], v[1], v[2], v[3]};
+                    } else {
+                        *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (byte & 15)) =
+                            u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    }
+                }
+        // the scratch is the wave's own: its LDS accesses complete in order
+#pragma unroll
+        for (int rr = 0; rr < 32 * MP; rr += ROWS_PER) {
+            const int r = rr + lane / P;
+            const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
+            const int m = mb + i0 * 32 + r;
+            const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * EB + col_off;
+            __builtin_amdgcn_raw_buffer_store_b128(v, d_rsrc, off, 0, 0);
+        }
+    }
+}
+
+// the three epilogue flavours picked at run time (uniform branch)
+template <int MA, int NB, int MP, bool OUT_F32>
+AA_DEV void store_block_any(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
+    if (p.bias)
+        store_block<MA, NB, MP, true, true, OUT_F32>(p, acc, cb, lane, mb, nb);
+    else if (p.alpha != 1.0f)
+        store_block<MA, NB, MP, false, true, OUT_F32>(p, acc, cb, lane, mb, nb);
+    else
+        store_block<MA, NB, MP, false, false, OUT_F32>(p, acc, cb, lane, mb, nb);
+}
+
+}  // namespace aiter_amd
