@@ -18,6 +18,7 @@
 #include "gemm_kernels.h"
 #include "mfma32.h"
 #include "gemm_flat.h"
+#include "gemm_flat_persist.h"
 #include "gemm_t32.h"
 
 namespace aiter_amd {
@@ -58,6 +59,7 @@ struct Instance {
     bool split;   // skinny split-K over blocks
     Variant var;
     LaunchFn fn;
+    bool persistent = false;   // grid of min(tiles, CUs) workgroups walking the tiles
 };
 
 template <int KA, int KB, int BM, int BN, bool AP, bool BP, bool OF>
@@ -71,6 +73,11 @@ constexpr int kSkinnyWaves = 8;
 template <int KA, int BM, bool OF = false>
 void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_flat_kernel<KA, BM, OF><<<grid, 256, 0, s>>>(p);
+}
+
+template <int KA, int BM, bool OF = false>
+void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
+    gemm_flat_persist_kernel<KA, BM, OF><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false>
@@ -169,6 +176,18 @@ std::vector<Instance>& registry() {
 #undef AA_S16
             }
         }
+        // ---- persistent forms of the flat tiles (gemm_flat_persist.h);
+        // appended so that the ids above stay stable ----
+        auto persist = [&](Family f, int bm, Variant v, LaunchFn fn, const char* fam) {
+            tile(f, bm, 256, v, fn, fam);
+            reg.back().name += "_persist";
+            reg.back().persistent = true;
+        };
+        persist(kA4W4, 256, pre, launch_flat_persist<kFp4, 256>, "a4w4");
+        persist(kA4W4, 128, pre, launch_flat_persist<kFp4, 128>, "a4w4");
+        persist(kA8W4, 128, a8, launch_flat_persist<kFp8, 128>, "a8w4");
+        persist(kA16W16, 256, Variant{false, true, false}, launch_flat_persist<kBf16, 256>, "a16w16");
+        persist(kA16W16, 128, Variant{false, true, false}, launch_flat_persist<kBf16, 128>, "a16w16");
     });
     return reg;
 }
@@ -216,7 +235,7 @@ const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int c
     long best_round = 1L << 40;
     double best_eff = 0;
     for (auto& in : registry()) {
-        if (in.skinny || !variant_ok(in, f, v)) continue;
+        if (in.skinny || in.persistent || !variant_ok(in, f, v)) continue;   // persistent: tuned tables only
         const long tiles = (long)((M + in.bm - 1) / in.bm) * ((N + in.bn - 1) / in.bn);
         const long rounds = (tiles + cus - 1) / cus;
         const double eff = (double)in.bm * in.bn / (in.bm + in.bn);
@@ -395,7 +414,18 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         p.tiles_m = (int)((M + inst->bm - 1) / inst->bm);
         p.tiles_n = (int)((N + inst->bn - 1) / inst->bn);
         AA_CHECK(M >= 16 || !c.var.a_pre, "preshuffled A needs M >= 16");
-        inst->fn(p, dim3(p.tiles_m * p.tiles_n), stream);
+        const int tiles = p.tiles_m * p.tiles_n;
+        if (inst->persistent && p.bias) {
+            // the persistent epilogue has no bias term: its one-tile-per-workgroup twin
+            const Instance* twin = nullptr;
+            for (auto& in : registry())
+                if (!in.skinny && !in.persistent && in.fam == inst->fam && in.bm == inst->bm && in.bn == inst->bn &&
+                    variant_ok(in, c.fam, c.var))
+                    twin = &in;
+            AA_CHECK(twin, "no non-persistent twin of ", inst->name);
+            inst = twin;
+        }
+        inst->fn(p, dim3(inst->persistent ? std::min(tiles, cus) : tiles), stream);
     } else {
         // the skinny kernels split K in k-pairs (one scale dword each)
         const int kpairs = ksteps / 2;

@@ -80,8 +80,10 @@ AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f
 // global origin.  Branch-free: stores go through a range-checked descriptor
 // of D (rows >= M fall outside it, columns >= N get an offset outside it) and
 // bias reads are clamped into the bias tensor.  SCALED = false skips the
-// alpha multiply (alpha == 1, no bias).
-template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false>
+// alpha multiply (alpha == 1, no bias).  FENCED = true converts one 32x32
+// block per scheduling region, for epilogues inside a loop where the other
+// live registers leave no room for all accumulator reads at once.
+template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false, bool FENCED = false>
 AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     static_assert(MA % MP == 0, "whole passes");
     constexpr int EB = OUT_F32 ? 4 : 2;         // output bytes per element
@@ -104,7 +106,8 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
 #pragma unroll
         for (int i = 0; i < MP; ++i)
 #pragma unroll
-            for (int j = 0; j < NB; ++j)
+            for (int j = 0; j < NB; ++j) {
+                if constexpr (FENCED) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int r = i * 32 + (lane & 31);
@@ -130,6 +133,8 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
                             u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     }
                 }
+            }
+        if constexpr (FENCED) __builtin_amdgcn_sched_barrier(0);
         // the scratch is the wave's own: its LDS accesses complete in order
 #pragma unroll
         for (int rr = 0; rr < 32 * MP; rr += ROWS_PER) {

@@ -89,9 +89,12 @@ def err_ratio(out: torch.Tensor, ref: torch.Tensor, rtol=1e-2, atol=1e-2) -> flo
 
 
 # ---------------------------------------------------------------- timing
-def time_rotated(fn, n_copies: int, iters: int) -> float:
+def time_rotated(fn, n_copies: int, iters: int, warm_s: float = 0.15, reps: int = 3) -> float:
     """Average seconds per call of ``fn(i)`` (i = rotation index), captured
-    ``iters`` times in one HIP graph and replayed after a warm replay."""
+    ``iters`` times in one HIP graph.  The graph is replayed for at least
+    ``warm_s`` first (the shader clock takes a few hundred milliseconds to
+    reach its loaded level, which would otherwise favour whichever candidate
+    runs later), then the median of ``reps`` timed replays is returned."""
     for i in range(min(3, n_copies)):
         fn(i)
     torch.cuda.synchronize()
@@ -105,16 +108,23 @@ def time_rotated(fn, n_copies: int, iters: int) -> float:
             for i in range(iters):
                 fn(i % n_copies)
     torch.cuda.synchronize()
-    g.replay()
-    torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    with torch.cuda.stream(s):
-        e0.record(s)
+    t0 = time.perf_counter()
+    while True:
         g.replay()
-        e1.record(s)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e-3 / iters
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= warm_s:
+            break
+    times = []
+    for _ in range(reps):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(s):
+            e0.record(s)
+            g.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e-3 / iters)
+    return sorted(times)[len(times) // 2]
 
 
 def _copies(per_call_bytes: int) -> int:

@@ -102,19 +102,29 @@ def a4w4_bytes(m, n, k):
     return m * k // 2 + n * k // 2 + m * k // 32 + n * k // 32 + 2 * m * n
 
 
+def headline_kernel():
+    """The instance gemm_a4w4 dispatches M=N=K=8192 to: the tuned table's
+    kernelName, else "" (the library heuristic)."""
+    import aiter_amd
+
+    cfg = aiter_amd.get_GEMM_config(8192, 8192, 8192)
+    return str(cfg["kernelName"]) if cfg else ""
+
+
 def bench_prefill(steps, warmup, dev):
     import aiter_amd
 
     m = n = k = 8192
     aq, as_, bq, bs = quantised_operands(m, n, k, 0, dev)
     out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+    kname = headline_kernel()
 
     def step():
-        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
+        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out, kernelName=kname)
 
     sec = time_graph(step, steps, warmup, min_warm_s=1.0)
     flop = 2.0 * m * n * k
-    return sec, flop / sec / 1e12
+    return sec, flop / sec / 1e12, kname
 
 
 def bench_decode(dev, steps=50):
@@ -251,11 +261,12 @@ def pmc_workload(dev):
     out = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
     for _ in range(3):
         dst.copy_(src)
+    kname = headline_kernel()
     for _ in range(3):
         dst.copy_(src)
-        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out)
+        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out, kernelName=kname)
     torch.cuda.synchronize()
-    log(f"pmc workload done: copy {COPY_BYTES} B x6, a4w4 8192^3 x3")
+    log(f"pmc workload done: copy {COPY_BYTES} B x6, a4w4 8192^3 x3 ({kname or 'heuristic'})")
 
 
 def traffic_from_profiles():
@@ -290,8 +301,8 @@ def main():
         return
 
     log("prefill A4W4 8192^3")
-    sec, tflops = bench_prefill(args.steps, args.warmup, dev)
-    log(f"prefill: {sec*1e6:.1f} us/step, {tflops:.0f} TFLOP/s")
+    sec, tflops, kname = bench_prefill(args.steps, args.warmup, dev)
+    log(f"prefill: {sec*1e6:.1f} us/step, {tflops:.0f} TFLOP/s ({kname or 'heuristic'})")
     decode = [] if args.quick else bench_decode(dev)
     extra = {} if args.quick else bench_extra(dev)
     cpu = None if (args.no_cpu or args.quick) else cpu_baseline()
@@ -310,7 +321,7 @@ def main():
         "dtype": "mxfp4",
         "data": "synthetic",
         "config": {"workload": "A4W4 MXFP4xMXFP4 GEMM, M=N=K=8192, preshuffled B, e8m0 per-1x32 scales, bf16 out "
-                               "(BASELINE configs[2])", "M": m, "N": n, "K": k},
+                               "(BASELINE configs[2])", "M": m, "N": n, "K": k, "kernel": kname or "heuristic"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": PEAK_MXFP4, "unit": "TFLOP/s",
                      "frac": round(tflops / PEAK_MXFP4, 4), "traffic": traffic_from_profiles()},
         "cpu_baseline": cpu,
