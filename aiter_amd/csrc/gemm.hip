@@ -80,9 +80,9 @@ void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_flat_persist_kernel<KA, BM, OF><<<grid, 256, 0, s>>>(p);
 }
 
-template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false>
+template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
 void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_t32_kernel<KA, BP, BM, BN, WMW, OF><<<grid, 256, 0, s>>>(p);
+    gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, int MF, bool BP, bool SPLIT, bool OF>
@@ -188,6 +188,36 @@ std::vector<Instance>& registry() {
         persist(kA8W4, 128, a8, launch_flat_persist<kFp8, 128>, "a8w4");
         persist(kA16W16, 256, Variant{false, true, false}, launch_flat_persist<kBf16, 256>, "a16w16");
         persist(kA16W16, 128, Variant{false, true, false}, launch_flat_persist<kBf16, 128>, "a16w16");
+        // ---- split-K forms of the smaller t32 tiles (K split over gridDim.y,
+        // f32 partial slices summed by splitk_reduce_kernel), for shapes
+        // whose tiles cannot fill the CUs ----
+        auto tsplit = [&](Family f, int bm, int bn, Variant v, LaunchFn fn, const char* fam) {
+            std::string nm = std::string(fam) + "_tile_" + std::to_string(bm) + "x" + std::to_string(bn) + "_splitk";
+            if (v.a_pre) nm += "_apre";
+            if (!v.b_pre) nm += "_bplain";
+            if (v.out_f32) nm += "_f32";
+            reg.push_back({id++, nm, f, false, bm, bn, true, v, fn});
+        };
+        tsplit(kA4W4, 64, 128, pre, launch_t32<kFp4, true, 64, 128, 1, false, true>, "a4w4");
+        tsplit(kA4W4, 64, 256, pre, launch_t32<kFp4, true, 64, 256, 1, false, true>, "a4w4");
+        tsplit(kA4W4, 128, 128, pre, launch_t32<kFp4, true, 128, 128, 2, false, true>, "a4w4");
+        tsplit(kA4W4, 64, 128, plain, launch_t32<kFp4, false, 64, 128, 1, false, true>, "a4w4");
+        tsplit(kA8W4, 64, 128, a8, launch_t32<kFp8, true, 64, 128, 1, false, true>, "a8w4");
+        tsplit(kA8W4, 64, 256, a8, launch_t32<kFp8, true, 64, 256, 1, false, true>, "a8w4");
+        for (int of = 0; of < 2; ++of) {
+            for (int bp = 0; bp < 2; ++bp) {
+                const Variant v{false, bp != 0, of != 0};
+#define AA_T16S(BM, BN, WMW)                                                                      \
+    tsplit(kA16W16, BM, BN, v,                                                                    \
+           of ? (bp ? launch_t32<kBf16, true, BM, BN, WMW, true, true>                            \
+                    : launch_t32<kBf16, false, BM, BN, WMW, true, true>)                          \
+              : (bp ? launch_t32<kBf16, true, BM, BN, WMW, false, true>                           \
+                    : launch_t32<kBf16, false, BM, BN, WMW, false, true>),                        \
+           "a16w16");
+                AA_T16S(64, 64, 2) AA_T16S(64, 128, 1) AA_T16S(128, 128, 2)
+#undef AA_T16S
+            }
+        }
     });
     return reg;
 }
@@ -215,6 +245,14 @@ int skinny_splits(int n_blocks, int k_steps, int cus) {
     return s;
 }
 
+// Split-K factor for a split tile launch: enough splits for about one
+// workgroup per CU, keeping >= 8 stages per split.
+int tile_splits(int tiles, int stages, int cus) {
+    int s = 1;
+    while (tiles * s * 2 <= cus && stages / (s * 2) >= 8) s *= 2;
+    return s;
+}
+
 // Heuristic choice among tile instances (reference heuristic idea:
 // csrc/py_itfs_cu/asm_gemm_a4w4.cu:81-152 — fewest rounds of tiles over the
 // CUs, then higher tile compute/memory ratio).
@@ -235,7 +273,7 @@ const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int c
     long best_round = 1L << 40;
     double best_eff = 0;
     for (auto& in : registry()) {
-        if (in.skinny || in.persistent || !variant_ok(in, f, v)) continue;   // persistent: tuned tables only
+        if (in.skinny || in.persistent || in.split || !variant_ok(in, f, v)) continue;   // tuned tables only
         const long tiles = (long)((M + in.bm - 1) / in.bm) * ((N + in.bn - 1) / in.bn);
         const long rounds = (tiles + cus - 1) / cus;
         const double eff = (double)in.bm * in.bn / (in.bm + in.bn);
@@ -415,6 +453,34 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         p.tiles_n = (int)((N + inst->bn - 1) / inst->bn);
         AA_CHECK(M >= 16 || !c.var.a_pre, "preshuffled A needs M >= 16");
         const int tiles = p.tiles_m * p.tiles_n;
+        if (inst->split) {
+            // split-K tile: stages of K over gridDim.y, f32 slices, then a sum
+            const int nst = (int)(K / (scaled ? 256 : 64));
+            int sp = c.log2_split >= 0 ? (1 << c.log2_split) : tile_splits(tiles, nst, cus);
+            sp = std::max(1, std::min(sp, nst));
+            p.k_steps_per_split = (nst + sp - 1) / sp;
+            sp = (nst + p.k_steps_per_split - 1) / p.k_steps_per_split;
+            if (sp > 1) {
+                const size_t need = (size_t)sp * M * N * sizeof(float);
+                p.ws = workspace(dev, stream, need);
+                inst->fn(p, dim3(tiles, sp), stream);
+                const unsigned blocks = (unsigned)(((int64_t)M * N / 4 + 255) / 256);
+                if (c.var.out_f32)
+                    splitk_reduce_kernel<true><<<dim3(blocks), 256, 0, stream>>>(p, sp);
+                else
+                    splitk_reduce_kernel<false><<<dim3(blocks), 256, 0, stream>>>(p, sp);
+                AA_HIP(hipGetLastError());
+                return;
+            }
+            // one split: the same tile without the split
+            const Instance* twin = nullptr;
+            for (auto& in : registry())
+                if (!in.skinny && !in.split && !in.persistent && in.bm == inst->bm && in.bn == inst->bn &&
+                    variant_ok(in, c.fam, c.var))
+                    twin = &in;
+            AA_CHECK(twin, "no non-split twin of ", inst->name);
+            inst = twin;
+        }
         if (inst->persistent && p.bias) {
             // the persistent epilogue has no bias term: its one-tile-per-workgroup twin
             const Instance* twin = nullptr;

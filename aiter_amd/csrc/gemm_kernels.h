@@ -51,7 +51,7 @@ struct GemmParams {
     const uint8_t* Bs;
     void* D;
     const float* bias;
-    float* ws;           // split-K f32 partial sums [M_pad, N] (skinny split path)
+    float* ws;           // split-K f32 partial sums: [M, N] (skinny), [splits][M][N] (tiles)
     int64_t lda, ldb;    // bytes per row (row-major) / per row of the preshuffled matrix
     int64_t ldd;         // elements per output row
     int64_t ld_bias;     // elements per bias row (0 = broadcast one row)
@@ -59,7 +59,7 @@ struct GemmParams {
     int M, N, K;
     int sa_groups, sb_groups;      // 32-row groups present in the scale buffers
     int tiles_m, tiles_n;
-    int k_steps_per_split;         // skinny split-K: MFMA k-steps per split
+    int k_steps_per_split;         // split-K: k-pairs (skinny) or stages (tiles) per split
     float alpha, beta;
 };
 
@@ -490,6 +490,19 @@ __global__ __launch_bounds__(256) void splitk_finish_kernel(GemmParams p) {
     if (idx >= total) return;
     const int m = (int)(idx / p.N), n = (int)(idx % p.N);
     const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.ws + idx);
+    store_frag<OUT_F32>(p, v, m, n);
+}
+
+// Sum of the `splits` f32 partial slices [splits][M][N] of a split tile
+// GEMM (slice order fixed) -> output (+alpha, +bias).
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int splits) {
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    const int64_t total = (int64_t)p.M * p.N;
+    if (idx >= total) return;
+    f32x4_t v = *reinterpret_cast<const f32x4_t*>(p.ws + idx);
+    for (int s = 1; s < splits; ++s) v += *reinterpret_cast<const f32x4_t*>(p.ws + s * total + idx);
+    const int m = (int)(idx / p.N), n = (int)(idx % p.N);
     store_frag<OUT_F32>(p, v, m, n);
 }
 

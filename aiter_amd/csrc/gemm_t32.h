@@ -42,7 +42,10 @@ struct T32Cfg {
     static constexpr int K_STAGE = MX ? 256 : 64;             // K elements per stage
 };
 
-template <int KA, bool BPRE, int BM, int BN, int WAVES_M, bool OUT_F32>
+// SPLIT: blockIdx.y takes stages [y*S, y*S + S) of K (S = p.k_steps_per_split)
+// and writes its fp32 partial tile to slice y of p.ws ([splits][M][N]); a
+// second kernel sums the slices (fixed order, so results are deterministic).
+template <int KA, bool BPRE, int BM, int BN, int WAVES_M, bool OUT_F32, bool SPLIT = false>
 __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
     using Cfg = T32Cfg<KA, BPRE, BM, BN>;
     constexpr bool MX = Cfg::MX;
@@ -74,7 +77,9 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
     int tm, tn;
     tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
-    const int nstages = p.K / Cfg::K_STAGE;
+    // stages of this workgroup: [t_base, t_base + nstages) of K
+    const int t_base = SPLIT ? (int)blockIdx.y * p.k_steps_per_split : 0;
+    const int nstages = SPLIT ? min(p.K / Cfg::K_STAGE - t_base, p.k_steps_per_split) : p.K / Cfg::K_STAGE;
     const __amdgpu_buffer_rsrc_t null_rsrc = make_rsrc(p.A, 0);
 
     // ---- A: chunk c = half*(BM/8) + 8-row block; lane l -> row l/8, stored piece l%8
@@ -132,11 +137,11 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
 #pragma unroll
         for (int q = part * DMA_PART; q < (part + 1) * DMA_PART && q < NDMA; ++q) {
             if (q < NA)
-                dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], t * A_ROW_BYTES);
+                dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], (t_base + t) * A_ROW_BYTES);
             else if (q < NA + NBW)
-                dma16(rb, base + (A_CH + wave + 4 * (q - NA)) * 1024, b_off[q - NA], t * B_STAGE_OFF);
+                dma16(rb, base + (A_CH + wave + 4 * (q - NA)) * 1024, b_off[q - NA], (t_base + t) * B_STAGE_OFF);
             else
-                dma16(rs, base + (A_CH + B_CH + wave) * 1024, sc_off, t * 256);
+                dma16(rs, base + (A_CH + B_CH + wave) * 1024, sc_off, (t_base + t) * 256);
         }
     };
 
@@ -281,7 +286,18 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
     static_assert(EP_MP * 32 * WN * EB <= WAVE_SCRATCH, "epilogue pass fits the ring");
     wait_vmcnt<0>();
     __syncthreads();
-    store_block_any<MA, NB, EP_MP, OUT_F32>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0 + wm * WM, n0 + wn * WN);
+    if constexpr (SPLIT) {
+        constexpr int EP_MP32 = (MA * 32 * WN * 4 <= WAVE_SCRATCH) ? MA
+                                : (MA % 2 == 0 && MA / 2 * 32 * WN * 4 <= WAVE_SCRATCH) ? MA / 2 : 1;
+        static_assert(EP_MP32 * 32 * WN * 4 <= WAVE_SCRATCH, "epilogue pass fits the ring");
+        GemmParams q = p;
+        q.D = p.ws + (int64_t)blockIdx.y * p.M * p.N;
+        q.ldd = p.N;
+        store_block<MA, NB, EP_MP32, false, false, true>(q, acc, smem + wave * WAVE_SCRATCH, lane, m0 + wm * WM,
+                                                         n0 + wn * WN);
+    } else {
+        store_block_any<MA, NB, EP_MP, OUT_F32>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0 + wm * WM, n0 + wn * WN);
+    }
 }
 
 }  // namespace aiter_amd

@@ -143,7 +143,8 @@ def candidates(family: str, M: int, bpreshuffle: bool = True, out_f32: bool = Fa
         if not skinny and M <= 16 and bm > 64:
             continue  # a 128/256-row tile for a handful of rows is never the fastest
         if split:
-            for l2 in (0, 1, 2, 3):  # 0 = the library's own split choice
+            # 0 = the library's own split choice; tiles also try 16 splits
+            for l2 in ((0, 1, 2, 3) if skinny else (0, 1, 2, 3, 4)):
                 out.append((kid, name, l2))
         else:
             out.append((kid, name, 0))
