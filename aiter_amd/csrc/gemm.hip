@@ -70,14 +70,14 @@ void launch_tile(const GemmParams& p, dim3 grid, hipStream_t s) {
 constexpr int kSkinnyWaves = 8;
 
 
-template <int KA, int BM, bool OF = false>
+template <int KA, int BM, bool OF = false, bool BP = true>
 void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_flat_kernel<KA, BM, OF><<<grid, 256, 0, s>>>(p);
+    gemm_flat_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
 }
 
-template <int KA, int BM, bool OF = false>
+template <int KA, int BM, bool OF = false, bool BP = true>
 void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_flat_persist_kernel<KA, BM, OF><<<grid, 256, 0, s>>>(p);
+    gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
@@ -218,6 +218,10 @@ std::vector<Instance>& registry() {
 #undef AA_T16S
             }
         }
+        // ---- a4w4 with row-major B on the flat kernels (B straight to VGPRs:
+        // 16 contiguous bytes of one row per lane) ----
+        tile(kA4W4, 256, 256, plain, launch_flat<kFp4, 256, false, false>, "a4w4");
+        persist(kA4W4, 256, plain, launch_flat_persist<kFp4, 256, false, false>, "a4w4");
     });
     return reg;
 }

@@ -45,7 +45,12 @@ struct FlatCfg {
     static constexpr int K_STAGE = MX ? 256 : 64;     // K elements per stage (128 bytes of a row)
 };
 
-template <int KA, int BM, bool OUT_F32>
+// BPRE = false: B row-major [N, K].  The 32x32 MFMA's B operand is then 16
+// contiguous bytes of one row per lane (row l%32, bytes 16*(l/32) of the
+// k-step's 32-byte window), so row-major B also loads straight into VGPRs;
+// one load touches 32 rows (32 bytes each), and the four k-steps of a stage
+// consume each row's 128-byte line.
+template <int KA, int BM, bool OUT_F32, bool BPRE = true>
 __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     using Cfg = FlatCfg<KA, BM>;
     constexpr int BN = 256;
@@ -87,14 +92,18 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
         const int r = rb * 8 + (lane >> 3);
         a_off[q] = r * (int)p.lda + half * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16);
     }
-    // ---- B (preshuffled (16,16)): tile j of wave w = 16-row blocks 4w+2j, 4w+2j+1;
+    // ---- B preshuffled (16,16): tile j of wave w = 16-row blocks 4w+2j, 4w+2j+1;
     //      k-step s of stage t at blk*16*ldb + (4t+s)*512 + (l/32)*256 + (l%16)*16
+    //      B row-major: row 64w+32j+l%32 at (4t+s)*32 + (l/32)*16
     const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.B + (int64_t)n0 * p.ldb, (int64_t)(p.N - n0) * p.ldb);
     int b_off[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const int blk = 4 * wave + 2 * j + ((lane >> 4) & 1);
-        b_off[j] = blk * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
+        if constexpr (BPRE)
+            b_off[j] = blk * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
+        else
+            b_off[j] = (64 * wave + 32 * j + (lane & 31)) * (int)p.ldb + (lane >> 5) * 16;
     }
     // ---- scales: wave w copies chunk w (A chunks first, then the 2 B chunks)
     const int ga0 = m0 / 32, gb0 = n0 / 32;
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     };
     auto load_b = [&](int t, int j, int s) -> i32x4_t {
         const __amdgpu_buffer_rsrc_t rb = t < nstages ? b_rsrc : null_rsrc;
-        return __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + s * 512, t * 2048, 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + s * (BPRE ? 512 : 32), t * (BPRE ? 2048 : 128), 0);
     };
 
     const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;

@@ -39,7 +39,8 @@ struct FlatPersistCfg {
     static constexpr int K_STAGE = MX ? 256 : 64;
 };
 
-template <int KA, int BM, bool OUT_F32>
+// BPRE = false: row-major B, loaded straight into VGPRs as in gemm_flat_kernel.
+template <int KA, int BM, bool OUT_F32, bool BPRE = true>
 __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p) {
     using Cfg = FlatPersistCfg<KA, BM>;
     constexpr int NS = 4;
@@ -85,7 +86,10 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
         const int b16 = 4 * wave + 2 * j + ((lane >> 4) & 1);
-        b_off[j] = b16 * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
+        if constexpr (BPRE)
+            b_off[j] = b16 * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
+        else
+            b_off[j] = (64 * wave + 32 * j + (lane & 31)) * (int)p.ldb + (lane >> 5) * 16;
     }
     // whole-tensor descriptors: rows past M / N and groups past the scale
     // tensors read zeros
@@ -166,7 +170,8 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         const __amdgpu_buffer_rsrc_t rb = bt < bnst ? b_rsrc : null_rsrc;
 #pragma unroll
         for (int j = 0; j < NB; ++j)
-            bq[bpar][j][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + bbase + s * 512, bt * 2048, 0);
+            bq[bpar][j][s] = __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + bbase + s * (BPRE ? 512 : 32),
+                                                                   bt * (BPRE ? 2048 : 128), 0);
     };
     constexpr int DMA_PART = (NDMA + 2) / 3;
     // third `part` of the copies of stage dt of the tile at (abase, scbase)

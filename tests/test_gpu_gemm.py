@@ -62,14 +62,15 @@ def _kernel_names(family, **kw):
         return []
 
 
-@pytest.mark.parametrize("name", _kernel_names("a4w4"))
+@pytest.mark.parametrize("name", _kernel_names("a4w4") + _kernel_names("a4w4", b_pre=False))
 def test_gemm_a4w4_every_instance(cuda, name):
-    """Every A4W4 instance (tile and skinny, incl. split-K) on a ragged shape."""
+    """Every A4W4 instance (tile and skinny, incl. split-K; preshuffled and
+    row-major B) on a ragged shape."""
     import aiter_amd
     from aiter_amd._lib import kernel_table
 
     row = [r for r in kernel_table() if r[1] == name][0]
-    skinny, bm = row[3], row[4]
+    skinny, bm, b_pre = row[3], row[4], row[8]
     m = min(bm, 48) if skinny else 200
     if skinny:
         m = max(1, bm - 3)
@@ -77,14 +78,15 @@ def test_gemm_a4w4_every_instance(cuda, name):
     announce(f"a4w4 instance {name} {m}x{n}x{k}")
     a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=3)
     out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
-    aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda),
-                            _dev(b_ss, cuda), out, kernelName=name, log2_k_split=2 if row[6] else 0)
+    aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q) if b_pre else b_q, cuda), _dev(a_ss, cuda),
+                            _dev(b_ss, cuda), out, kernelName=name, log2_k_split=2 if row[6] else 0,
+                            bpreshuffle=bool(b_pre))
     torch.cuda.synchronize()
     ok, msg = allclose_report(_bf16_np(out[:m]), ref)
     assert ok, msg
 
 
-@pytest.mark.parametrize("m", [1, 32, 96])
+@pytest.mark.parametrize("m", [1, 32, 96, 600])
 def test_gemm_a4w4_row_major_b(cuda, m):
     import aiter_amd
 

@@ -63,13 +63,13 @@ def _operands(fam, m, n, k, cuda, seed):
     return a, b, sa, sb
 
 
-def _run(fam, name, a, b, sa, sb, m, n, cuda, bias=None, alpha=1.0):
+def _run(fam, name, a, b, sa, sb, m, n, cuda, bias=None, alpha=1.0, b_pre=True):
     import aiter_amd
 
     if fam == "a4w4":
         out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
         aiter_amd.gemm_a4w4_asm(a, b, sa, sb, out, kernelName=name, bias=bias, alpha=alpha,
-                                beta=1.0 if bias is not None else 0.0)
+                                beta=1.0 if bias is not None else 0.0, bpreshuffle=b_pre)
     elif fam == "a8w4":
         out = aiter_amd.gemm_a8w4_mxfp8(a.view(torch.float8_e4m3fn), b, sa, sb, a_preshuffle=False, kernelName=name)
     else:
@@ -81,16 +81,16 @@ def _run(fam, name, a, b, sa, sb, m, n, cuda, bias=None, alpha=1.0):
 
 @pytest.mark.parametrize("row", ROWS, ids=IDS)
 def test_persist_matches_twin(cuda, row):
-    name, fam = row[1], row[2]
+    name, fam, b_pre = row[1], row[2], bool(row[8])
     twin = name[: -len("_persist")]
     for i, (m, n, k) in enumerate(_shapes(row)):
         announce(f"persist {name} vs {twin} {m}x{n}x{k}")
         a, b, sa, sb = _operands(fam, m, n, k, cuda, seed=40 + i)
-        got = _run(fam, name, a, b, sa, sb, m, n, cuda)
-        want = _run(fam, twin, a, b, sa, sb, m, n, cuda)
+        got = _run(fam, name, a, b, sa, sb, m, n, cuda, b_pre=b_pre)
+        want = _run(fam, twin, a, b, sa, sb, m, n, cuda, b_pre=b_pre)
         assert torch.equal(got, want), f"{name} {m}x{n}x{k}: differs from {twin}"
         # a second call reuses nothing: same result again
-        assert torch.equal(_run(fam, name, a, b, sa, sb, m, n, cuda), want)
+        assert torch.equal(_run(fam, name, a, b, sa, sb, m, n, cuda, b_pre=b_pre), want)
 
 
 def test_persist_alpha_and_bias(cuda):
