@@ -7,6 +7,8 @@ Ops (all backed by hand-written HIP kernels in libaiter_amd.so):
   get_hip_quant / get_triton_quant(QuantType.per_1x32), quant_mxfp4_hip,
   per_1x32_mx_quant_hip, dynamic_mxfp4_quant, dynamic_mxfp8_quant
   shuffle_weight, shuffle_scale
+The GEMMs and quantisers are also torch custom ops, torch.ops.aiter_amd.<name>
+(torch_ops.py), with fake implementations for torch.compile / torch.export.
 """
 from . import dtypes
 from .gemm_common import get_padded_m
@@ -20,5 +22,6 @@ from .quant import (MxScaleRoundMode, QuantType, dynamic_mxfp4_quant, dynamic_mx
                     quant_mxfp4_hip)
 from .shuffle import e8m0_shuffle, shuffle_scale, shuffle_weight
 from .tuned_gemm import TunedGemm, gemm_a16w16, get_GEMM_A16W16_config, tgemm
+from . import torch_ops  # registers torch.ops.aiter_amd.*
 
 __all__ = [n for n in dir() if not n.startswith("_")]

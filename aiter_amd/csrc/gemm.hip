@@ -273,19 +273,32 @@ const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int c
                 return &in;
             }
     }
+    // time ~ rounds of tiles x per-tile time, and a tile's time per K step
+    // grows like BM + BN (operand bytes) while its work grows like BM * BN:
+    // minimise rounds * (BM + BN); on ties the larger tile
     const Instance* best = nullptr;
-    long best_round = 1L << 40;
-    double best_eff = 0;
+    long best_cost = 1L << 40;
+    long best_tiles = 0;
     for (auto& in : registry()) {
         if (in.skinny || in.persistent || in.split || !variant_ok(in, f, v)) continue;   // tuned tables only
         const long tiles = (long)((M + in.bm - 1) / in.bm) * ((N + in.bn - 1) / in.bn);
         const long rounds = (tiles + cus - 1) / cus;
-        const double eff = (double)in.bm * in.bn / (in.bm + in.bn);
-        if (rounds < best_round || (rounds == best_round && eff > best_eff)) {
+        const long cost = rounds * (in.bm + in.bn);
+        if (cost < best_cost || (cost == best_cost && tiles < best_tiles)) {
             best = &in;
-            best_round = rounds;
-            best_eff = eff;
+            best_cost = cost;
+            best_tiles = tiles;
         }
+    }
+    // a grid that leaves most CUs idle splits K when the tile has a split form
+    const int nst = K / (f == kA16W16 ? 64 : 256);
+    if (best && best_tiles * 2 <= cus && nst >= 16) {
+        for (auto& in : registry())
+            if (!in.skinny && in.split && !in.persistent && in.bm == best->bm && in.bn == best->bn &&
+                variant_ok(in, f, v)) {
+                *splits = 0;   // the launcher picks the split count
+                return &in;
+            }
     }
     return best;
 }

@@ -179,17 +179,19 @@ def bench_extra(dev):
     import aiter_amd
 
     out = {}
-    # bf16 A16W16 M=N=K=8192
+    # bf16 A16W16 M=N=K=8192 through the tuned dispatch (gemm_a16w16 / tgemm.mm),
+    # row-major B and preshuffled B
     m = n = k = 8192
     g = torch.Generator(device="cpu").manual_seed(2)
     a = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
     b = torch.randn((n, k), generator=g).to(torch.bfloat16).to(dev)
-    c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-    sema = torch.empty(0, dtype=torch.uint32, device=dev)
-    t = time_graph(lambda: aiter_amd.gemm_a16w16_asm(a, b, c), 10, 2)
-    out["bf16_8192x8192x8192"] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1),
-                                  "frac_bf16_peak": round(2 * m * n * k / t / 1e12 / PEAK_BF16, 4)}
-    del a, b, c
+    bs = aiter_amd.shuffle_weight(b)
+    for tag, w in (("bf16_8192x8192x8192", b), ("bf16_8192x8192x8192_bpreshuffle", bs)):
+        t = time_graph(lambda w=w: aiter_amd.gemm_a16w16(a, w), 10, 2)
+        out[tag] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1),
+                    "frac_bf16_peak": round(2 * m * n * k / t / 1e12 / PEAK_BF16, 4)}
+    del a, b, bs
+    out["bf16_cpu_plumbing"] = bf16_plumbing(dev)
     # MXFP8 x MXFP4 M=4096 N=7168 K=16384 (+ dynamic quant of the bf16 activation)
     m, n, k = 4096, 7168, 16384
     x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
@@ -210,6 +212,50 @@ def bench_extra(dev):
     out["mxfp4_quant_8192x8192"] = {"us": round(tq * 1e6, 1),
                                     "GBps": round(8192 * 8192 * (2 + 0.5 + 1 / 32) / tq / 1e9, 1)}
     return out
+
+
+def bf16_plumbing(dev):
+    """A[128,4096] x B[4096,4096]^T bf16 from N(0,1) with
+    seed 0.  The reference's CPU torch path (F.linear in bf16, and the fp32
+    reference), median of 5 runs after 2 warm-ups on all host threads, next
+    to the same GEMM on the GPU through gemm_a16w16 and its max error."""
+    import platform
+
+    import aiter_amd
+
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(128, 4096, generator=g).to(torch.bfloat16)
+    b = torch.randn(4096, 4096, generator=g).to(torch.bfloat16)
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+
+    def med(fn):
+        for _ in range(2):
+            fn()
+        ts = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sorted(ts)[2]
+
+    t_bf16 = med(lambda: torch.nn.functional.linear(a, b))
+    ref = (a.float() @ b.float().T)
+    t_f32 = med(lambda: a.float() @ b.float().T)
+    ad, bd = a.to(dev), b.to(dev)
+    got = aiter_amd.gemm_a16w16(ad, bd).float().cpu()
+    t_gpu = time_graph(lambda: aiter_amd.gemm_a16w16(ad, bd), 20, 5)
+    cpu_model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        cpu_model = platform.processor() or "unknown"
+    return {"cpu_bf16_linear_ms": round(t_bf16 * 1e3, 2), "cpu_f32_ref_ms": round(t_f32 * 1e3, 2),
+            "cpu_threads": threads, "cpu_model": cpu_model, "gpu_us": round(t_gpu * 1e6, 2),
+            "max_abs_err_vs_f32": round(float((got - ref).abs().max()), 4),
+            "frac_within_1e-2": round(float(((got - ref.bfloat16().float()).abs()
+                                            <= 1e-2 + 1e-2 * ref.bfloat16().float().abs()).float().mean()), 6)}
 
 
 def cpu_baseline(budget_s=10.0):

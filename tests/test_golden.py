@@ -59,3 +59,20 @@ def test_gemm_fixture_layouts_invert():
     g = load("gemm_40x64x512.npz")
     np.testing.assert_array_equal(O.unshuffle_weight(g["b_fp4_shuf"]), g["b_fp4"])
     np.testing.assert_array_equal(O.unshuffle_scale(g["a_scale_shuf"], 40, 16), g["a_scale"])
+
+
+def test_bf16_plumbing_config_oracle_vs_torch():
+    """BASELINE configs[0] (A[128,4096] x B[4096,4096]^T bf16, torch seed 0):
+    the oracle's bf16 GEMM against torch's CPU fp32 matmul of the same bf16
+    operands (a library routine), rounded to bf16."""
+    import torch
+
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(128, 4096, generator=g).to(torch.bfloat16)
+    b = torch.randn(4096, 4096, generator=g).to(torch.bfloat16)
+    want = (a.float() @ b.float().T).bfloat16().float().numpy()
+    got = O.bf16_bits_to_f32(O.gemm_a16w16_ref(a.view(torch.int16).numpy().view(np.uint16),
+                                               b.view(torch.int16).numpy().view(np.uint16)))
+    np.testing.assert_allclose(got, want, rtol=1e-2, atol=1e-2)
+    # the two f32 sums differ only in order: almost every bf16 result is equal
+    assert (got == want).mean() > 0.99

@@ -329,3 +329,22 @@ def test_tile_instances_more_tiles_than_cus(cuda, m, n, k):
         torch.cuda.synchronize()
         ok, msg = allclose_report(_bf16_np(out[:m]), ref)
         assert ok, f"{name}: {msg}"
+
+
+def test_bf16_cpu_plumbing_config(cuda):
+    """BASELINE configs[0] on the GPU: A[128,4096] x B[4096,4096]^T, bf16 from
+    N(0,1) with torch seed 0, against the CPU fp32 reference of that config
+    (tgemm.mm and gemm_a16w16, row-major and preshuffled B)."""
+    import aiter_amd
+
+    announce("bf16 plumbing config 128x4096x4096")
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(128, 4096, generator=g).to(torch.bfloat16)
+    b = torch.randn(4096, 4096, generator=g).to(torch.bfloat16)
+    ref = (a.float() @ b.float().T).bfloat16().float().numpy()
+    ad, bd = a.to(cuda), b.to(cuda)
+    for got in (aiter_amd.tgemm.mm(ad, bd), aiter_amd.gemm_a16w16(ad, bd),
+                aiter_amd.gemm_a16w16(ad, aiter_amd.shuffle_weight(bd))):
+        torch.cuda.synchronize()
+        ok, msg = allclose_report(got.float().cpu().numpy(), ref)
+        assert ok, msg
