@@ -8,8 +8,13 @@
 // plus one scale byte.  The work is HBM-bound: 64 B in / 17 B out per block
 // for bf16 -> fp4.
 //
-// Element conversion is integer arithmetic (round to nearest even) so the
-// bytes are identical to the reference's CPU restatements on every input.
+// Element conversion: gfx950's scaled pair conversions
+// (v_cvt_scalef32_pk_fp4_* / v_cvt_scalef32_pk_fp8_*: value / 2^(e-127),
+// round to nearest even, saturating) for scale bytes 1..254, and integer
+// arithmetic (RNE) for the two bytes whose scale is not a normal f32 (0:
+// 2^-127, 255).  Both give the reference CPU restatements' bytes; the
+// hardware form costs one instruction per pair instead of ~15 per element,
+// which moves the kernel from VALU-bound to HBM-bound.
 
 #include "common.h"
 
@@ -83,6 +88,49 @@ AA_DEV uint32_t f32_to_e4m3(float x) {
     return s | code;
 }
 
+// One scaled pair conversion; `sel` (byte of the destination) must fold to a
+// constant.  InT selects the source form: bf16 pair, f16 pair (both as the
+// raw 32-bit pair) or two f32 values.
+template <typename InT>
+AA_DEV uint32_t cvt_fp4_pair(uint32_t old, uint32_t pair, float a, float b, float scale, int sel) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+#define AA_CVT_SEL(S)                                                                                   \
+    case S:                                                                                             \
+        if constexpr (std::is_same<InT, float>::value)                                                  \
+            return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, a, b, scale, S);                       \
+        else if constexpr (std::is_same<InT, _Float16>::value)                                          \
+            return __builtin_amdgcn_cvt_scalef32_pk_fp4_f16(old, __builtin_bit_cast(f16x2_t, pair), scale, S); \
+        else                                                                                            \
+            return __builtin_amdgcn_cvt_scalef32_pk_fp4_bf16(old, __builtin_bit_cast(bf16x2_t, pair), scale, S);
+    switch (sel) {
+        AA_CVT_SEL(0) AA_CVT_SEL(1) AA_CVT_SEL(2) AA_CVT_SEL(3)
+    }
+#undef AA_CVT_SEL
+    return old;
+}
+
+// Scaled pair conversion to e4m3fn: two values / scale -> two bytes in word
+// `hi` (0 or 1, constant) of the destination.
+template <typename InT>
+AA_DEV uint32_t cvt_fp8_pair(uint32_t old, uint32_t pair, float a, float b, float scale, bool hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+    typedef short s16x2_t __attribute__((ext_vector_type(2)));
+    const s16x2_t o = __builtin_bit_cast(s16x2_t, old);
+    s16x2_t r;
+    if constexpr (std::is_same<InT, float>::value)
+        r = hi ? __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, a, b, scale, true)
+               : __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(o, a, b, scale, false);
+    else if constexpr (std::is_same<InT, _Float16>::value)
+        r = hi ? __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(f16x2_t, pair), scale, true)
+               : __builtin_amdgcn_cvt_scalef32_pk_fp8_f16(o, __builtin_bit_cast(f16x2_t, pair), scale, false);
+    else
+        r = hi ? __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(bf16x2_t, pair), scale, true)
+               : __builtin_amdgcn_cvt_scalef32_pk_fp8_bf16(o, __builtin_bit_cast(bf16x2_t, pair), scale, false);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
 AA_DEV int scale_shuffle_idx(int scale_n_pad, int x, int y) {
     // csrc/include/mx_quant_utils.h:212-216
     return (x / 32 * scale_n_pad) * 32 + (y / 8) * 256 + (y % 4) * 64 + (x % 16) * 4 +
@@ -128,6 +176,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
 
     constexpr int kVec = 16 / sizeof(InT);  // elements per 16-byte load
     float v[32];
+    uint32_t raw[sizeof(InT) == 2 ? 16 : 1];   // 16-bit inputs: the loaded element pairs
     const InT* src = reinterpret_cast<const InT*>(p.in) + x * p.in_stride + (int64_t)y * 32;
 #pragma unroll
     for (int i = 0; i < 32 / kVec; ++i) {
@@ -144,6 +193,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t d = (uint32_t)w[j];
+                raw[i * 4 + j] = d;
                 v[i * 8 + 2 * j] = (float)__builtin_bit_cast(_Float16, (uint16_t)(d & 0xffffu));
                 v[i * 8 + 2 * j + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(d >> 16));
             }
@@ -151,6 +201,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const uint32_t d = (uint32_t)w[j];
+                raw[i * 4 + j] = d;
                 v[i * 8 + 2 * j] = __builtin_bit_cast(float, d << 16);
                 v[i * 8 + 2 * j + 1] = __builtin_bit_cast(float, d & 0xffff0000u);
             }
@@ -165,24 +216,65 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
 
     if constexpr (OUT_FP8) {
         i32x4_t o[2];
+        if (byte != 0u && byte != 255u) {
+            const float ds = __builtin_bit_cast(float, byte << 23);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            uint32_t w = 0;
+            for (int i = 0; i < 8; ++i) {
+                uint32_t w = 0;
+                if constexpr (sizeof(InT) == 2) {
+                    w = cvt_fp8_pair<InT>(w, raw[2 * i], 0.f, 0.f, ds, false);
+                    w = cvt_fp8_pair<InT>(w, raw[2 * i + 1], 0.f, 0.f, ds, true);
+                } else {
+                    w = cvt_fp8_pair<float>(w, 0u, v[4 * i], v[4 * i + 1], ds, false);
+                    w = cvt_fp8_pair<float>(w, 0u, v[4 * i + 2], v[4 * i + 3], ds, true);
+                }
+                o[i / 4][i % 4] = (int)w;
+            }
+        } else {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) w |= f32_to_e4m3(v[i * 4 + j] * inv) << (8 * j);
-            o[i / 4][i % 4] = (int)w;
+            for (int i = 0; i < 8; ++i) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) w |= f32_to_e4m3(v[i * 4 + j] * inv) << (8 * j);
+                o[i / 4][i % 4] = (int)w;
+            }
         }
         uint8_t* dst = p.out + x * p.out_stride + (int64_t)y * 32;
         *reinterpret_cast<i32x4_t*>(dst) = o[0];
         *reinterpret_cast<i32x4_t*>(dst + 16) = o[1];
     } else {
         i32x4_t o;
+        if (byte != 0u && byte != 255u) {
+            // gfx950 v_cvt_scalef32_pk_fp4_*: two values / 2^(byte-127) -> two
+            // e2m1 nibbles (RNE, saturating at 6; the even element in the low
+            // nibble), placed in byte `sel` of the destination: the same
+            // codes as f32_to_e2m1(x * 2^(127-byte)) below for every finite
+            // input, in one instruction per pair
+            const float ds = __builtin_bit_cast(float, byte << 23);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            uint32_t w = 0;
+            for (int i = 0; i < 4; ++i) {
+                uint32_t w = 0;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) w |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
-            o[i] = (int)w;
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (std::is_same<InT, _Float16>::value)
+                        w = cvt_fp4_pair<_Float16>(w, raw[i * 4 + j], 0.f, 0.f, ds, j);
+                    else if constexpr (sizeof(InT) == 2)
+                        w = cvt_fp4_pair<uint16_t>(w, raw[i * 4 + j], 0.f, 0.f, ds, j);
+                    else
+                        w = cvt_fp4_pair<float>(w, 0u, v[i * 8 + 2 * j], v[i * 8 + 2 * j + 1], ds, j);
+                }
+                o[i] = (int)w;
+            }
+        } else {
+            // scale byte 0 (2^-127, a subnormal f32) or 255 (NaN): the
+            // integer conversion
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t w = 0;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) w |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
+                o[i] = (int)w;
+            }
         }
         int64_t off;
         if (p.shuffle_weight) {

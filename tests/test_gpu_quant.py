@@ -170,3 +170,46 @@ def test_quant_fp32_input(cuda):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(_u8(q), q_ref)
     np.testing.assert_array_equal(_u8(s), s_ref)
+
+
+_EXP_RANGE = {torch.float32: (-140, 40), torch.bfloat16: (-130, 40), torch.float16: (-22, 12)}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_quant_block_magnitudes(cuda, dtype, fp8):
+    """Every input dtype into e2m1 and e4m3, each 32-block scaled by its own
+    power of two across the dtype's whole range (down to subnormal inputs,
+    whose Even scale byte is 0), plus all-zero blocks; Even (dynamic_*) and
+    RoundUp (per_1x32_mx_quant_hip) scales, bytes equal to the oracle."""
+    import aiter_amd
+
+    m, k = 64, 1024
+    announce(f"quant block magnitudes {dtype} fp8={fp8}")
+    rs = np.random.default_rng(90)
+    lo, hi = _EXP_RANGE[dtype]
+    e = rs.integers(lo, hi, (m, k // 32))
+    x = rs.standard_normal((m, k)).astype(np.float32) * np.repeat(np.exp2(e.astype(np.float64)), 32, axis=1)
+    x[::7, 64:96] = 0.0                                     # all-zero blocks
+    xt = torch.from_numpy(x.astype(np.float32)).to(dtype)
+    xf = xt.float().numpy()
+    xd = xt.to(cuda)
+    if fp8:
+        q, s = aiter_amd.dynamic_mxfp8_quant(xd, shuffle=False)
+        q_ref, s_ref = O.quant_mxfp8(xf, O.EVEN)
+    else:
+        q, s = aiter_amd.dynamic_mxfp4_quant(xd, shuffle=False)
+        q_ref, s_ref = O.quant_mxfp4_triton_even(xf)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(_u8(s), s_ref)
+    np.testing.assert_array_equal(_u8(q), q_ref)
+    assert (s_ref == 0).any() or dtype == torch.float16    # the subnormal-scale branch is exercised
+    qd = aiter_amd.dtypes.fp8 if fp8 else aiter_amd.dtypes.fp4x2
+    q, s = aiter_amd.per_1x32_mx_quant_hip(xd, quant_dtype=qd, shuffle=False)
+    torch.cuda.synchronize()
+    if fp8:
+        q_ref, s_ref = O.quant_mxfp8(xf, O.ROUND_UP, amax_floor=1e-10)
+    else:
+        q_ref, s_ref = O.quant_mxfp4(xf, O.ROUND_UP, amax_floor=1e-10)
+    np.testing.assert_array_equal(_u8(s), s_ref)
+    np.testing.assert_array_equal(_u8(q), q_ref)
