@@ -6,6 +6,7 @@ Ops (all backed by hand-written HIP kernels in libaiter_amd.so):
   gemm_a16w16, tgemm.mm, gemm_a16w16_opus, gemm_a16w16_asm bf16
   get_hip_quant / get_triton_quant(QuantType.per_1x32), quant_mxfp4_hip,
   per_1x32_mx_quant_hip, dynamic_mxfp4_quant, dynamic_mxfp8_quant
+  fused_rms_mxfp4_quant, fused_rms_mxfp8_quant            RMSNorm -> MX quant
   shuffle_weight, shuffle_scale
 The GEMMs and quantisers are also torch custom ops, torch.ops.aiter_amd.<name>
 (torch_ops.py), with fake implementations for torch.compile / torch.export.
@@ -14,6 +15,7 @@ from . import dtypes
 from .gemm_common import get_padded_m
 from .gemm_op_a4w4 import (compute_gemm_SplitK, gemm_a4w4, gemm_a4w4_asm, gemm_a4w4_blockscale,
                            gemm_a4w4_blockscale_tune, get_GEMM_config)
+from .fused_quant import fused_rms_mxfp4_quant, fused_rms_mxfp8_quant
 from .gemm_op_a8w4 import gemm_a8w4_mxfp8, gemm_a8w4_mxfp8_dynamic
 from .gemm_op_a16w16 import gemm_a16w16_asm
 from .opus import gemm_a16w16_opus, opus_gemm_a16w16_tune, opus_gemm_workspace_init

@@ -101,6 +101,8 @@ SIGNATURES = {
                      ctypes.c_int, _S], ctypes.c_int),
     "dynamic_mxfp4_quant": ([_T, _T, _T, ctypes.c_int, _S], ctypes.c_int),
     "dynamic_mxfp8_quant": ([_T, _T, _T, ctypes.c_int, _S], ctypes.c_int),
+    "fused_rms_mx_quant": ([_T, _T, ctypes.c_float, _T, _T, ctypes.c_float, _T, _T, _T, _T, _T, _T, ctypes.c_int,
+                            ctypes.c_int, _S], ctypes.c_int),
     "aiter_amd_num_kernels": ([], ctypes.c_int),
     "aiter_amd_kernel_info": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
     "gemm_workspace_reserve": ([ctypes.c_int, _S, ctypes.c_size_t], ctypes.c_int),

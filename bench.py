@@ -211,6 +211,14 @@ def bench_extra(dev):
     tq = time_graph(lambda: aiter_amd.per_1x32_mx_quant_hip(xa, shuffle=True), 20, 2)
     out["mxfp4_quant_8192x8192"] = {"us": round(tq * 1e6, 1),
                                     "GBps": round(8192 * 8192 * (2 + 0.5 + 1 / 32) / tq / 1e9, 1)}
+    # fused RMSNorm -> MXFP4 quant prologue vs RMSNorm (torch, bf16 out) then the quantiser
+    wa = torch.randn(8192, generator=g).to(torch.bfloat16).to(dev)
+    tf = time_graph(lambda: aiter_amd.fused_rms_mxfp4_quant(xa, wa, 1e-6, shuffle=True), 20, 2)
+    tu = time_graph(lambda: aiter_amd.per_1x32_mx_quant_hip(
+        torch.nn.functional.rms_norm(xa, (8192,), wa, eps=1e-6), shuffle=True), 20, 2)
+    out["fused_rms_mxfp4_quant_8192x8192"] = {"us": round(tf * 1e6, 1),
+                                              "GBps": round(8192 * 8192 * (2 + 0.5 + 1 / 32) / tf / 1e9, 1),
+                                              "unfused_us": round(tu * 1e6, 1)}
     return out
 
 

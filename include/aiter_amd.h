@@ -140,6 +140,22 @@ int dynamic_mxfp4_quant(aiter_tensor_t* x, aiter_tensor_t* x_fp4, aiter_tensor_t
 int dynamic_mxfp8_quant(aiter_tensor_t* x, aiter_tensor_t* y, aiter_tensor_t* scale,
                         int shuffle, aiter_stream_t stream);
 
+/* Fused RMSNorm -> MX quant prologue: the entry behind fused_rms_mxfp4_quant
+ * (aiter/ops/triton/quant/fused_mxfp4_quant.py:23-147) and
+ * fused_rms_mxfp8_quant (aiter/ops/triton/quant/fused_mxfp8_quant.py:22-76),
+ * which launch Triton kernels in the reference.  x1 [M, N1] (N1 % 32 == 0,
+ * N1 <= 32768) + optional res1 -> out_res1, RMSNorm with x1_weight / eps1 in
+ * f32 -> optional out1, Even-scale MX quant into out_q ([M, N1/2] u8 e2m1
+ * pairs, or [M, N1] fp8 e4m3) and out_scale ([M, N1/32], or shuffled
+ * [pad256(M), pad8(N1/32)] when shuffle=1; pad_scale=1 writes 127 into the
+ * padding columns of each row, as the reference does).  Optional x2 [M, N2]
+ * with x2_weight / eps2 -> out2 (RMSNorm only).  NULL for every absent
+ * tensor. */
+int fused_rms_mx_quant(aiter_tensor_t* x1, aiter_tensor_t* x1_weight, float eps1, aiter_tensor_t* x2,
+                       aiter_tensor_t* x2_weight, float eps2, aiter_tensor_t* res1, aiter_tensor_t* out_q,
+                       aiter_tensor_t* out_scale, aiter_tensor_t* out1, aiter_tensor_t* out2,
+                       aiter_tensor_t* out_res1, int shuffle, int pad_scale, aiter_stream_t stream);
+
 /* ---- library introspection and workspace --------------------------------
  * The reference keeps its kernel list in per-arch CSVs next to its ASM code
  * objects (hsa/gfx950/f4gemm/f4gemm_bf16_per1x32Fp4.csv) and the CK instance

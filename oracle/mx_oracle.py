@@ -492,6 +492,40 @@ def get_padded_m(m: int, n: int, k: int, gl: int) -> int:
     return m
 
 
+# --------------------------------------------------------------------------
+# Fused RMSNorm -> MX quant prologue
+# --------------------------------------------------------------------------
+
+def rms_norm_f32(x: np.ndarray, w: np.ndarray, eps: float, res: np.ndarray | None = None):
+    """RMSNorm in f32 as the fused Triton kernels compute it
+    (aiter/ops/triton/_triton_kernels/quant/fused_mxfp4_quant.py:8-17 and
+    :119-147; fused_mxfp8_quant.py, _fused_rms_mxfp8_kernel): optional
+    residual added in f32 first, then ``row * rsqrt(mean(row**2) + eps) *
+    weight`` (multiplied in that order).  Returns (normed f32, x + res f32).
+    The sum of squares is an f32 reduction whose order the reference leaves
+    to Triton; here it is numpy's pairwise sum, so results agree with any
+    other order to f32 rounding only."""
+    xf = np.asarray(x, dtype=np.float32)
+    if res is not None:
+        xf = (xf + np.asarray(res, dtype=np.float32)).astype(np.float32)
+    ss = np.sum(xf * xf, axis=-1, dtype=np.float32)
+    nf = (np.float32(1.0) / np.sqrt(ss / np.float32(xf.shape[-1]) + np.float32(eps))).astype(np.float32)
+    y = (xf * nf[..., None]).astype(np.float32) * np.asarray(w, dtype=np.float32)
+    return y.astype(np.float32), xf
+
+
+def fused_rms_mx_quant_ref(x, w, eps, fp8: bool, res=None):
+    """fused_rms_mxfp4_quant / fused_rms_mxfp8_quant on one input
+    (aiter/ops/triton/quant/fused_mxfp4_quant.py:23-147,
+    aiter/ops/triton/quant/fused_mxfp8_quant.py:22-76): RMSNorm in f32, then
+    the Even-scale quant of the f32 result (the Triton _mxfp4_quant_op /
+    _mxfp8_quant_op, aiter/ops/triton/_triton_kernels/quant/quant.py:86-160,
+    380-397).  Returns (q, scale [M, K/32], normed f32, x + res f32)."""
+    y, xr = rms_norm_f32(x, w, eps, res)
+    q, s = quant_mxfp8(y, EVEN) if fp8 else quant_mxfp4_triton_even(y)
+    return q, s, y, xr
+
+
 # How each function above is pinned (checked by tests/test_oracle.py).
 PINNED = {
     "e2m1_decode": "OCP closed form 2**(e-1)*(1+m/2) + FP4 grid known answer",
@@ -509,4 +543,8 @@ PINNED = {
     "shuffle_scale": "three formulations agree: permute, mx_scale_shuffle_idx, Triton store",
     "gemm_*_ref": "float64 brute force on tiny shapes",
     "get_padded_m": "tuned CSV keys (aiter/configs/a4w4_blockscale_tuned_gemm.csv)",
+    "rms_norm_f32": "torch.nn.functional.rms_norm (library routine) in f32, and an exact case "
+                    "(constant-magnitude power-of-two rows, eps 0: the factor is an exact power of two)",
+    "fused_rms_mx_quant_ref": "composition of rms_norm_f32 and the pinned Even quants; exact case "
+                              "bit-equal to quantising +-weight directly",
 }

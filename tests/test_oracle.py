@@ -303,3 +303,35 @@ def test_get_padded_m_known_answers():
         [16, 16, 32, 256, 288, 1024, 1088, 4224]
     assert [O.get_padded_m(m, 4096, 4096, 1) for m in (1, 3, 33, 1000, 9000)] == [1, 4, 64, 1024, 16384]
     assert O.get_padded_m(9000, 8192, 1024, 1) == 8192
+
+
+def test_rms_norm_f32_vs_torch():
+    """rms_norm_f32 against torch's own RMSNorm (a library routine), f32."""
+    import torch
+
+    rs = np.random.default_rng(11)
+    x = rs.standard_normal((5, 1536)).astype(np.float32) * 3
+    res = rs.standard_normal((5, 1536)).astype(np.float32)
+    w = rs.standard_normal(1536).astype(np.float32)
+    y, xr = O.rms_norm_f32(x, w, 1e-6, res)
+    want = torch.nn.functional.rms_norm(torch.from_numpy(x + res), (1536,), torch.from_numpy(w), eps=1e-6)
+    np.testing.assert_allclose(y, want.numpy(), rtol=2e-6, atol=2e-6)
+    np.testing.assert_array_equal(xr, (x + res).astype(np.float32))
+
+
+def test_fused_rms_quant_exact_case():
+    """Rows of constant magnitude 2**e with eps = 0: the norm factor is
+    exactly 2**-e, the normalised row is exactly +-weight, so the fused
+    quant must equal the plain quant of +-weight bit for bit."""
+    rs = np.random.default_rng(12)
+    k = 1024
+    e = rs.integers(-20, 20, 6)
+    signs = rs.choice([-1.0, 1.0], (6, k)).astype(np.float32)
+    x = signs * np.exp2(e.astype(np.float32))[:, None]
+    w = (rs.standard_normal(k) * 2).astype(np.float32)
+    for fp8 in (False, True):
+        q, s, y, _ = O.fused_rms_mx_quant_ref(x, w, 0.0, fp8)
+        np.testing.assert_array_equal(y, signs * w)
+        q2, s2 = O.quant_mxfp8(signs * w, O.EVEN) if fp8 else O.quant_mxfp4_triton_even(signs * w)
+        np.testing.assert_array_equal(q, q2)
+        np.testing.assert_array_equal(s, s2)
