@@ -103,6 +103,13 @@ SIGNATURES = {
     "dynamic_mxfp8_quant": ([_T, _T, _T, ctypes.c_int, _S], ctypes.c_int),
     "fused_rms_mx_quant": ([_T, _T, ctypes.c_float, _T, _T, ctypes.c_float, _T, _T, _T, _T, _T, _T, ctypes.c_int,
                             ctypes.c_int, _S], ctypes.c_int),
+    "moe_sorting_fwd": ([_T] * 7 + [ctypes.c_int, ctypes.c_int, _T, _T, ctypes.c_int, _S], ctypes.c_int),
+    "fused_dynamic_mx_quant_moe_sort_hip": ([_T] * 5 + [ctypes.c_int] * 3 + [_T, _S], ctypes.c_int),
+    "mxfp4_moe_sort_hip": ([_T] * 4 + [ctypes.c_int] * 2 + [_S], ctypes.c_int),
+    "ck_moe_stage1": ([_T] * 7 + [ctypes.c_int, ctypes.c_char_p, _T, _T, ctypes.c_int, _T] + [ctypes.c_int] * 4
+                      + [ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
+    "ck_moe_stage2": ([_T] * 7 + [ctypes.c_int, ctypes.c_char_p, _T, _T, ctypes.c_int, _T] + [ctypes.c_int] * 4
+                      + [ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
     "aiter_amd_num_kernels": ([], ctypes.c_int),
     "aiter_amd_kernel_info": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
     "gemm_workspace_reserve": ([ctypes.c_int, _S, ctypes.c_size_t], ctypes.c_int),

@@ -14,7 +14,7 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
-SOURCES = ["gemm.hip", "quant.hip", "fused_quant.hip"]
+SOURCES = ["gemm.hip", "quant.hip", "fused_quant.hip", "moe_sorting.hip", "moe_gemm.hip"]
 LIB = os.path.join(PKG, "libaiter_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

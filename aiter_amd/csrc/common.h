@@ -125,6 +125,11 @@ struct DeviceGuard {
 
 int device_cu_count(int dev);
 
+// Library-owned device scratch of (device, stream), grown on demand (never
+// inside graph capture: that raises); shared by the split-K GEMMs and the
+// MoE sort, which are stream-ordered on one stream.
+void* lib_workspace(int dev, hipStream_t st, size_t bytes);
+
 }  // namespace aiter_amd
 
 // ---------------------------------------------------------------------------

@@ -520,7 +520,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             const size_t need = (size_t)M * N * sizeof(float);
             p.ws = workspace(dev, stream, need);
             const int64_t n4 = (int64_t)M * N;
-            fill_zero_kernel<<<dim3((unsigned)((n4 / 4 + 255) / 256 + 1)), 256, 0, stream>>>(p.ws, n4);
+            fill_zero_kernel<><<<dim3((unsigned)((n4 / 4 + 255) / 256 + 1)), 256, 0, stream>>>(p.ws, n4);
             inst->fn(p, grid, stream);
             if (c.var.out_f32)
                 splitk_finish_kernel<true><<<dim3((unsigned)((n4 / 4 + 255) / 256)), 256, 0, stream>>>(p);
@@ -543,6 +543,9 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
 }
 
 }  // namespace
+
+void* lib_workspace(int dev, hipStream_t st, size_t bytes) { return workspace(dev, st, bytes); }
+
 }  // namespace aiter_amd
 
 using namespace aiter_amd;

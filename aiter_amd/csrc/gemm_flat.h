@@ -45,13 +45,51 @@ struct FlatCfg {
     static constexpr int K_STAGE = MX ? 256 : 64;     // K elements per stage (128 bytes of a row)
 };
 
+// MoE stages (the two grouped GEMMs of fused_moe) on the same main loop.
+// Row block b of the sorted routing list (see moe_sorting.hip) belongs to
+// expert sorted_eids[b]: B and its scales are that expert's slices, and the
+// A rows are gathered through sorted_ids (slot << 24 | token; padding entries
+// point past the end of A, whose range check returns zeros).  A's scales are
+// already in sorted order.  Stage 1 pairs gate and up rows of B in one tile
+// (wave w: gate rows n0 + 32w.., up rows inter + n0 + 32w..), so one lane
+// holds gate and up of the same output element and the epilogue writes
+// act(gate) * up as bf16 to row token * topk + slot.  Stage 2 scales by the
+// routing weight and adds into the token's output row with packed bf16
+// atomics (the order of the topk additions is not fixed).
+enum MoeStage : int { kMoeNone = 0, kMoeStage1 = 1, kMoeStage2 = 2 };
+enum MoeAct : int { kActSilu = 0, kActGelu = 1 };
+
+struct MoeParams {
+    const int* sorted_ids;
+    const int* sorted_eids;
+    const int* num_valid;       // [0]: entries of the sorted list incl. padding
+    const float* sorted_w;      // routing weight per sorted entry (null: 1)
+    uint16_t* out;              // bf16
+    int64_t out_stride;         // elements per output row
+    int64_t b_expert_bytes;     // bytes of one expert's B / B scales
+    int64_t bs_expert_bytes;
+    int64_t a_rows;             // rows of A (gathered rows must stay below)
+    int sorted_len;             // entries of sorted_ids (later positions are padding)
+    int token_num, topk, inter, n_experts, act;
+};
+
+AA_DEV void atomic_add_bf16x2(uint16_t* addr, uint32_t v) {
+    asm volatile("global_atomic_pk_add_bf16 %0, %1, off" : : "v"(addr), "v"(v) : "memory");
+}
+
+AA_DEV float moe_act(float g, int act) {
+    if (act == kActGelu) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
+    return g / (1.0f + __expf(-g));
+}
+
 // BPRE = false: B row-major [N, K].  The 32x32 MFMA's B operand is then 16
 // contiguous bytes of one row per lane (row l%32, bytes 16*(l/32) of the
 // k-step's 32-byte window), so row-major B also loads straight into VGPRs;
 // one load touches 32 rows (32 bytes each), and the four k-steps of a stage
 // consume each row's 128-byte line.
-template <int KA, int BM, bool OUT_F32, bool BPRE = true>
-__global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
+template <int KA, int BM, bool OUT_F32, bool BPRE, int MOE>
+AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
+    static_assert(MOE == kMoeNone || (BPRE && !OUT_F32), "MoE stages: preshuffled B, bf16 output");
     using Cfg = FlatCfg<KA, BM>;
     constexpr int BN = 256;
     constexpr int NS = Cfg::NS;
@@ -77,29 +115,56 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
 
     int tm, tn;
-    tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
-    const int m0 = tm * BM, n0 = tn * BN;
+    const uint8_t* b_base = p.B;
+    const uint8_t* bs_base = p.Bs;
+    if constexpr (MOE != kMoeNone) {
+        tn = blockIdx.x;
+        tm = blockIdx.y;
+        if (tm * BM >= mq.num_valid[0]) return;   // whole workgroup: past the sorted list
+        const int e = mq.sorted_eids[tm];
+        if (e < 0 || e >= mq.n_experts) return;
+        b_base += (int64_t)e * mq.b_expert_bytes;
+        bs_base += (int64_t)e * mq.bs_expert_bytes;
+    } else {
+        tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
+    }
+    // stage 1: 128 output columns per tile (128 gate + 128 up rows of B)
+    const int m0 = tm * BM, n0 = (MOE == kMoeStage1) ? tn * (BN / 2) : tn * BN;
     const int nstages = p.K / Cfg::K_STAGE;
 
     // ---- A: chunk c = half*(BM/8) + 8-row block; lane l -> row l/8, stored piece l%8
     //      holding global 16-byte piece (l%8) ^ swz(row), swz(r) = (r>>1)&7
-    const __amdgpu_buffer_rsrc_t a_rsrc = make_rsrc(p.A + (int64_t)m0 * p.lda, (int64_t)(p.M - m0) * p.lda);
+    const __amdgpu_buffer_rsrc_t a_rsrc = (MOE != kMoeNone)
+                                              ? make_rsrc(p.A, mq.a_rows * p.lda)
+                                              : make_rsrc(p.A + (int64_t)m0 * p.lda, (int64_t)(p.M - m0) * p.lda);
     int a_off[NA];
 #pragma unroll
     for (int q = 0; q < NA; ++q) {
         const int c = wave + 4 * q;
         const int half = c / (BM / 8), rb = c % (BM / 8);
         const int r = rb * 8 + (lane >> 3);
-        a_off[q] = r * (int)p.lda + half * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16);
+        int row = r;
+        if constexpr (MOE != kMoeNone) {
+            // A row of sorted entry m0 + r; padding -> a_rows (reads zeros)
+            const int id = m0 + r < mq.sorted_len ? mq.sorted_ids[m0 + r] : mq.token_num;
+            const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+            row = (tok >= mq.token_num || slot >= mq.topk) ? (int)mq.a_rows
+                                                           : (MOE == kMoeStage1 ? tok : tok * mq.topk + slot);
+        }
+        a_off[q] = row * (int)p.lda + half * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16);
     }
     // ---- B preshuffled (16,16): tile j of wave w = 16-row blocks 4w+2j, 4w+2j+1;
     //      k-step s of stage t at blk*16*ldb + (4t+s)*512 + (l/32)*256 + (l%16)*16
     //      B row-major: row 64w+32j+l%32 at (4t+s)*32 + (l/32)*16
-    const __amdgpu_buffer_rsrc_t b_rsrc = make_rsrc(p.B + (int64_t)n0 * p.ldb, (int64_t)(p.N - n0) * p.ldb);
+    const __amdgpu_buffer_rsrc_t b_rsrc = (MOE != kMoeNone)
+                                              ? make_rsrc(b_base, (int64_t)p.N * p.ldb)
+                                              : make_rsrc(p.B + (int64_t)n0 * p.ldb, (int64_t)(p.N - n0) * p.ldb);
     int b_off[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        const int blk = 4 * wave + 2 * j + ((lane >> 4) & 1);
+        int blk = 4 * wave + 2 * j + ((lane >> 4) & 1);
+        if constexpr (MOE == kMoeStage1) blk = ((j ? mq.inter : 0) + n0 + 32 * wave) / 16 + ((lane >> 4) & 1);
+        if constexpr (MOE == kMoeStage2) blk += n0 / 16;
         if constexpr (BPRE)
             b_off[j] = blk * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
         else
@@ -110,12 +175,21 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     const __amdgpu_buffer_rsrc_t sa_rsrc =
         make_rsrc(p.As + (int64_t)ga0 * 32 * p.sa_stride, (int64_t)(p.sa_groups - ga0) * 32 * p.sa_stride);
     const __amdgpu_buffer_rsrc_t sb_rsrc =
-        make_rsrc(p.Bs + (int64_t)gb0 * 32 * p.sb_stride, (int64_t)(p.sb_groups - gb0) * 32 * p.sb_stride);
+        (MOE != kMoeNone)
+            ? make_rsrc(bs_base, (int64_t)p.sb_groups * 32 * p.sb_stride)
+            : make_rsrc(p.Bs + (int64_t)gb0 * 32 * p.sb_stride, (int64_t)(p.sb_groups - gb0) * 32 * p.sb_stride);
     const __amdgpu_buffer_rsrc_t null_rsrc = make_rsrc(p.A, 0);
     const bool sc_is_a = wave < SCA;
     const bool sc_is_b = wave >= SCA && wave < SCA + 2;
     const int sc_chunk = sc_is_a ? wave : (sc_is_b ? wave - SCA : 0);
-    const int sc_off = (4 * sc_chunk + (lane >> 4)) * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + (lane & 15) * 16;
+    int sc_group = 4 * sc_chunk + (lane >> 4);
+    if constexpr (MOE == kMoeStage1) {
+        if (sc_is_b) sc_group = (sc_chunk ? mq.inter / 32 : 0) + gb0 + (lane >> 4);   // chunk 0 gate, 1 up
+    }
+    if constexpr (MOE == kMoeStage2) {
+        if (sc_is_b) sc_group += gb0;
+    }
+    const int sc_off = sc_group * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + (lane & 15) * 16;
     const __amdgpu_buffer_rsrc_t sc_rsrc = sc_is_a ? sa_rsrc : (sc_is_b ? sb_rsrc : null_rsrc);
 
     auto dma_stage = [&](int t) {
@@ -175,7 +249,8 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
         }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            const uint8_t* g = base + SCA * 1024 + (2 * wave + j) * 256;
+            const int bg = (MOE == kMoeStage1) ? 4 * j + wave : 2 * wave + j;
+            const uint8_t* g = base + SCA * 1024 + bg * 256;
             const unsigned d0 = *reinterpret_cast<const unsigned*>(g);
             const unsigned d1 = *reinterpret_cast<const unsigned*>(g + 128);
             pb[j] = (int)__builtin_amdgcn_perm(d1, d0, sc_perm);
@@ -315,8 +390,57 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
     constexpr int EP_MP = (MA * 32 * 64 * EB <= WAVE_SCRATCH) ? MA : MA / 2;
     static_assert(MA % EP_MP == 0 && EP_MP * 32 * 64 * EB <= WAVE_SCRATCH, "epilogue pass fits the ring");
     wait_vmcnt<0>();
+    if constexpr (MOE != kMoeNone) {
+        // lane: row 32i + l%32 of the tile, columns 8q + 4(l/32) + r of each 32-column tile
+#pragma unroll
+        for (int i = 0; i < MA; ++i) {
+            const int pos = m0 + 32 * i + (lane & 31);
+            if (pos >= mq.sorted_len) continue;
+            const int id = mq.sorted_ids[pos];
+            const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+            if (tok >= mq.token_num || slot >= mq.topk) continue;
+            const float wgt = mq.sorted_w ? mq.sorted_w[pos] : 1.0f;
+            if constexpr (MOE == kMoeStage1) {
+                uint16_t* orow = mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + n0 + 32 * wave +
+                                 4 * (lane >> 5);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        v[r] = moe_act(acc[i][0][4 * q + r] * wgt, mq.act) * (acc[i][1][4 * q + r] * wgt);
+                    uint2 o;
+                    o.x = pack_bf16x2(v[0], v[1]);
+                    o.y = pack_bf16x2(v[2], v[3]);
+                    *reinterpret_cast<uint2*>(orow + 8 * q) = o;
+                }
+            } else {
+                uint16_t* orow = mq.out + (int64_t)tok * mq.out_stride + n0 + 64 * wave + 4 * (lane >> 5);
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x16v_t& a = acc[i][j];
+                        atomic_add_bf16x2(orow + 32 * j + 8 * q, pack_bf16x2(a[4 * q] * wgt, a[4 * q + 1] * wgt));
+                        atomic_add_bf16x2(orow + 32 * j + 8 * q + 2,
+                                          pack_bf16x2(a[4 * q + 2] * wgt, a[4 * q + 3] * wgt));
+                    }
+            }
+        }
+        return;
+    }
     __syncthreads();
     store_block_any<MA, NB, EP_MP, OUT_F32>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0, n0 + wave * 64);
+}
+
+template <int KA, int BM, bool OUT_F32, bool BPRE = true>
+__global__ __launch_bounds__(256, 1) void gemm_flat_kernel(GemmParams p) {
+    flat_body<KA, BM, OUT_F32, BPRE, kMoeNone>(p, MoeParams{});
+}
+
+template <int KA, int BM, int MOE>
+__global__ __launch_bounds__(256, 1) void moe_flat_kernel(GemmParams p, MoeParams mq) {
+    flat_body<KA, BM, false, true, MOE>(p, mq);
 }
 
 }  // namespace aiter_amd

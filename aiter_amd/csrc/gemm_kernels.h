@@ -506,6 +506,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p, int sp
     store_frag<OUT_F32>(p, v, m, n);
 }
 
+template <int = 0>
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int64_t n) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i + 4 <= n) *reinterpret_cast<f32x4_t*>(p + i) = f32x4_t{0.f, 0.f, 0.f, 0.f};

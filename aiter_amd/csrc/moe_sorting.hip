@@ -1,0 +1,305 @@
+// MoE token sorting for gfx950: groups the (token, slot) routing entries by
+// expert, pads every expert's run to a multiple of the GEMM row block, and
+// records the expert of each row block (aiter's moe_sorting_fwd,
+// aiter/ops/moe_sorting.py:12-27; output format restated from the reference
+// CPU sort op_tests/test_moe_sorting.py:45-98):
+//
+//   sorted_ids[p]        = slot << 24 | token, experts in order, tokens in
+//                          increasing (token, slot) order inside an expert;
+//                          padding = topk << 24 | M
+//   sorted_weights[p]    = topk_weights[token, slot] (padding: 0)
+//   sorted_expert_ids[b] = expert of row block b, renumbered over the experts
+//                          the mask keeps (unused blocks: -1)
+//   num_valid_ids        = {padded entry count, token count}
+//
+// The order inside an expert is fixed (a stable counting sort), so the output
+// is deterministic.  Entries are processed in chunks of 1024 (one workgroup
+// of 16 waves): each wave ranks its 64 entries among equal experts with a
+// ballot per distinct expert, and per-wave counts in LDS give each wave its
+// offset inside the chunk.  Up to kSingleChunks chunks run in one workgroup
+// (count, scan, place); more take three launches: per-chunk counts, one scan
+// over chunks and experts, and one placement workgroup per chunk.
+#include "common.h"
+
+namespace {
+
+constexpr int kThreads = 1024;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxE = 1024;
+constexpr int kSingleChunks = 4;
+
+struct SortParams {
+    const int* topk_ids;
+    const float* topk_w;
+    int* sorted_ids;
+    float* sorted_w;
+    int* sorted_eids;
+    int* num_valid;
+    const int* expert_mask;   // [E], 0 drops the expert (may be null)
+    const int* num_local;     // device token count (may be null)
+    int* ws;                  // chunk counts [nchunks][E], then expert offsets [E]
+    int64_t ids_stride, w_stride;   // elements per row of topk_ids / topk_weights
+    int M, topk, E, bs, max_padded, max_blocks, nchunks;
+};
+
+struct SortSmem {
+    int cnt[kMaxE];        // entries per expert
+    int off[kMaxE + 1];    // padded start of each expert, then the total
+    int base[kMaxE];       // next output position of each expert
+    int scan[kMaxE];
+    int lid[kMaxE];        // renumbered expert id
+    uint8_t wcnt[kWaves][kMaxE];
+};
+
+__device__ __forceinline__ int local_tokens(const SortParams& p) {
+    return p.num_local ? min(max(*p.num_local, 0), p.M) : p.M;
+}
+
+// expert of entry i (token i / topk, slot i % topk), -1 if dropped
+__device__ __forceinline__ int expert_of(const SortParams& p, int i, int n) {
+    if (i >= n) return -1;
+    const int t = i / p.topk, s = i - t * p.topk;
+    const int e = p.topk_ids[(int64_t)t * p.ids_stride + s];
+    if (e < 0 || e >= p.E) return -1;
+    if (p.expert_mask && p.expert_mask[e] == 0) return -1;
+    return e;
+}
+
+// exclusive scan of v over the workgroup's threads (one value per thread)
+__device__ int block_exclusive_scan(int v, int* buf) {
+    const int tid = threadIdx.x;
+    buf[tid] = v;
+    __syncthreads();
+    for (int d = 1; d < kThreads; d <<= 1) {
+        const int add = tid >= d ? buf[tid - d] : 0;
+        __syncthreads();
+        buf[tid] += add;
+        __syncthreads();
+    }
+    const int incl = buf[tid];
+    __syncthreads();
+    return incl - v;
+}
+
+// from sm.cnt: expert offsets, block -> expert table, padding entries,
+// num_valid_ids; leaves sm.off / sm.lid set
+__device__ void scan_experts(const SortParams& p, SortSmem& sm, int n_tokens) {
+    const int e = threadIdx.x;
+    const bool live = e < p.E;
+    const bool kept = live && !(p.expert_mask && p.expert_mask[e] == 0);
+    const int c = live ? sm.cnt[e] : 0;
+    const int padded = (c + p.bs - 1) / p.bs * p.bs;
+    const int start = block_exclusive_scan(padded, sm.scan);
+    const int lid = block_exclusive_scan(kept ? 1 : 0, sm.scan);
+    if (live) {
+        sm.off[e] = start;
+        sm.lid[e] = lid;
+    }
+    if (e == p.E - 1) sm.off[p.E] = start + padded;
+    __syncthreads();
+    const int total = sm.off[p.E];
+    const int pad_id = (p.topk << 24) | p.M;
+    if (live) {
+        for (int b = start / p.bs; b < (start + padded) / p.bs && b < p.max_blocks; ++b) p.sorted_eids[b] = lid;
+        for (int q = start + c; q < start + padded && q < p.max_padded; ++q) {
+            p.sorted_ids[q] = pad_id;
+            p.sorted_w[q] = 0.0f;
+        }
+    }
+    for (int q = total + threadIdx.x; q < p.max_padded; q += kThreads) {
+        p.sorted_ids[q] = pad_id;
+        p.sorted_w[q] = 0.0f;
+    }
+    for (int b = total / p.bs + threadIdx.x; b < p.max_blocks; b += kThreads) p.sorted_eids[b] = -1;
+    if (threadIdx.x == 0) {
+        p.num_valid[0] = total;
+        p.num_valid[1] = n_tokens;
+    }
+}
+
+// places entries [c0, c0 + 1024) at sm.base[e] onward and advances sm.base
+__device__ void place_chunk(const SortParams& p, SortSmem& sm, int c0, int n) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    reinterpret_cast<i32x4_t*>(&sm.wcnt[0][0])[tid] = i32x4_t{0, 0, 0, 0};
+    static_assert(sizeof(sm.wcnt) == kThreads * 16, "one 16-byte clear per thread");
+    __syncthreads();
+    const int i = c0 + tid;
+    const int e = expert_of(p, i, n);
+    // rank among the lanes of this wave with the same expert and a lower lane
+    uint64_t act = __ballot(e >= 0);
+    const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int rank = 0;
+    while (act) {
+        const int leader = __builtin_ctzll(act);
+        const int le = __builtin_amdgcn_readlane(e, leader);
+        const uint64_t m = __ballot(e == le);
+        if (e == le) rank = __popcll(m & below);
+        if (lane == leader) sm.wcnt[w][le] = (uint8_t)__popcll(m);
+        act &= ~m;
+    }
+    __syncthreads();
+    if (e >= 0) {
+        int pos = sm.base[e] + rank;
+        for (int v = 0; v < w; ++v) pos += sm.wcnt[v][e];
+        const int t = i / p.topk, s = i - t * p.topk;
+        if (pos < p.max_padded) {
+            p.sorted_ids[pos] = (s << 24) | t;
+            p.sorted_w[pos] = p.topk_w[(int64_t)t * p.w_stride + s];
+        }
+    }
+    __syncthreads();
+    for (int x = tid; x < p.E; x += kThreads) {
+        int add = 0;
+        for (int v = 0; v < kWaves; ++v) add += sm.wcnt[v][x];
+        sm.base[x] += add;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kThreads) void moe_sort_single(SortParams p) {
+    __shared__ SortSmem sm;
+    const int nt = local_tokens(p);
+    const int n = nt * p.topk;
+    for (int x = threadIdx.x; x < kMaxE; x += kThreads) sm.cnt[x] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const int e = expert_of(p, i, n);
+        if (e >= 0) atomicAdd(&sm.cnt[e], 1);
+    }
+    __syncthreads();
+    scan_experts(p, sm, nt);
+    for (int x = threadIdx.x; x < p.E; x += kThreads) sm.base[x] = sm.off[x];
+    __syncthreads();
+    for (int c0 = 0; c0 < n; c0 += kThreads) place_chunk(p, sm, c0, n);
+}
+
+__global__ __launch_bounds__(kThreads) void moe_sort_count(SortParams p) {
+    __shared__ int cnt[kMaxE];
+    const int n = local_tokens(p) * p.topk;
+    for (int x = threadIdx.x; x < p.E; x += kThreads) cnt[x] = 0;
+    __syncthreads();
+    const int e = expert_of(p, blockIdx.x * kThreads + threadIdx.x, n);
+    if (e >= 0) atomicAdd(&cnt[e], 1);
+    __syncthreads();
+    for (int x = threadIdx.x; x < p.E; x += kThreads) p.ws[(int64_t)blockIdx.x * p.E + x] = cnt[x];
+}
+
+__global__ __launch_bounds__(kThreads) void moe_sort_scan(SortParams p) {
+    __shared__ SortSmem sm;
+    const int e = threadIdx.x;
+    if (e < p.E) {
+        // chunk counts -> exclusive prefix over chunks (the chunk's start inside the expert)
+        int run = 0;
+        for (int c = 0; c < p.nchunks; ++c) {
+            int* q = p.ws + (int64_t)c * p.E + e;
+            const int v = *q;
+            *q = run;
+            run += v;
+        }
+        sm.cnt[e] = run;
+    }
+    __syncthreads();
+    scan_experts(p, sm, local_tokens(p));
+    if (e < p.E) p.ws[(int64_t)p.nchunks * p.E + e] = sm.off[e];
+}
+
+__global__ __launch_bounds__(kThreads) void moe_sort_place(SortParams p) {
+    __shared__ SortSmem sm;
+    const int n = local_tokens(p) * p.topk;
+    for (int x = threadIdx.x; x < p.E; x += kThreads)
+        sm.base[x] = p.ws[(int64_t)p.nchunks * p.E + x] + p.ws[(int64_t)blockIdx.x * p.E + x];
+    __syncthreads();
+    place_chunk(p, sm, blockIdx.x * kThreads, n);
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint8_t* dst, int64_t bytes) {
+    const int64_t n16 = bytes / 16;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        reinterpret_cast<i32x4_t*>(dst)[i] = i32x4_t{0, 0, 0, 0};
+    for (int64_t i = n16 * 16 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes; i += stride) dst[i] = 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aiter_tensor_t* sorted_token_ids,
+                    aiter_tensor_t* sorted_weights, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
+                    aiter_tensor_t* moe_buf, int num_experts, int unit_size, aiter_tensor_t* local_expert_mask,
+                    aiter_tensor_t* num_local_tokens, int dispatch_policy, aiter_stream_t stream) {
+    using namespace aiter_amd;
+    return safe_call([&] {
+        check_tensor(topk_ids, "topk_ids", 2);
+        check_tensor(topk_weights, "topk_weights", 2);
+        check_tensor(sorted_token_ids, "sorted_token_ids", 1);
+        check_tensor(sorted_weights, "sorted_weights", 1);
+        check_tensor(sorted_expert_ids, "sorted_expert_ids", 1);
+        check_tensor(num_valid_ids, "num_valid_ids", 1);
+        DeviceGuard g(topk_ids->device_id);
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        AA_CHECK(topk_ids->dtype == AITER_DTYPE_i32, "topk_ids must be int32");
+        AA_CHECK(topk_weights->dtype == AITER_DTYPE_fp32, "topk_weights must be float32");
+        AA_CHECK(sorted_token_ids->dtype == AITER_DTYPE_i32 && sorted_expert_ids->dtype == AITER_DTYPE_i32 &&
+                     num_valid_ids->dtype == AITER_DTYPE_i32,
+                 "sorted_token_ids, sorted_expert_ids and num_valid_ids must be int32");
+        AA_CHECK(sorted_weights->dtype == AITER_DTYPE_fp32, "sorted_weights must be float32");
+        AA_CHECK(topk_ids->strides[1] == 1 && topk_weights->strides[1] == 1, "topk tensors need unit column stride");
+        const int M = (int)topk_ids->shape[0], topk = (int)topk_ids->shape[1];
+        AA_CHECK(topk_weights->shape[0] == M && topk_weights->shape[1] == topk, "topk_weights shape != topk_ids shape");
+        AA_CHECK(num_experts >= 1 && num_experts <= kMaxE, "num_experts must be in [1, ", kMaxE, "], got ",
+                 num_experts);
+        AA_CHECK(unit_size >= 1, "unit_size must be positive");
+        AA_CHECK(topk >= 1 && topk < 128 && M < (1 << 24), "topk must be in [1, 127] and tokens < 2^24");
+        AA_CHECK(dispatch_policy == 0, "only dispatch_policy 0 is supported");
+        const int64_t max_padded = (int64_t)M * topk + (int64_t)num_experts * unit_size - topk;
+        const int64_t max_blocks = (max_padded + unit_size - 1) / unit_size;
+        AA_CHECK(sorted_token_ids->numel >= (size_t)max_padded && sorted_weights->numel >= (size_t)max_padded,
+                 "sorted_token_ids / sorted_weights need ", max_padded, " entries");
+        AA_CHECK(sorted_expert_ids->numel >= (size_t)max_blocks, "sorted_expert_ids needs ", max_blocks, " entries");
+        AA_CHECK(num_valid_ids->numel >= 2, "num_valid_ids needs 2 entries");
+        if (local_expert_mask) {
+            AA_CHECK(local_expert_mask->dtype == AITER_DTYPE_i32 && local_expert_mask->numel >= (size_t)num_experts,
+                     "local_expert_mask must be int32 with num_experts entries");
+        }
+        if (num_local_tokens) AA_CHECK(num_local_tokens->dtype == AITER_DTYPE_i32, "num_local_tokens must be int32");
+
+        SortParams p{};
+        p.topk_ids = static_cast<const int*>(topk_ids->ptr);
+        p.topk_w = static_cast<const float*>(topk_weights->ptr);
+        p.sorted_ids = static_cast<int*>(sorted_token_ids->ptr);
+        p.sorted_w = static_cast<float*>(sorted_weights->ptr);
+        p.sorted_eids = static_cast<int*>(sorted_expert_ids->ptr);
+        p.num_valid = static_cast<int*>(num_valid_ids->ptr);
+        p.expert_mask = local_expert_mask ? static_cast<const int*>(local_expert_mask->ptr) : nullptr;
+        p.num_local = num_local_tokens ? static_cast<const int*>(num_local_tokens->ptr) : nullptr;
+        p.ids_stride = topk_ids->strides[0];
+        p.w_stride = topk_weights->strides[0];
+        p.M = M;
+        p.topk = topk;
+        p.E = num_experts;
+        p.bs = unit_size;
+        p.max_padded = (int)max_padded;
+        p.max_blocks = (int)max_blocks;
+        const int64_t entries = (int64_t)M * topk;
+        p.nchunks = (int)((entries + kThreads - 1) / kThreads);
+        if (p.nchunks <= kSingleChunks) {
+            moe_sort_single<<<1, kThreads, 0, st>>>(p);
+        } else {
+            p.ws = static_cast<int*>(
+                lib_workspace(topk_ids->device_id, st, (size_t)(p.nchunks + 1) * num_experts * sizeof(int)));
+            moe_sort_count<<<p.nchunks, kThreads, 0, st>>>(p);
+            moe_sort_scan<<<1, kThreads, 0, st>>>(p);
+            moe_sort_place<<<p.nchunks, kThreads, 0, st>>>(p);
+        }
+        AA_HIP(hipGetLastError());
+        if (moe_buf && moe_buf->numel > 0) {
+            const int64_t bytes = (int64_t)moe_buf->numel * (int64_t)dtype_size(moe_buf->dtype);
+            const int64_t blocks = std::min<int64_t>((bytes / 16 + 255) / 256 + 1, 4096);
+            fill_zero_kernel<<<(unsigned)blocks, 256, 0, st>>>(static_cast<uint8_t*>(moe_buf->ptr), bytes);
+            AA_HIP(hipGetLastError());
+        }
+    });
+}
+
+}  // extern "C"

@@ -45,25 +45,13 @@ struct QuantParams {
     float amax_floor;
 };
 
+// Quantises the 32 elements at src (16-byte aligned): returns the e8m0 byte
+// and the packed codes (fp4: o[0]; fp8: o[0], o[1]).
 template <typename InT, bool OUT_FP8, int MODE>
-__global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t x = gid / p.scale_n_pad;
-    const int y = (int)(gid % p.scale_n_pad);
-    int64_t rows = p.rows;
-    if (p.num_rows) rows = (int64_t)(*p.num_rows) * p.num_rows_factor;
-    if (x >= p.cover_rows) return;
-    const bool valid = (x < rows) && (y < p.scale_n);
-    if (!valid) {
-        // padding of the (Triton-layout) shuffled scale buffer is written as zero
-        if (p.zero_pad) p.scale[scale_shuffle_idx(p.scale_n_pad, (int)x, y)] = 0;
-        return;
-    }
-
+AA_DEV uint32_t quant_block32(const QuantParams& p, const InT* src, i32x4_t (&o)[2]) {
     constexpr int kVec = 16 / sizeof(InT);  // elements per 16-byte load
     float v[32];
     uint32_t raw[sizeof(InT) == 2 ? 16 : 1];   // 16-bit inputs: the loaded element pairs
-    const InT* src = reinterpret_cast<const InT*>(p.in) + x * p.in_stride + (int64_t)y * 32;
 #pragma unroll
     for (int i = 0; i < 32 / kVec; ++i) {
         const i32x4_t w = *reinterpret_cast<const i32x4_t*>(src + i * kVec);
@@ -101,7 +89,6 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
     const float inv = inv_scale_from_byte(byte);
 
     if constexpr (OUT_FP8) {
-        i32x4_t o[2];
         if (byte != 0u && byte != 255u) {
             const float ds = __builtin_bit_cast(float, byte << 23);
 #pragma unroll
@@ -125,11 +112,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
                 o[i / 4][i % 4] = (int)w;
             }
         }
-        uint8_t* dst = p.out + x * p.out_stride + (int64_t)y * 32;
-        *reinterpret_cast<i32x4_t*>(dst) = o[0];
-        *reinterpret_cast<i32x4_t*>(dst + 16) = o[1];
     } else {
-        i32x4_t o;
         if (byte != 0u && byte != 255u) {
             // gfx950 v_cvt_scalef32_pk_fp4_*: two values / 2^(byte-127) -> two
             // e2m1 nibbles (RNE, saturating at 6; the even element in the low
@@ -149,7 +132,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
                     else
                         w = cvt_fp4_pair<float>(w, 0u, v[i * 8 + 2 * j], v[i * 8 + 2 * j + 1], ds, j);
                 }
-                o[i] = (int)w;
+                o[0][i] = (int)w;
             }
         } else {
             // scale byte 0 (2^-127, a subnormal f32) or 255 (NaN): the
@@ -159,9 +142,36 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
                 uint32_t w = 0;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) w |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
-                o[i] = (int)w;
+                o[0][i] = (int)w;
             }
         }
+    }
+    return byte;
+}
+
+template <typename InT, bool OUT_FP8, int MODE>
+__global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t x = gid / p.scale_n_pad;
+    const int y = (int)(gid % p.scale_n_pad);
+    int64_t rows = p.rows;
+    if (p.num_rows) rows = (int64_t)(*p.num_rows) * p.num_rows_factor;
+    if (x >= p.cover_rows) return;
+    const bool valid = (x < rows) && (y < p.scale_n);
+    if (!valid) {
+        // padding of the (Triton-layout) shuffled scale buffer is written as zero
+        if (p.zero_pad) p.scale[scale_shuffle_idx(p.scale_n_pad, (int)x, y)] = 0;
+        return;
+    }
+
+    const InT* src = reinterpret_cast<const InT*>(p.in) + x * p.in_stride + (int64_t)y * 32;
+    i32x4_t o[2];
+    const uint32_t byte = quant_block32<InT, OUT_FP8, MODE>(p, src, o);
+    if constexpr (OUT_FP8) {
+        uint8_t* dst = p.out + x * p.out_stride + (int64_t)y * 32;
+        *reinterpret_cast<i32x4_t*>(dst) = o[0];
+        *reinterpret_cast<i32x4_t*>(dst + 16) = o[1];
+    } else {
         int64_t off;
         if (p.shuffle_weight) {
             // shuffle_weight((16,16)) position of bytes [16y, 16y+16) of row x
@@ -170,7 +180,7 @@ __global__ __launch_bounds__(256) void mx_quant_kernel(QuantParams p) {
         } else {
             off = x * p.out_stride + (int64_t)y * 16;
         }
-        *reinterpret_cast<i32x4_t*>(p.out + off) = o;
+        *reinterpret_cast<i32x4_t*>(p.out + off) = o[0];
     }
     if (p.shuffle_scale)
         p.scale[scale_shuffle_idx(p.scale_n_pad, (int)x, y)] = (uint8_t)byte;
@@ -188,6 +198,70 @@ void launch_mode(int mode, const QuantParams& p, int64_t nthreads, hipStream_t s
         case kCeil: mx_quant_kernel<InT, OUT_FP8, kCeil><<<grid, 256, 0, st>>>(p); break;
         default: aiter_amd::fail("quant", "round_mode must be 0..3, got ", mode);
     }
+}
+
+// ---- MoE: rows named by a sorted routing list, scale bytes in sorted order ----
+// Sorted position x holds entry sorted_ids[x] = slot << 24 | token; its input
+// row is token (stage 1: one row per token) or token * topk + slot (stage 2:
+// one row per routed pair).  Scale byte (x, block) goes to the shuffled
+// [pad32(len), pad8(K/32)] layout at row x, so that a GEMM over the sorted
+// list reads its A scales in row order.  Padding positions (token >= token
+// count, x >= num_valid_ids[0]) and padding columns get scale byte 0.
+struct SortQuant {
+    const int* sorted_ids;
+    const int* num_valid;
+    const float* sorted_w;    // optional: a zero routing weight writes a zero row
+    int64_t sorted_rows;      // positions covered (pad32 of the sorted list)
+    int token_num, topk;
+};
+
+AA_DEV int64_t sorted_source_row(const SortQuant& s, int64_t x, int& valid) {
+    const int nv = *s.num_valid;
+    const int id = x < nv ? s.sorted_ids[x] : s.token_num;
+    const int token = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+    valid = token < s.token_num && (s.topk == 1 || slot < s.topk);
+    return s.topk == 1 ? (int64_t)token : (int64_t)token * s.topk + slot;
+}
+
+// fused quant + sort (csrc/kernels/quant_kernels.cu:1733-1880): RoundUp e8m0
+// from the running max 1e-10, one thread per (sorted position, 32-block)
+template <typename InT, bool OUT_FP8>
+__global__ __launch_bounds__(256) void mx_quant_sorted_kernel(QuantParams p, SortQuant s) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t x = gid / p.scale_n_pad;
+    const int y = (int)(gid % p.scale_n_pad);
+    if (x >= s.sorted_rows) return;
+    int valid;
+    const int64_t row = sorted_source_row(s, x, valid);
+    uint8_t* sc = p.scale + scale_shuffle_idx(p.scale_n_pad, (int)x, y);
+    if (!valid || y >= p.scale_n) {
+        *sc = 0;
+        return;
+    }
+    constexpr int OB = OUT_FP8 ? 32 : 16;   // output bytes per block
+    uint8_t* dst = p.out + row * p.out_stride + (int64_t)y * OB;
+    i32x4_t o[2] = {i32x4_t{0, 0, 0, 0}, i32x4_t{0, 0, 0, 0}};
+    uint32_t byte = 0;
+    if (!(s.sorted_w && s.sorted_w[x] == 0.0f)) {
+        const InT* src = reinterpret_cast<const InT*>(p.in) + row * p.in_stride + (int64_t)y * 32;
+        byte = quant_block32<InT, OUT_FP8, kRoundUp>(p, src, o);
+    }
+    *reinterpret_cast<i32x4_t*>(dst) = o[0];
+    if constexpr (OUT_FP8) *reinterpret_cast<i32x4_t*>(dst + 16) = o[1];
+    *sc = (uint8_t)byte;
+}
+
+// byte sort of per-row scales (csrc/kernels/quant_kernels.cu mxfp4_moe_sort):
+// plain [rows, K/32] -> sorted shuffled layout
+__global__ __launch_bounds__(256) void mx_scale_sort_kernel(const uint8_t* scale, int64_t scale_stride, uint8_t* out,
+                                                            SortQuant s, int scale_n, int scale_n_pad) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t x = gid / scale_n_pad;
+    const int y = (int)(gid % scale_n_pad);
+    if (x >= s.sorted_rows) return;
+    int valid;
+    const int64_t row = sorted_source_row(s, x, valid);
+    out[scale_shuffle_idx(scale_n_pad, (int)x, y)] = (valid && y < scale_n) ? scale[row * scale_stride + y] : 0;
 }
 
 struct QuantRequest {
@@ -320,6 +394,119 @@ int dynamic_per_group_scaled_quant(aiter_tensor_t* out, aiter_tensor_t* input,
         q.num_rows = num_rows ? static_cast<const int*>(num_rows->ptr) : nullptr;
         q.num_rows_factor = num_rows_factor;
         run_quant(q, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int fused_dynamic_mx_quant_moe_sort_hip(aiter_tensor_t* out, aiter_tensor_t* scales, aiter_tensor_t* input,
+                                        aiter_tensor_t* sorted_ids, aiter_tensor_t* num_valid_ids, int token_num,
+                                        int block_m, int group_size, aiter_tensor_t* sorted_weights,
+                                        aiter_stream_t stream) {
+    using namespace aiter_amd;
+    return safe_call([&] {
+        AA_CHECK(group_size == 32, "only group_size 32 (MX) is implemented, got ", group_size);
+        (void)block_m;
+        check_tensor(out, "out");
+        check_tensor(scales, "scales");
+        check_tensor(input, "input");
+        check_tensor(sorted_ids, "sorted_ids");
+        check_tensor(num_valid_ids, "num_valid_ids");
+        DeviceGuard g(input->device_id);
+        const int in_dt = input->dtype;
+        AA_CHECK(in_dt == AITER_DTYPE_bf16 || in_dt == AITER_DTYPE_fp16 || in_dt == AITER_DTYPE_fp32,
+                 "input must be bf16/fp16/fp32");
+        const bool fp8 = out->dtype == AITER_DTYPE_fp8;
+        AA_CHECK(fp8 || out->dtype == AITER_DTYPE_fp4x2 || out->dtype == AITER_DTYPE_u8, "out must be fp4x2 or fp8");
+        AA_CHECK(sorted_ids->dtype == AITER_DTYPE_i32 && num_valid_ids->dtype == AITER_DTYPE_i32,
+                 "sorted_ids / num_valid_ids must be int32");
+        const int64_t rows = rows_2d(input), cols = cols_2d(input);
+        AA_CHECK(cols % 32 == 0, "input columns must be a multiple of 32");
+        AA_CHECK(token_num > 0 && rows % token_num == 0, "input rows ", rows, " must be a multiple of token_num ",
+                 token_num);
+        AA_CHECK(input->strides[input->ndim - 1] == 1 && ((uintptr_t)input->ptr & 15) == 0,
+                 "input must have unit column stride and 16-byte alignment");
+        const int64_t in_stride = input->ndim >= 2 ? input->strides[input->ndim - 2] : cols;
+        AA_CHECK(in_stride % (16 / dtype_size(in_dt)) == 0, "input row stride must keep 16-byte alignment");
+        const int64_t out_cols = fp8 ? cols : cols / 2;
+        AA_CHECK(rows_2d(out) == rows && cols_2d(out) == out_cols && out->strides[out->ndim - 1] == 1,
+                 "out must be [", rows, ", ", out_cols, "]");
+        const int64_t out_stride = out->ndim >= 2 ? out->strides[out->ndim - 2] : out_cols;
+        AA_CHECK(out_stride % 16 == 0 && ((uintptr_t)out->ptr & 15) == 0, "out rows must be 16-byte aligned");
+        const int scale_n = (int)(cols / 32), scale_n_pad = (scale_n + 7) / 8 * 8;
+        const int64_t sorted_rows = ((int64_t)sorted_ids->numel + 31) / 32 * 32;
+        AA_CHECK((int64_t)scales->numel >= sorted_rows * scale_n_pad, "scales needs [pad32(len(sorted_ids)), ",
+                 scale_n_pad, "] bytes");
+        if (sorted_weights) {
+            AA_CHECK(sorted_weights->dtype == AITER_DTYPE_fp32 && sorted_weights->numel >= sorted_ids->numel,
+                     "sorted_weights must be float32 with len(sorted_ids) entries");
+        }
+        QuantParams p{};
+        p.in = input->ptr;
+        p.out = static_cast<uint8_t*>(out->ptr);
+        p.scale = static_cast<uint8_t*>(scales->ptr);
+        p.in_stride = in_stride;
+        p.out_stride = out_stride;
+        p.scale_n = scale_n;
+        p.scale_n_pad = scale_n_pad;
+        p.cols = (int)cols;
+        p.inv_max_pos = fp8 ? 1.0f / 448.0f : 1.0f / 6.0f;
+        p.inv_max_pow2 = fp8 ? 1.0f / 256.0f : 0.25f;
+        p.emax = fp8 ? 8 : 2;
+        p.amax_floor = 1e-10f;   // csrc/kernels/quant_kernels.cu:1837
+        SortQuant s{};
+        s.sorted_ids = static_cast<const int*>(sorted_ids->ptr);
+        s.num_valid = static_cast<const int*>(num_valid_ids->ptr);
+        s.sorted_w = sorted_weights ? static_cast<const float*>(sorted_weights->ptr) : nullptr;
+        s.sorted_rows = sorted_rows;
+        s.token_num = token_num;
+        s.topk = (int)(rows / token_num);
+        const int64_t nthreads = sorted_rows * scale_n_pad;
+        const dim3 grid((unsigned)((nthreads + 255) / 256));
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        if (in_dt == AITER_DTYPE_bf16) {
+            if (fp8) mx_quant_sorted_kernel<uint16_t, true><<<grid, 256, 0, st>>>(p, s);
+            else mx_quant_sorted_kernel<uint16_t, false><<<grid, 256, 0, st>>>(p, s);
+        } else if (in_dt == AITER_DTYPE_fp16) {
+            if (fp8) mx_quant_sorted_kernel<_Float16, true><<<grid, 256, 0, st>>>(p, s);
+            else mx_quant_sorted_kernel<_Float16, false><<<grid, 256, 0, st>>>(p, s);
+        } else {
+            if (fp8) mx_quant_sorted_kernel<float, true><<<grid, 256, 0, st>>>(p, s);
+            else mx_quant_sorted_kernel<float, false><<<grid, 256, 0, st>>>(p, s);
+        }
+        AA_HIP(hipGetLastError());
+    });
+}
+
+int mxfp4_moe_sort_hip(aiter_tensor_t* out_scale, aiter_tensor_t* scale, aiter_tensor_t* sorted_ids,
+                       aiter_tensor_t* num_valid_ids, int token_num, int cols, aiter_stream_t stream) {
+    using namespace aiter_amd;
+    return safe_call([&] {
+        check_tensor(out_scale, "out_scale");
+        check_tensor(scale, "scale", 2);
+        check_tensor(sorted_ids, "sorted_ids");
+        check_tensor(num_valid_ids, "num_valid_ids");
+        DeviceGuard g(scale->device_id);
+        AA_CHECK(is_byte_type(scale->dtype) && is_byte_type(out_scale->dtype), "scales must be e8m0/u8");
+        AA_CHECK(sorted_ids->dtype == AITER_DTYPE_i32 && num_valid_ids->dtype == AITER_DTYPE_i32,
+                 "sorted_ids / num_valid_ids must be int32");
+        const int scale_n = (cols + 31) / 32, scale_n_pad = (scale_n + 7) / 8 * 8;
+        const int64_t rows = rows_2d(scale);
+        AA_CHECK(token_num > 0 && rows % token_num == 0, "scale rows ", rows, " must be a multiple of token_num");
+        AA_CHECK(cols_2d(scale) >= scale_n && scale->strides[scale->ndim - 1] == 1, "scale must be [rows, ",
+                 scale_n, "]");
+        const int64_t sorted_rows = ((int64_t)sorted_ids->numel + 31) / 32 * 32;
+        AA_CHECK((int64_t)out_scale->numel >= sorted_rows * scale_n_pad, "out_scale needs [pad32(len(sorted_ids)), ",
+                 scale_n_pad, "] bytes");
+        SortQuant s{};
+        s.sorted_ids = static_cast<const int*>(sorted_ids->ptr);
+        s.num_valid = static_cast<const int*>(num_valid_ids->ptr);
+        s.sorted_rows = sorted_rows;
+        s.token_num = token_num;
+        s.topk = (int)(rows / token_num);
+        const int64_t nthreads = sorted_rows * scale_n_pad;
+        mx_scale_sort_kernel<<<(unsigned)((nthreads + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+            static_cast<const uint8_t*>(scale->ptr), scale->strides[scale->ndim - 2], static_cast<uint8_t*>(out_scale->ptr),
+            s, scale_n, scale_n_pad);
+        AA_HIP(hipGetLastError());
     });
 }
 

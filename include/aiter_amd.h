@@ -156,6 +156,63 @@ int fused_rms_mx_quant(aiter_tensor_t* x1, aiter_tensor_t* x1_weight, float eps1
                        aiter_tensor_t* out_scale, aiter_tensor_t* out1, aiter_tensor_t* out2,
                        aiter_tensor_t* out_res1, int shuffle, int pad_scale, aiter_stream_t stream);
 
+/* ---- fused MoE (MXFP4 weights, per-1x32 e8m0 scales) ---------------------
+ * Routing sort: replaces moe_sorting_fwd (aiter/ops/moe_sorting.py:12-27,
+ * called from aiter/fused_moe.py:171-285).  topk_ids int32 [M, topk],
+ * topk_weights fp32 [M, topk]; outputs sized as aiter/fused_moe.py:206-215:
+ * sorted_token_ids int32 / sorted_weights fp32 [M*topk + E*unit - topk]
+ * (slot << 24 | token, experts in order, tokens in order inside an expert,
+ * padding topk << 24 | M), sorted_expert_ids int32 [ceil(len / unit)]
+ * (unused: -1), num_valid_ids int32 [2] = {padded count, tokens};
+ * moe_buf (optional) is zeroed.  local_expert_mask int32 [E] (0 drops an
+ * expert; kept experts renumbered), num_local_tokens int32 [1] (device
+ * count of tokens to route).  dispatch_policy must be 0. */
+int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aiter_tensor_t* sorted_token_ids,
+                    aiter_tensor_t* sorted_weights, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
+                    aiter_tensor_t* moe_buf, int num_experts, int unit_size, aiter_tensor_t* local_expert_mask,
+                    aiter_tensor_t* num_local_tokens, int dispatch_policy, aiter_stream_t stream);
+
+/* Sorted MX quant: replaces fused_dynamic_mx_quant_moe_sort_hip
+ * (aiter/ops/quant.py:895-911; kernel csrc/kernels/quant_kernels.cu:1733-1880).
+ * input bf16/fp16/fp32 [token_num * t, K] (t = 1: stage 1, t = topk: stage
+ * 2), out fp4x2 [rows, K/2] or fp8 [rows, K], scales u8 [pad32(len(sorted_ids)),
+ * pad8(K/32)] in sorted shuffled order; RoundUp e8m0 from the running max
+ * 1e-10; sorted_weights (optional) zero weight -> zero row. */
+int fused_dynamic_mx_quant_moe_sort_hip(aiter_tensor_t* out, aiter_tensor_t* scales, aiter_tensor_t* input,
+                                        aiter_tensor_t* sorted_ids, aiter_tensor_t* num_valid_ids, int token_num,
+                                        int block_m, int group_size, aiter_tensor_t* sorted_weights,
+                                        aiter_stream_t stream);
+
+/* Scale byte sort: replaces mxfp4_moe_sort_hip (aiter/ops/quant.py:861-871):
+ * per-row e8m0 [rows, K/32] -> sorted shuffled [pad32(len), pad8(K/32)]. */
+int mxfp4_moe_sort_hip(aiter_tensor_t* out_scale, aiter_tensor_t* scale, aiter_tensor_t* sorted_ids,
+                       aiter_tensor_t* num_valid_ids, int token_num, int cols, aiter_stream_t stream);
+
+/* Grouped GEMM stages: replace ck_moe_stage1 / ck_moe_stage2
+ * (aiter/ops/moe_op.py:350-394; numerics aiter/fused_moe.py:3437-3680).
+ * quant_type must be 3 (per_1x32); weights fp4x2 [E, N, K/2] preshuffled
+ * (is_shuffled = 1) with scales shuffled as one [E*N, K/32] matrix; A fp4x2
+ * (a4w4) or fp8 (a8w4) with its sorted scale (fused_dynamic_mx_quant_moe_sort).
+ * Stage 1: w1 [E, 2*inter, K/2] (gate rows then up rows), out bf16
+ * [token_num, topk, inter] = act(gate) * up (activation 0 Silu, 1 Gelu;
+ * sorted_weights, if given, scale gate and up first).  Stage 2: w2
+ * [E, model_dim, inter/2], inter_states [token_num*topk, inter(/2)], out bf16
+ * [token_num, model_dim] += weight * GEMM (packed bf16 atomics; out must start
+ * at zero).  block_m (32, 64, 128) must equal the sort's unit_size; splitk
+ * must be <= 1.  w2 (stage 1) and w1 (stage 2) may be NULL. */
+int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
+                  aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
+                  aiter_tensor_t* out, int topk, const char* kernelName, aiter_tensor_t* w1_scale,
+                  aiter_tensor_t* a1_scale, int block_m, aiter_tensor_t* sorted_weights, int quant_type,
+                  int activation, int splitk, int use_non_temporal_load, const char* dst_type, int is_shuffled,
+                  aiter_stream_t stream);
+int ck_moe_stage2(aiter_tensor_t* inter_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
+                  aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
+                  aiter_tensor_t* out, int topk, const char* kernelName, aiter_tensor_t* w2_scale,
+                  aiter_tensor_t* a2_scale, int block_m, aiter_tensor_t* sorted_weights, int quant_type,
+                  int activation, int splitk, int use_non_temporal_load, const char* dst_type, int is_shuffled,
+                  aiter_stream_t stream);
+
 /* ---- library introspection and workspace --------------------------------
  * The reference keeps its kernel list in per-arch CSVs next to its ASM code
  * objects (hsa/gfx950/f4gemm/f4gemm_bf16_per1x32Fp4.csv) and the CK instance
