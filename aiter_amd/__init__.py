@@ -18,7 +18,8 @@ from .gemm_op_a4w4 import (compute_gemm_SplitK, gemm_a4w4, gemm_a4w4_asm, gemm_a
 from .fused_quant import fused_rms_mxfp4_quant, fused_rms_mxfp8_quant
 from .fused_moe import (ActivationType, ck_moe_stage1, ck_moe_stage2, fused_dynamic_mx_quant_moe_sort,
                         fused_dynamic_mxfp4_quant_moe_sort, fused_dynamic_mxfp8_quant_moe_sort, fused_moe,
-                        fused_moe_2stages, get_block_size_M, moe_sorting, moe_sorting_fwd, mxfp4_moe_sort_fwd)
+                        fused_moe_2stages, get_block_size_M, moe_sorting, moe_sorting_fwd, moe_sum,
+                        mxfp4_moe_sort_fwd)
 from .gemm_op_a8w4 import gemm_a8w4_mxfp8, gemm_a8w4_mxfp8_dynamic
 from .gemm_op_a16w16 import gemm_a16w16_asm
 from .opus import gemm_a16w16_opus, opus_gemm_a16w16_tune, opus_gemm_workspace_init

@@ -71,6 +71,10 @@ struct MoeParams {
     int64_t a_rows;             // rows of A (gathered rows must stay below)
     int sorted_len;             // entries of sorted_ids (later positions are padding)
     int token_num, topk, inter, n_experts, act;
+    int per_pair;               // stage 2: store rows token * topk + slot instead of adding into token rows
+    int sort_bs;                // row block of the sort (a multiple of BM): expert of row r = sorted_eids[r / sort_bs]
+    int k_splits;               // stage 1 split-K: > 1 -> raw f32 gate/up partials into GemmParams::ws
+    int64_t ws_rows;            //   rows per split slice of ws (grid row blocks * BM)
 };
 
 AA_DEV void atomic_add_bf16x2(uint16_t* addr, uint32_t v) {
@@ -115,13 +119,28 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
 
     int tm, tn;
+    int kt0 = 0;   // first K stage of this workgroup (MoE stage-1 split-K)
     const uint8_t* b_base = p.B;
     const uint8_t* bs_base = p.Bs;
     if constexpr (MOE != kMoeNone) {
-        tn = blockIdx.x;
-        tm = blockIdx.y;
+        // 1-D grid, tiles in (row block, N tile) order with N fastest; the
+        // workgroups of one row block (and the neighbouring blocks of the same
+        // expert) share B, so consecutive tiles go to the same XCD (workgroup
+        // ids are dealt round-robin over the 8 XCDs, each with its own L2)
+        // (the host pads the grid to a multiple of 8; the extra ids leave)
+        int bid = blockIdx.x;
+        bid = (bid % 8) * (gridDim.x / 8) + bid / 8;
+        if (bid >= p.tiles_n * p.tiles_m * ((MOE == kMoeStage1 && mq.k_splits > 1) ? mq.k_splits : 1)) return;
+        if constexpr (MOE == kMoeStage1) {
+            const int per_split = p.tiles_n * p.tiles_m;
+            const int sp = bid / per_split;
+            bid -= sp * per_split;
+            kt0 = sp * p.k_steps_per_split;
+        }
+        tn = bid % p.tiles_n;
+        tm = bid / p.tiles_n;
         if (tm * BM >= mq.num_valid[0]) return;   // whole workgroup: past the sorted list
-        const int e = mq.sorted_eids[tm];
+        const int e = mq.sorted_eids[tm * BM / mq.sort_bs];
         if (e < 0 || e >= mq.n_experts) return;
         b_base += (int64_t)e * mq.b_expert_bytes;
         bs_base += (int64_t)e * mq.bs_expert_bytes;
@@ -130,7 +149,28 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     }
     // stage 1: 128 output columns per tile (128 gate + 128 up rows of B)
     const int m0 = tm * BM, n0 = (MOE == kMoeStage1) ? tn * (BN / 2) : tn * BN;
-    const int nstages = p.K / Cfg::K_STAGE;
+    const int nstages = (MOE == kMoeStage1 && mq.k_splits > 1) ? min(p.k_steps_per_split, p.K / Cfg::K_STAGE - kt0)
+                                                                : p.K / Cfg::K_STAGE;
+    // MoE: the block's sorted entries and routing weights, one per lane
+    // (registers 0 / 1 = rows 0-63 / 64-127), loaded once; later uses read
+    // them with lane shuffles instead of a dependent global load per row
+    constexpr int IDR = (BM + 63) / 64;
+    int ids_r[IDR];
+    float w_r[IDR];
+    if constexpr (MOE != kMoeNone) {
+#pragma unroll
+        for (int k = 0; k < IDR; ++k) {
+            const int pos = m0 + 64 * k + lane;
+            const bool in = 64 * k + lane < BM && pos < mq.sorted_len;
+            ids_r[k] = in ? mq.sorted_ids[pos] : mq.token_num;
+            w_r[k] = (in && mq.sorted_w) ? mq.sorted_w[pos] : 1.0f;
+        }
+    }
+    // entry of tile row r (any lane pattern; rows in one 64-row half when uniform)
+    auto row_entry = [&](int r) -> int {
+        const int lo = __shfl(ids_r[0], r & 63);
+        return (IDR == 1 || r < 64) ? lo : __shfl(ids_r[IDR - 1], r & 63);
+    };
 
     // ---- A: chunk c = half*(BM/8) + 8-row block; lane l -> row l/8, stored piece l%8
     //      holding global 16-byte piece (l%8) ^ swz(row), swz(r) = (r>>1)&7
@@ -146,7 +186,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         int row = r;
         if constexpr (MOE != kMoeNone) {
             // A row of sorted entry m0 + r; padding -> a_rows (reads zeros)
-            const int id = m0 + r < mq.sorted_len ? mq.sorted_ids[m0 + r] : mq.token_num;
+            const int id = row_entry(r);
             const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
             row = (tok >= mq.token_num || slot >= mq.topk) ? (int)mq.a_rows
                                                            : (MOE == kMoeStage1 ? tok : tok * mq.topk + slot);
@@ -198,12 +238,13 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         const __amdgpu_buffer_rsrc_t rs = live ? sc_rsrc : null_rsrc;
         uint8_t* base = smem + (t % NS) * STAGE_BYTES;
 #pragma unroll
-        for (int q = 0; q < NA; ++q) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], t * A_ROW_BYTES);
-        if constexpr (MX) dma16(rs, base + (A_CH + wave) * 1024, sc_off, t * 256);
+        for (int q = 0; q < NA; ++q) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], (kt0 + t) * A_ROW_BYTES);
+        if constexpr (MX) dma16(rs, base + (A_CH + wave) * 1024, sc_off, (kt0 + t) * 256);
     };
     auto load_b = [&](int t, int j, int s) -> i32x4_t {
         const __amdgpu_buffer_rsrc_t rb = t < nstages ? b_rsrc : null_rsrc;
-        return __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + s * (BPRE ? 512 : 32), t * (BPRE ? 2048 : 128), 0);
+        return __builtin_amdgcn_raw_buffer_load_b128(rb, b_off[j] + s * (BPRE ? 512 : 32),
+                                                     (kt0 + t) * (BPRE ? 2048 : 128), 0);
     };
 
     const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;
@@ -286,8 +327,8 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         uint8_t* base = smem + (t % NS) * STAGE_BYTES;
 #pragma unroll
         for (int q = part * DMA_PART; q < (part + 1) * DMA_PART && q < NDMA; ++q) {
-            if (q < NA) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], t * A_ROW_BYTES);
-            else dma16(rs, base + (A_CH + wave) * 1024, sc_off, t * 256);
+            if (q < NA) dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], (kt0 + t) * A_ROW_BYTES);
+            else dma16(rs, base + (A_CH + wave) * 1024, sc_off, (kt0 + t) * 256);
         }
     };
     // loads issued after the last A copy of stage t+1 and before the wait at
@@ -390,41 +431,93 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     constexpr int EP_MP = (MA * 32 * 64 * EB <= WAVE_SCRATCH) ? MA : MA / 2;
     static_assert(MA % EP_MP == 0 && EP_MP * 32 * 64 * EB <= WAVE_SCRATCH, "epilogue pass fits the ring");
     wait_vmcnt<0>();
+    if constexpr (MOE == kMoeStage1) {
+        if (mq.k_splits > 1) {
+            // raw f32 gate / up partials [split][ws_rows][2 * inter]; the reduce
+            // kernel sums the splits and applies weight and activation
+            float* wsb = p.ws + (int64_t)(kt0 / p.k_steps_per_split) * mq.ws_rows * (2 * mq.inter);
+#pragma unroll
+            for (int i = 0; i < MA; ++i) {
+                float* wrow = wsb + (int64_t)(m0 + 32 * i + (lane & 31)) * (2 * mq.inter) + n0 + 32 * wave +
+                              4 * (lane >> 5);
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const f32x16v_t& a = acc[i][j];
+                        *reinterpret_cast<f32x4_t*>(wrow + (j ? mq.inter : 0) + 8 * q) =
+                            f32x4_t{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                    }
+            }
+            return;
+        }
+    }
     if constexpr (MOE != kMoeNone) {
-        // lane: row 32i + l%32 of the tile, columns 8q + 4(l/32) + r of each 32-column tile
+        // Through LDS, so that every store / atomic instruction covers whole
+        // output rows instead of one 8-byte piece of 32 rows: the tile goes to
+        // the (now idle) ring as [BM][OC] bf16 (OC = 128 for stage 1, act(gate) *
+        // up, or 256 for stage 2), 8-byte chunks XOR-swizzled by row; then
+        // stage 1 stores two 256-byte rows per instruction and stage 2 adds
+        // one 512-byte row per pair of packed-bf16 atomics.
+        constexpr int OC = (MOE == kMoeStage1) ? 128 : 256;
+        static_assert(BM * OC * 2 <= NS * STAGE_BYTES, "epilogue tile fits the ring");
+        auto chunk = [&](int row, int c) -> uint2* {
+            return reinterpret_cast<uint2*>(smem + row * (OC * 2) + ((c ^ (row & 31)) * 8));
+        };
+        __syncthreads();
 #pragma unroll
         for (int i = 0; i < MA; ++i) {
-            const int pos = m0 + 32 * i + (lane & 31);
-            if (pos >= mq.sorted_len) continue;
-            const int id = mq.sorted_ids[pos];
-            const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
-            if (tok >= mq.token_num || slot >= mq.topk) continue;
-            const float wgt = mq.sorted_w ? mq.sorted_w[pos] : 1.0f;
+            // lane: row 32i + l%32 of the tile, columns 8q + 4(l/32) + r of each 32-column tile
+            const int row = 32 * i + (lane & 31);
+            const float wgt = __shfl(w_r[i / 2], row & 63);
             if constexpr (MOE == kMoeStage1) {
-                uint16_t* orow = mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + n0 + 32 * wave +
-                                 4 * (lane >> 5);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     float v[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         v[r] = moe_act(acc[i][0][4 * q + r] * wgt, mq.act) * (acc[i][1][4 * q + r] * wgt);
-                    uint2 o;
-                    o.x = pack_bf16x2(v[0], v[1]);
-                    o.y = pack_bf16x2(v[2], v[3]);
-                    *reinterpret_cast<uint2*>(orow + 8 * q) = o;
+                    *chunk(row, 8 * wave + 2 * q + (lane >> 5)) = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                 }
             } else {
-                uint16_t* orow = mq.out + (int64_t)tok * mq.out_stride + n0 + 64 * wave + 4 * (lane >> 5);
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const f32x16v_t& a = acc[i][j];
-                        atomic_add_bf16x2(orow + 32 * j + 8 * q, pack_bf16x2(a[4 * q] * wgt, a[4 * q + 1] * wgt));
-                        atomic_add_bf16x2(orow + 32 * j + 8 * q + 2,
-                                          pack_bf16x2(a[4 * q + 2] * wgt, a[4 * q + 3] * wgt));
+                        *chunk(row, 16 * wave + 8 * j + 2 * q + (lane >> 5)) =
+                            uint2{pack_bf16x2(a[4 * q] * wgt, a[4 * q + 1] * wgt),
+                                  pack_bf16x2(a[4 * q + 2] * wgt, a[4 * q + 3] * wgt)};
                     }
+            }
+        }
+        __syncthreads();
+        if constexpr (MOE == kMoeStage1) {
+            // lane l: row r0 + l/32, columns 4(l%32) .. +3
+            for (int r0 = 2 * wave; r0 < BM; r0 += 8) {
+                const int row = r0 + (lane >> 5);
+                const int id = __shfl((IDR == 1 || r0 < 64) ? ids_r[0] : ids_r[IDR - 1], row & 63);
+                const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+                if (tok >= mq.token_num || slot >= mq.topk) continue;
+                *reinterpret_cast<uint2*>(mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + n0 +
+                                          4 * (lane & 31)) = *chunk(row, lane & 31);
+            }
+        } else {
+            // one row per iteration (uniform over the wave); lane l: columns 4l .. 4l+3
+            for (int row = wave; row < BM; row += 4) {
+                const int id = __builtin_amdgcn_readlane((IDR == 1 || row < 64) ? ids_r[0] : ids_r[IDR - 1], row & 63);
+                const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+                if (tok >= mq.token_num || slot >= mq.topk) continue;
+                const uint2 v = *chunk(row, lane);
+                if (mq.per_pair) {
+                    // per-pair rows, summed over the slots afterwards (moe_sum): no atomics
+                    *reinterpret_cast<uint2*>(mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + n0 +
+                                              4 * lane) = v;
+                } else {
+                    uint16_t* o = mq.out + (int64_t)tok * mq.out_stride + n0 + 4 * lane;
+                    atomic_add_bf16x2(o, v.x);
+                    atomic_add_bf16x2(o + 2, v.y);
+                }
             }
         }
         return;

@@ -4,6 +4,9 @@
 // flat tile kernel's MoE stages (gemm_flat.h).  Entry points keep the argument
 // lists of the reference's ck_moe_stage1 / ck_moe_stage2
 // (aiter/ops/moe_op.py:350-394).
+#include <cstdlib>
+#include <string>
+
 #include "gemm_kernels.h"
 #include "mfma32.h"
 #include "gemm_flat.h"
@@ -12,9 +15,36 @@ namespace {
 
 using namespace aiter_amd;
 
+// stage-1 split-K: sum the f32 partials of every split, then weight and
+// act(gate) * up -> bf16 row token * topk + slot; 4 columns per thread
+__global__ __launch_bounds__(256) void moe_stage1_reduce_kernel(const float* ws, int splits, MoeParams mq) {
+    const int per_row = mq.inter / 4;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t pos = gid / per_row;
+    const int c = (int)(gid % per_row) * 4;
+    if (pos >= mq.ws_rows || pos >= *mq.num_valid || pos >= mq.sorted_len) return;
+    const int id = mq.sorted_ids[pos];
+    const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+    if (tok >= mq.token_num || slot >= mq.topk) return;
+    const float w = mq.sorted_w ? mq.sorted_w[pos] : 1.0f;
+    f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    const int64_t slice = mq.ws_rows * 2 * mq.inter;
+    const float* src = ws + pos * 2 * mq.inter + c;
+    for (int sp = 0; sp < splits; ++sp) {
+        g += *reinterpret_cast<const f32x4_t*>(src + sp * slice);
+        u += *reinterpret_cast<const f32x4_t*>(src + sp * slice + mq.inter);
+    }
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = moe_act(g[r] * w, mq.act) * (u[r] * w);
+    *reinterpret_cast<uint2*>(mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + c) =
+        uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+}
+
 struct StageArgs {
     aiter_tensor_t *a, *w, *a_scale, *w_scale, *sorted_ids, *sorted_eids, *num_valid, *out, *sorted_w;
-    int topk, block_m, activation, stage;
+    int topk, block_m, activation, stage, splitk;
+    int tile_m;   // GEMM row block (divides block_m; 0 = block_m)
     const char* kernel_name;
 };
 
@@ -26,6 +56,19 @@ void launch_bm(int bm, dim3 grid, const GemmParams& p, const MoeParams& mq, hipS
         case 128: moe_flat_kernel<KA, 128, MOE><<<grid, 256, 0, st>>>(p, mq); break;
         default: fail("moe", "block_m must be 32, 64 or 128, got ", bm);
     }
+}
+
+// GEMM row block: kernelName "moe_m32" / "moe_m64" / "moe_m128" picks it;
+// otherwise the sort's block for stage 1 and at most 64 rows for stage 2
+// (K is one or two stages there, so the tile is latency-bound and the smaller
+// tile's lower register count lets two workgroups share a CU)
+int tile_from_name(const char* name, int stage, int block_m) {
+    if (name && name[0]) {
+        const std::string n(name);
+        AA_CHECK(n.rfind("moe_m", 0) == 0, "unknown MoE kernel name '", n, "' (moe_m32 / moe_m64 / moe_m128)");
+        return std::atoi(n.c_str() + 5);
+    }
+    return stage == 1 ? block_m : std::min(block_m, 64);
 }
 
 void run_stage(const StageArgs& s, hipStream_t st) {
@@ -69,6 +112,9 @@ void run_stage(const StageArgs& s, hipStream_t st) {
     AA_CHECK(sorted_len < ((int64_t)1 << 31), "sorted_token_ids too long");
     const int64_t max_blocks = (sorted_len + s.block_m - 1) / s.block_m;
     AA_CHECK((int64_t)s.sorted_eids->numel >= max_blocks, "sorted_expert_ids needs ", max_blocks, " entries");
+    const int bm = s.tile_m > 0 ? s.tile_m : s.block_m;
+    AA_CHECK(bm == 32 || bm == 64 || bm == 128, "GEMM row block must be 32, 64 or 128, got ", bm);
+    AA_CHECK(s.block_m % bm == 0, "the sort's block_m ", s.block_m, " must be a multiple of the GEMM row block ", bm);
 
     int64_t token_num = s.out->shape[0];
     MoeParams mq{};
@@ -80,6 +126,7 @@ void run_stage(const StageArgs& s, hipStream_t st) {
     mq.b_expert_bytes = wrows * wbytes;
     mq.bs_expert_bytes = wrows * sn_pad;
     mq.a_rows = arows;
+    mq.sort_bs = s.block_m;
     mq.sorted_len = (int)sorted_len;
     mq.topk = s.topk;
     mq.n_experts = (int)E;
@@ -104,12 +151,22 @@ void run_stage(const StageArgs& s, hipStream_t st) {
         mq.inter = (int)inter;
         tiles_n = (int)(inter / 128);
     } else {
+        // out [token_num, model_dim]: packed-bf16 atomic adds into the token rows
+        // (out starts at zero); out [token_num, topk, model_dim] (or its 2-D
+        // view [token_num * topk, model_dim]): one row per routed pair, plain
+        // stores, summed over the slots by moe_sum
         const int64_t model_dim = wrows;
         AA_CHECK(model_dim % 256 == 0, "ck_moe_stage2: model_dim = ", model_dim, " must be a multiple of 256");
-        AA_CHECK(cols_2d(s.out) == model_dim && s.out->strides[1] == 1, "ck_moe_stage2: out must be [token_num, ",
-                 model_dim, "] bf16");
+        AA_CHECK(cols_2d(s.out) == model_dim && s.out->strides[s.out->ndim - 1] == 1,
+                 "ck_moe_stage2: out must be [token_num, (topk,) ", model_dim, "] bf16");
+        mq.per_pair = s.out->ndim == 3 ? 1 : 0;
+        if (mq.per_pair) {
+            AA_CHECK(s.out->shape[1] == s.topk, "ck_moe_stage2: out [token_num, topk, model_dim] needs topk = ",
+                     s.topk);
+            token_num = s.out->shape[0];
+        }
         AA_CHECK(arows == token_num * s.topk, "ck_moe_stage2: inter_states must have token_num * topk rows");
-        mq.out_stride = s.out->strides[0];
+        mq.out_stride = s.out->strides[s.out->ndim - 2];
         mq.token_num = (int)token_num;
         mq.inter = 0;
         tiles_n = (int)(model_dim / 256);
@@ -136,23 +193,101 @@ void run_stage(const StageArgs& s, hipStream_t st) {
     // row blocks in use are at most ceil(entries / block_m) + (experts hit);
     // blocks past num_valid_ids[0] leave at once
     const int64_t entries = token_num * s.topk;
-    const int64_t used = std::min<int64_t>(max_blocks, (entries + s.block_m - 1) / s.block_m + std::min<int64_t>(E, entries));
+    const int64_t used_sort = std::min<int64_t>(max_blocks, (entries + s.block_m - 1) / s.block_m +
+                                                              std::min<int64_t>(E, entries));
+    const int64_t used = std::min<int64_t>(used_sort * (s.block_m / bm), (sorted_len + bm - 1) / bm);
     if (used == 0) return;
     p.tiles_m = (int)used;
-    const dim3 grid((unsigned)tiles_n, (unsigned)used);
+    AA_CHECK((int64_t)tiles_n * used < ((int64_t)1 << 31), "grid too large");
+    // stage-1 split-K when the tiles cannot fill the chip (decode): about 256
+    // workgroups, at least 2 K stages each
+    const int nst = (int)(K / 256);
+    const int64_t tiles = (int64_t)tiles_n * used;
+    int splits = 1;
     if (s.stage == 1) {
-        if (a_fp8) launch_bm<kFp8, kMoeStage1>(s.block_m, grid, p, mq, st);
-        else launch_bm<kFp4, kMoeStage1>(s.block_m, grid, p, mq, st);
+        // splitk: 1 = one pass over K (the reference's default), > 1 = that
+        // many K slices, 0 = chosen here
+        int want = s.splitk != 0 ? s.splitk : (tiles < 128 ? (int)std::max<int64_t>(1, 256 / tiles) : 1);
+        want = std::min(want, std::max(1, nst / 2));
+        if (want > 1) {
+            const int per = (nst + want - 1) / want;
+            splits = (nst + per - 1) / per;
+            p.k_steps_per_split = per;
+        }
+    }
+    mq.k_splits = splits;
+    mq.ws_rows = used * bm;
+    if (splits > 1) {
+        const size_t bytes = (size_t)splits * mq.ws_rows * 2 * mq.inter * sizeof(float);
+        p.ws = static_cast<float*>(lib_workspace(s.out->device_id, st, bytes));
+    }
+    const dim3 grid((unsigned)((tiles * splits + 7) / 8 * 8));   // multiple of 8: XCD-aware tile order
+    if (s.stage == 1) {
+        if (a_fp8) launch_bm<kFp8, kMoeStage1>(bm, grid, p, mq, st);
+        else launch_bm<kFp4, kMoeStage1>(bm, grid, p, mq, st);
+        if (splits > 1) {
+            AA_HIP(hipGetLastError());
+            const int64_t n = mq.ws_rows * (mq.inter / 4);
+            moe_stage1_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
+        }
     } else {
-        if (a_fp8) launch_bm<kFp8, kMoeStage2>(s.block_m, grid, p, mq, st);
-        else launch_bm<kFp4, kMoeStage2>(s.block_m, grid, p, mq, st);
+        if (a_fp8) launch_bm<kFp8, kMoeStage2>(bm, grid, p, mq, st);
+        else launch_bm<kFp4, kMoeStage2>(bm, grid, p, mq, st);
     }
     AA_HIP(hipGetLastError());
+}
+
+// out[t, c] = sum over slots s of in[t, s, c] (f32, slot order), bf16 in / out;
+// 8 columns (16 bytes) per thread
+__global__ __launch_bounds__(256) void moe_sum_kernel(const uint16_t* in, uint16_t* out, int64_t tokens, int topk,
+                                                      int64_t dim, int64_t in_tok_stride, int64_t in_slot_stride,
+                                                      int64_t out_stride) {
+    const int64_t per_row = dim / 8;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= tokens * per_row) return;
+    const int64_t t = gid / per_row, c = (gid % per_row) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    const uint16_t* src = in + t * in_tok_stride + c;
+    for (int s = 0; s < topk; ++s) {
+        const i32x4_t v = *reinterpret_cast<const i32x4_t*>(src + s * in_slot_stride);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            acc[2 * k] += bf16_bits_to_f32((uint32_t)v[k] & 0xffffu);
+            acc[2 * k + 1] += bf16_bits_to_f32((uint32_t)v[k] >> 16);
+        }
+    }
+    i32x4_t o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = (int)pack_bf16x2(acc[2 * k], acc[2 * k + 1]);
+    *reinterpret_cast<i32x4_t*>(out + t * out_stride + c) = o;
 }
 
 }  // namespace
 
 extern "C" {
+
+int moe_sum(aiter_tensor_t* input, aiter_tensor_t* output, aiter_stream_t stream) {
+    return safe_call([&] {
+        check_tensor(input, "input", 3);
+        check_tensor(output, "output", 2);
+        DeviceGuard g(input->device_id);
+        AA_CHECK(input->dtype == AITER_DTYPE_bf16 && output->dtype == AITER_DTYPE_bf16, "moe_sum: bf16 only");
+        AA_CHECK(input->ndim == 3 && output->ndim == 2, "moe_sum: input [M, topk, D], output [M, D]");
+        const int64_t M = input->shape[0], topk = input->shape[1], D = input->shape[2];
+        AA_CHECK(output->shape[0] == M && output->shape[1] == D, "moe_sum: output must be [M, D]");
+        AA_CHECK(input->strides[2] == 1 && output->strides[1] == 1, "moe_sum: unit column stride needed");
+        AA_CHECK(D % 8 == 0 && input->strides[1] % 8 == 0 && input->strides[0] % 8 == 0 && output->strides[0] % 8 == 0 &&
+                     ((uintptr_t)input->ptr & 15) == 0 && ((uintptr_t)output->ptr & 15) == 0,
+                 "moe_sum: rows must be 16-byte aligned and D a multiple of 8");
+        const int64_t n = M * (D / 8);
+        if (n == 0) return;
+        moe_sum_kernel<<<(unsigned)((n + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+            static_cast<const uint16_t*>(input->ptr), static_cast<uint16_t*>(output->ptr), M, (int)topk, D,
+            input->strides[0], input->strides[1], output->strides[0]);
+        AA_HIP(hipGetLastError());
+    });
+}
+
 
 int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
                   aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
@@ -165,11 +300,11 @@ int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tenso
     (void)dst_type;
     return safe_call([&] {
         AA_CHECK(quant_type == 3, "ck_moe_stage1: only QuantType.per_1x32 (3) is implemented, got ", quant_type);
-        AA_CHECK(splitk <= 1, "ck_moe_stage1: split-K is not implemented for per_1x32");
         AA_CHECK(is_shuffled != 0, "ck_moe_stage1: weights must be preshuffled (shuffle_weight (16,16))");
         DeviceGuard g(hidden_states ? hidden_states->device_id : -1);
         StageArgs s{hidden_states, w1, a1_scale, w1_scale, sorted_token_ids, sorted_expert_ids, num_valid_ids, out,
-                    sorted_weights, topk, block_m, activation, 1, kernelName};
+                    sorted_weights, topk, block_m, activation, 1, splitk, tile_from_name(kernelName, 1, block_m),
+                    kernelName};
         run_stage(s, reinterpret_cast<hipStream_t>(stream));
     });
 }
@@ -190,7 +325,7 @@ int ck_moe_stage2(aiter_tensor_t* inter_states, aiter_tensor_t* w1, aiter_tensor
         AA_CHECK(is_shuffled != 0, "ck_moe_stage2: weights must be preshuffled (shuffle_weight (16,16))");
         DeviceGuard g(inter_states ? inter_states->device_id : -1);
         StageArgs s{inter_states, w2, a2_scale, w2_scale, sorted_token_ids, sorted_expert_ids, num_valid_ids, out,
-                    sorted_weights, topk, block_m, 0, 2, kernelName};
+                    sorted_weights, topk, block_m, 0, 2, 1, tile_from_name(kernelName, 2, block_m), kernelName};
         run_stage(s, reinterpret_cast<hipStream_t>(stream));
     });
 }

@@ -65,20 +65,31 @@ __device__ __forceinline__ int expert_of(const SortParams& p, int i, int n) {
     return e;
 }
 
-// exclusive scan of v over the workgroup's threads (one value per thread)
+// exclusive scan of v over the workgroup's threads (one value per thread):
+// shuffles inside each wave, then one wave scans the 16 wave totals
 __device__ int block_exclusive_scan(int v, int* buf) {
-    const int tid = threadIdx.x;
-    buf[tid] = v;
-    __syncthreads();
-    for (int d = 1; d < kThreads; d <<= 1) {
-        const int add = tid >= d ? buf[tid - d] : 0;
-        __syncthreads();
-        buf[tid] += add;
-        __syncthreads();
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d);
+        if (lane >= d) x += y;
     }
-    const int incl = buf[tid];
+    if (lane == 63) buf[w] = x;
     __syncthreads();
-    return incl - v;
+    if (w == 0) {
+        int t = lane < kWaves ? buf[lane] : 0;
+#pragma unroll
+        for (int d = 1; d < kWaves; d <<= 1) {
+            const int y = __shfl_up(t, d);
+            if (lane >= d) t += y;
+        }
+        if (lane < kWaves) buf[lane] = t;
+    }
+    __syncthreads();
+    const int r = (w ? buf[w - 1] : 0) + x - v;
+    __syncthreads();
+    return r;
 }
 
 // from sm.cnt: expert offsets, block -> expert table, padding entries,
@@ -189,12 +200,19 @@ __global__ __launch_bounds__(kThreads) void moe_sort_scan(SortParams p) {
     const int e = threadIdx.x;
     if (e < p.E) {
         // chunk counts -> exclusive prefix over chunks (the chunk's start inside the expert)
+        // 16 loads in flight per batch (the stores of a batch would otherwise
+        // order every load behind the previous store)
         int run = 0;
-        for (int c = 0; c < p.nchunks; ++c) {
-            int* q = p.ws + (int64_t)c * p.E + e;
-            const int v = *q;
-            *q = run;
-            run += v;
+        for (int c0 = 0; c0 < p.nchunks; c0 += 16) {
+            int v[16];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = c0 + k < p.nchunks ? p.ws[(int64_t)(c0 + k) * p.E + e] : 0;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (c0 + k < p.nchunks) {
+                    p.ws[(int64_t)(c0 + k) * p.E + e] = run;
+                    run += v[k];
+                }
         }
         sm.cnt[e] = run;
     }

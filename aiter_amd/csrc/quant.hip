@@ -205,8 +205,11 @@ void launch_mode(int mode, const QuantParams& p, int64_t nthreads, hipStream_t s
 // row is token (stage 1: one row per token) or token * topk + slot (stage 2:
 // one row per routed pair).  Scale byte (x, block) goes to the shuffled
 // [pad32(len), pad8(K/32)] layout at row x, so that a GEMM over the sorted
-// list reads its A scales in row order.  Padding positions (token >= token
-// count, x >= num_valid_ids[0]) and padding columns get scale byte 0.
+// list reads its A scales in row order.  One workgroup (or thread, for the
+// byte sort) per 32 sorted positions; groups at or past num_valid_ids[0] (a
+// multiple of the row block) exit at once and leave their bytes unwritten, as
+// the GEMM never reads them.  Padding positions inside the list (token >=
+// token count) and padding columns get scale byte 0.
 struct SortQuant {
     const int* sorted_ids;
     const int* num_valid;
@@ -227,41 +230,96 @@ AA_DEV int64_t sorted_source_row(const SortQuant& s, int64_t x, int& valid) {
 // from the running max 1e-10, one thread per (sorted position, 32-block)
 template <typename InT, bool OUT_FP8>
 __global__ __launch_bounds__(256) void mx_quant_sorted_kernel(QuantParams p, SortQuant s) {
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t x = gid / p.scale_n_pad;
-    const int y = (int)(gid % p.scale_n_pad);
-    if (x >= s.sorted_rows) return;
-    int valid;
-    const int64_t row = sorted_source_row(s, x, valid);
-    uint8_t* sc = p.scale + scale_shuffle_idx(p.scale_n_pad, (int)x, y);
-    if (!valid || y >= p.scale_n) {
-        *sc = 0;
-        return;
+    const int64_t g0 = (int64_t)blockIdx.x * 32;
+    const int nv = *s.num_valid;
+    if (g0 >= nv) return;
+    // the group's 32 input rows, resolved once (not one dependent load per item)
+    __shared__ int64_t rows[32];
+    __shared__ int valid_of[32];
+    if (threadIdx.x < 32) {
+        int v;
+        rows[threadIdx.x] = sorted_source_row(s, g0 + threadIdx.x, v);
+        valid_of[threadIdx.x] = v;
     }
-    constexpr int OB = OUT_FP8 ? 32 : 16;   // output bytes per block
-    uint8_t* dst = p.out + row * p.out_stride + (int64_t)y * OB;
-    i32x4_t o[2] = {i32x4_t{0, 0, 0, 0}, i32x4_t{0, 0, 0, 0}};
-    uint32_t byte = 0;
-    if (!(s.sorted_w && s.sorted_w[x] == 0.0f)) {
-        const InT* src = reinterpret_cast<const InT*>(p.in) + row * p.in_stride + (int64_t)y * 32;
-        byte = quant_block32<InT, OUT_FP8, kRoundUp>(p, src, o);
+    __syncthreads();
+    const int items = 32 * p.scale_n_pad;
+    for (int it = threadIdx.x; it < items; it += 256) {
+        const int xr = it / p.scale_n_pad;
+        const int64_t x = g0 + xr;
+        const int y = it % p.scale_n_pad;
+        const int valid = valid_of[xr];
+        const int64_t row = rows[xr];
+        uint8_t* sc = p.scale + scale_shuffle_idx(p.scale_n_pad, (int)x, y);
+        if (!valid || y >= p.scale_n) {
+            *sc = 0;
+            continue;
+        }
+        constexpr int OB = OUT_FP8 ? 32 : 16;   // output bytes per block
+        uint8_t* dst = p.out + row * p.out_stride + (int64_t)y * OB;
+        i32x4_t o[2] = {i32x4_t{0, 0, 0, 0}, i32x4_t{0, 0, 0, 0}};
+        uint32_t byte = 0;
+        if (!(s.sorted_w && s.sorted_w[x] == 0.0f)) {
+            const InT* src = reinterpret_cast<const InT*>(p.in) + row * p.in_stride + (int64_t)y * 32;
+            byte = quant_block32<InT, OUT_FP8, kRoundUp>(p, src, o);
+        }
+        *reinterpret_cast<i32x4_t*>(dst) = o[0];
+        if constexpr (OUT_FP8) *reinterpret_cast<i32x4_t*>(dst + 16) = o[1];
+        *sc = (uint8_t)byte;
     }
-    *reinterpret_cast<i32x4_t*>(dst) = o[0];
-    if constexpr (OUT_FP8) *reinterpret_cast<i32x4_t*>(dst + 16) = o[1];
-    *sc = (uint8_t)byte;
 }
 
 // byte sort of per-row scales (csrc/kernels/quant_kernels.cu mxfp4_moe_sort):
-// plain [rows, K/32] -> sorted shuffled layout
+// plain [rows, K/32] -> sorted shuffled layout.  Byte (x = 32g + xr, y = 8y8
+// + yy) sits at g * 32 * pad8 + y8 * 256 + dword (yy % 4) * 16 + xr % 16, byte
+// (yy / 4) * 2 + xr / 16 (mx_scale_shuffle_idx).  Thread (g, y8, h) owns the
+// dwords with xr % 16 in [8h, 8h + 8): rows 8h.. and 16 + 8h.. of the group,
+// four 32-byte runs of the 256-byte block, built in registers.
 __global__ __launch_bounds__(256) void mx_scale_sort_kernel(const uint8_t* scale, int64_t scale_stride, uint8_t* out,
                                                             SortQuant s, int scale_n, int scale_n_pad) {
+    const int y8n = scale_n_pad / 8;
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t x = gid / scale_n_pad;
-    const int y = (int)(gid % scale_n_pad);
-    if (x >= s.sorted_rows) return;
-    int valid;
-    const int64_t row = sorted_source_row(s, x, valid);
-    out[scale_shuffle_idx(scale_n_pad, (int)x, y)] = (valid && y < scale_n) ? scale[row * scale_stride + y] : 0;
+    const int h = (int)(gid & 1);
+    const int64_t g = (gid >> 1) / y8n;
+    const int y8 = (int)((gid >> 1) % y8n);
+    if (g * 32 >= s.sorted_rows || g * 32 >= *s.num_valid) return;
+    const bool whole = (scale_stride % 8 == 0) && (y8 * 8 + 8 <= scale_n);
+    uint32_t o[32];
+#pragma unroll
+    for (int k = 0; k < 32; ++k) o[k] = 0;
+#pragma unroll
+    for (int xs = 0; xs < 16; ++xs) {
+        const int xr = (xs < 8) ? 8 * h + xs : 16 + 8 * h + (xs - 8);
+        int valid;
+        const int64_t row = sorted_source_row(s, g * 32 + xr, valid);
+        if (!valid) continue;
+        const uint8_t* src = scale + row * scale_stride + y8 * 8;
+        uint32_t lo = 0, hi = 0;
+        if (whole) {
+            const uint2 v = *reinterpret_cast<const uint2*>(src);
+            lo = v.x;
+            hi = v.y;
+        } else {
+#pragma unroll
+            for (int yy = 0; yy < 8; ++yy) {
+                const uint32_t b = (y8 * 8 + yy < scale_n) ? src[yy] : 0u;
+                if (yy < 4) lo |= b << (8 * yy);
+                else hi |= b << (8 * (yy - 4));
+            }
+        }
+#pragma unroll
+        for (int yy = 0; yy < 8; ++yy) {
+            const uint32_t b = ((yy < 4 ? lo : hi) >> (8 * (yy & 3))) & 0xffu;
+            o[(yy & 3) * 8 + (xs & 7)] |= b << (8 * ((yy >> 2) * 2 + (xs >> 3)));
+        }
+    }
+    uint8_t* dst = out + g * scale_n_pad * 32 + (int64_t)y8 * 256 + h * 32;
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4) {
+        *reinterpret_cast<i32x4_t*>(dst + k4 * 64) =
+            i32x4_t{(int)o[8 * k4], (int)o[8 * k4 + 1], (int)o[8 * k4 + 2], (int)o[8 * k4 + 3]};
+        *reinterpret_cast<i32x4_t*>(dst + k4 * 64 + 16) =
+            i32x4_t{(int)o[8 * k4 + 4], (int)o[8 * k4 + 5], (int)o[8 * k4 + 6], (int)o[8 * k4 + 7]};
+    }
 }
 
 struct QuantRequest {
@@ -459,8 +517,7 @@ int fused_dynamic_mx_quant_moe_sort_hip(aiter_tensor_t* out, aiter_tensor_t* sca
         s.sorted_rows = sorted_rows;
         s.token_num = token_num;
         s.topk = (int)(rows / token_num);
-        const int64_t nthreads = sorted_rows * scale_n_pad;
-        const dim3 grid((unsigned)((nthreads + 255) / 256));
+        const dim3 grid((unsigned)(sorted_rows / 32));
         hipStream_t st = reinterpret_cast<hipStream_t>(stream);
         if (in_dt == AITER_DTYPE_bf16) {
             if (fp8) mx_quant_sorted_kernel<uint16_t, true><<<grid, 256, 0, st>>>(p, s);
@@ -502,7 +559,7 @@ int mxfp4_moe_sort_hip(aiter_tensor_t* out_scale, aiter_tensor_t* scale, aiter_t
         s.sorted_rows = sorted_rows;
         s.token_num = token_num;
         s.topk = (int)(rows / token_num);
-        const int64_t nthreads = sorted_rows * scale_n_pad;
+        const int64_t nthreads = sorted_rows / 32 * (scale_n_pad / 8) * 2;
         mx_scale_sort_kernel<<<(unsigned)((nthreads + 255) / 256), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
             static_cast<const uint8_t*>(scale->ptr), scale->strides[scale->ndim - 2], static_cast<uint8_t*>(out_scale->ptr),
             s, scale_n, scale_n_pad);

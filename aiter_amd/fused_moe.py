@@ -63,12 +63,13 @@ def moe_sorting_fwd(topk_ids, topk_weights, sorted_token_ids, sorted_weights, so
 
 
 def moe_sorting(topk_ids, topk_weights, num_experts, model_dim, moebuf_dtype, block_size=BLOCK_SIZE_M,
-                expert_mask=None, num_local_tokens=None, dispatch_policy=0):
+                expert_mask=None, num_local_tokens=None, dispatch_policy=0, accumulate=True):
     """-> (sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf).
 
     Sizes as aiter/fused_moe.py:206-215: ``max_num_tokens_padded = M * topk +
     E * block_size - topk``; ``moe_buf`` [M, model_dim] is zeroed (stage 2
-    accumulates into it)."""
+    accumulates into it), or empty [0, 0] when ``accumulate`` is False and no
+    expert mask is given (stage 2 then reduces per-pair rows instead)."""
     device = topk_ids.device
     M, topk = topk_ids.shape
     if topk_ids.dtype != torch.int32:
@@ -85,7 +86,10 @@ def moe_sorting(topk_ids, topk_weights, num_experts, model_dim, moebuf_dtype, bl
     sorted_weights = torch.empty(max_num_tokens_padded, dtype=torch.float32, device=device)
     sorted_expert_ids = torch.empty(max_num_m_blocks, dtype=torch.int32, device=device)
     num_valid_ids = torch.empty(2, dtype=torch.int32, device=device)
-    moe_buf = torch.empty((M, model_dim), dtype=moebuf_dtype, device=device)
+    if expert_mask is not None or accumulate:
+        moe_buf = torch.empty((M, model_dim), dtype=moebuf_dtype, device=device)
+    else:
+        moe_buf = torch.empty((0, 0), dtype=moebuf_dtype, device=device)
     moe_sorting_fwd(topk_ids.contiguous(), topk_weights.contiguous(), sorted_ids, sorted_weights, sorted_expert_ids,
                     num_valid_ids, moe_buf, num_experts, int(block_size), expert_mask, num_local_tokens,
                     dispatch_policy)
@@ -138,8 +142,11 @@ def fused_dynamic_mx_quant_moe_sort(input, sorted_ids, num_valid_ids, token_num:
     is_stage1 = M == token_num
     eff_topk = 1 if is_stage1 else topk
     scale = _sorted_scale(sorted_ids, N, x.device)
-    switch = (8 * 256 / topk, 8 * 1024 / topk)
-    use_fused = (is_stage1 and M <= switch[0]) or (not is_stage1 and M <= switch[1] * eff_topk)
+    # stage 2 names every input row once, so the fused kernel never re-reads
+    # a row and is used at every size (the reference switches both stages to
+    # the split path above 8 * 1024 rows, aiter/ops/quant.py:1085-1114);
+    # stage 1 re-reads each token once per slot, so large inputs split
+    use_fused = (not is_stage1) or M <= 8 * 256 / topk
     if use_fused:
         out = torch.empty(M, out_cols, dtype=quant_dtype, device=x.device)
         fused_dynamic_mx_quant_moe_sort_hip(out, scale, x, sorted_ids, num_valid_ids, token_num, block_size,
@@ -171,11 +178,15 @@ def ck_moe_stage1(hidden_states, w1, w2, sorted_token_ids, sorted_expert_ids, nu
                   use_non_temporal_load: bool = False, dst_type: str | None = None, is_shuffled: bool = True) -> None:
     """out [token_num, topk, inter_dim] bf16 = act(gate) * up of the expert
     GEMM over the sorted rows; ``sorted_weights`` (doweight_stage1) scales
-    gate and up before the activation (aiter/fused_moe.py:3546-3573)."""
+    gate and up before the activation (aiter/fused_moe.py:3546-3573).
+    ``splitk``: 1 = one pass over K, n > 1 = n K slices summed by a second
+    kernel, 0 = chosen by the library (split when the tiles cannot fill the
+    GPU, as in decode)."""
     a = hidden_states if hidden_states.dtype == dtypes.fp8 else _u8(hidden_states)
     call("ck_moe_stage1", a, _u8(w1), None, sorted_token_ids, sorted_expert_ids, num_valid_ids,
          out.view(-1, out.shape[-1]), int(topk), kernelName or "", _u8(w1_scale), _u8(a1_scale), int(block_m or 32),
-         sorted_weights, int(quant_type), int(activation), int(splitk or 1), int(bool(use_non_temporal_load)),
+         sorted_weights, int(quant_type), int(activation), int(1 if splitk is None else splitk),
+         int(bool(use_non_temporal_load)),
          dst_type, int(bool(is_shuffled)))
 
 
@@ -185,12 +196,20 @@ def ck_moe_stage2(inter_states, w1, w2, sorted_token_ids, sorted_expert_ids, num
                   use_non_temporal_load: bool = False, dst_type: str | None = None, is_shuffled: bool = True) -> None:
     """out [token_num, model_dim] bf16 += sum over the routed pairs of
     weight * (a2 row @ w2[expert]^T) (aiter/fused_moe.py:3575-3680); ``out``
-    must start at zero (moe_sorting zeroes its moe_buf)."""
+    must start at zero (moe_sorting zeroes its moe_buf).  With ``out``
+    [token_num, topk, model_dim] each routed pair's weighted row is stored
+    instead (no atomics) and ``moe_sum`` reduces the slots."""
     a = inter_states.view(-1, inter_states.shape[-1])
     a = a if a.dtype == dtypes.fp8 else _u8(a)
     call("ck_moe_stage2", a, None, _u8(w2), sorted_token_ids, sorted_expert_ids, num_valid_ids, out, int(topk),
          kernelName or "", _u8(w2_scale), _u8(a2_scale), int(block_m or 32), sorted_weights, int(quant_type),
          int(activation), int(splitk), int(bool(use_non_temporal_load)), dst_type, int(bool(is_shuffled)))
+
+
+def moe_sum(input: torch.Tensor, output: torch.Tensor) -> None:
+    """output [M, D] = sum over slots of input [M, topk, D] (bf16; f32 sums in
+    slot order) (aiter/ops/moe_op.py:91-98)."""
+    call("moe_sum", input, output)
 
 
 # -------------------------------------------------------------------- fused
@@ -218,23 +237,45 @@ def get_inter_dim(w1_shape, w2_shape):
 def fused_moe_2stages(hidden_states, w1, w2, topk, sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids,
                       moe_out, block_size_M, activation=ActivationType.Silu, quant_type=QuantType.per_1x32,
                       doweight_stage1=False, q_dtype_a=dtypes.fp4x2, w1_scale=None, w2_scale=None,
-                      num_local_tokens=None):
+                      num_local_tokens=None, expert_mask=None):
     """The per_1x32 two-stage flow of aiter/fused_moe.py:2892-3276: quant +
     sort of the tokens, stage 1, quant + sort of the stage-1 output, stage 2
     accumulating into ``moe_out``."""
     token_num = hidden_states.shape[0]
     E, model_dim, inter_dim = get_inter_dim(w1.shape, w2.shape)
+    # per-pair rows miss the pairs routed to masked experts or past
+    # num_local_tokens, so those cases accumulate (as in the reference)
+    reduce = expert_mask is None and num_local_tokens is None and _use_reduce(token_num, topk)
+    if moe_out.numel() == 0:
+        moe_out = torch.empty((token_num, model_dim), dtype=dtypes.bf16, device=hidden_states.device)
     a1, a1_scale = fused_dynamic_mx_quant_moe_sort(hidden_states, sorted_ids, num_valid_ids, token_num, topk,
                                                    block_size_M, q_dtype_a, num_rows=num_local_tokens,
                                                    sorted_weights=sorted_weights)
     a2 = torch.empty((token_num, topk, inter_dim), dtype=dtypes.bf16, device=hidden_states.device)
     ck_moe_stage1(a1, w1, w2, sorted_ids, sorted_expert_ids, num_valid_ids, a2, topk, "", w1_scale, a1_scale,
-                  block_size_M, sorted_weights if doweight_stage1 else None, int(quant_type), int(activation))
+                  block_size_M, sorted_weights if doweight_stage1 else None, int(quant_type), int(activation), splitk=0)
     a2q, a2_scale = fused_dynamic_mx_quant_moe_sort(a2.view(-1, inter_dim), sorted_ids, num_valid_ids, token_num,
                                                     topk, block_size_M, q_dtype_a, sorted_weights=sorted_weights)
-    ck_moe_stage2(a2q, w1, w2, sorted_ids, sorted_expert_ids, num_valid_ids, moe_out, topk, "", w2_scale, a2_scale,
-                  block_size_M, None if doweight_stage1 else sorted_weights, int(quant_type))
+    if reduce:
+        # one row per routed pair, then a fixed-order sum over the slots: device-
+        # wide atomics cost one memory-side operation per 4 bytes, which
+        # dominates once there are more than a few hundred routed rows
+        per_pair = torch.empty((token_num, topk, model_dim), dtype=moe_out.dtype, device=moe_out.device)
+        ck_moe_stage2(a2q, w1, w2, sorted_ids, sorted_expert_ids, num_valid_ids, per_pair, topk, "", w2_scale,
+                      a2_scale, block_size_M, None if doweight_stage1 else sorted_weights, int(quant_type))
+        moe_sum(per_pair, moe_out)
+    else:
+        ck_moe_stage2(a2q, w1, w2, sorted_ids, sorted_expert_ids, num_valid_ids, moe_out, topk, "", w2_scale,
+                      a2_scale, block_size_M, None if doweight_stage1 else sorted_weights, int(quant_type))
     return moe_out
+
+
+REDUCE_MIN_ROWS = 128
+
+
+def _use_reduce(token_num: int, topk: int) -> bool:
+    """Per-pair rows + moe_sum instead of atomics: from REDUCE_MIN_ROWS routed rows."""
+    return token_num * topk >= REDUCE_MIN_ROWS
 
 
 def fused_moe(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None, activation=ActivationType.Silu,
@@ -271,9 +312,10 @@ def fused_moe(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None, ac
     global_E = expert_mask.numel() if expert_mask is not None else E
     bm = block_size_M if block_size_M and block_size_M > 0 else get_block_size_M(token_num, topk, global_E,
                                                                                  inter_dim)
+    accumulate = not (expert_mask is None and num_local_tokens is None and _use_reduce(token_num, topk))
     sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf = moe_sorting(
         topk_ids, topk_weight, global_E, model_dim, dtype, bm, expert_mask, num_local_tokens,
-        moe_sorting_dispatch_policy)
+        moe_sorting_dispatch_policy, accumulate=accumulate)
     return fused_moe_2stages(hidden_states, w1, w2, topk, sorted_ids, sorted_weights, sorted_expert_ids,
                              num_valid_ids, moe_buf, bm, activation, quant_type, doweight_stage1, dtypes.fp4x2,
-                             w1_scale, w2_scale, num_local_tokens)
+                             w1_scale, w2_scale, num_local_tokens, expert_mask)

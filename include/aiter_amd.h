@@ -198,8 +198,11 @@ int mxfp4_moe_sort_hip(aiter_tensor_t* out_scale, aiter_tensor_t* scale, aiter_t
  * sorted_weights, if given, scale gate and up first).  Stage 2: w2
  * [E, model_dim, inter/2], inter_states [token_num*topk, inter(/2)], out bf16
  * [token_num, model_dim] += weight * GEMM (packed bf16 atomics; out must start
- * at zero).  block_m (32, 64, 128) must equal the sort's unit_size; splitk
- * must be <= 1.  w2 (stage 1) and w1 (stage 2) may be NULL. */
+ * at zero), or, with out [token_num, topk, model_dim], each pair's weighted
+ * row stored (then moe_sum).  block_m (32, 64, 128) must equal the sort's
+ * unit_size.  Stage-1 splitk: 1 one pass over K, n > 1 n K slices (f32
+ * partials in the library workspace, summed by a second kernel), 0 chosen
+ * here; stage 2 ignores it.  w2 (stage 1) and w1 (stage 2) may be NULL. */
 int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
                   aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
                   aiter_tensor_t* out, int topk, const char* kernelName, aiter_tensor_t* w1_scale,
@@ -212,6 +215,11 @@ int ck_moe_stage2(aiter_tensor_t* inter_states, aiter_tensor_t* w1, aiter_tensor
                   aiter_tensor_t* a2_scale, int block_m, aiter_tensor_t* sorted_weights, int quant_type,
                   int activation, int splitk, int use_non_temporal_load, const char* dst_type, int is_shuffled,
                   aiter_stream_t stream);
+
+/* Slot reduction: replaces _moe_sum (aiter/ops/moe_op.py:87-98): output
+ * bf16 [M, D] = sum over topk of input bf16 [M, topk, D], f32 sums in slot
+ * order (the reduce form of stage 2: ck_moe_stage2 with out [M, topk, D]). */
+int moe_sum(aiter_tensor_t* input, aiter_tensor_t* output, aiter_stream_t stream);
 
 /* ---- library introspection and workspace --------------------------------
  * The reference keeps its kernel list in per-arch CSVs next to its ASM code

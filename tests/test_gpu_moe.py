@@ -3,8 +3,8 @@
 * moe_sorting: bit-exact (ids, weights, block table, counts), single- and
   multi-workgroup paths, expert mask, num_local_tokens; moe_buf zeroed.
 * sorted MX quant (fused and split paths, MXFP4 and MXFP8, stage-1 and
-  stage-2 row indexing): quantised rows and the whole sorted scale buffer
-  bit-exact.
+  stage-2 row indexing): quantised rows and the sorted scale rows below
+  num_valid_ids[0] (all the GEMM reads) bit-exact.
 * stage 1 (act(gate) * up, bf16): every element within rtol = atol = 1e-2 of
   the f32 oracle on the same quantised operands, for each row block, a4w4 and
   a8w4, Silu and Gelu, routing weight in stage 1 or not.
@@ -100,10 +100,19 @@ def test_quant_sort_exact(cuda, fp8, m, topk, stage):
     fn = aiter_amd.fused_dynamic_mxfp8_quant_moe_sort if fp8 else aiter_amd.fused_dynamic_mxfp4_quant_moe_sort
     q, sc = fn(_bf16_dev(x, cuda), s, nv, m, topk, bs, sorted_weights=sw)
     torch.cuda.synchronize()
-    rq, written, rsc = MO.quant_sort_ref(x, s.cpu().numpy(), int(nv[0].item()), m, fp8)
+    n_valid = int(nv[0].item())
+    rq, written, rsc = MO.quant_sort_ref(x, s.cpu().numpy(), n_valid, m, fp8)
     gq = q.view(torch.uint8).cpu().numpy()
     np.testing.assert_array_equal(gq[written], rq[written])
-    np.testing.assert_array_equal(sc.view(torch.uint8).cpu().numpy(), rsc)
+    # positions past num_valid_ids[0] are never read by the GEMM and stay unwritten
+    np.testing.assert_array_equal(sc.view(torch.uint8).cpu().numpy()[:n_valid], rsc[:n_valid])
+    # the split form directly: per-row quant, then the byte sort
+    qd, per_row = aiter_amd.per_1x32_mx_quant_hip(_bf16_dev(x, cuda), quant_dtype=torch.float8_e4m3fn if fp8 else
+                                                  aiter_amd.dtypes.fp4x2, shuffle=False)
+    sc2 = aiter_amd.mxfp4_moe_sort_fwd(per_row, s, nv, m, k)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(qd.view(torch.uint8).cpu().numpy(), rq)
+    np.testing.assert_array_equal(sc2.view(torch.uint8).cpu().numpy()[:n_valid], rsc[:n_valid])
 
 
 # -------------------------------------------------------------------- stages
@@ -131,11 +140,14 @@ def _stage_setup(m, e, topk, dim, inter, bs, seed, cuda, fp8):
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("act,doweight", [(0, False), (1, False), (0, True)])
 @pytest.mark.parametrize("m", [5, 200])
-def test_stage1(cuda, bs, fp8, act, doweight, m):
+@pytest.mark.parametrize("splitk", [1, 0, 3])
+def test_stage1(cuda, bs, fp8, act, doweight, m, splitk):
+    """splitk 1: one pass over K; 0: library choice (K split for these
+    under-filled grids); 3: K = 512 has 2 stages, so 2 slices of 1."""
     import aiter_amd
 
     e, topk, dim, inter = 8, 3, 512, 256
-    announce(f"moe stage1 m={m} bs={bs} fp8={fp8} act={act} doweight={doweight}")
+    announce(f"moe stage1 m={m} bs={bs} fp8={fp8} act={act} doweight={doweight} splitk={splitk}")
     rng, ids, w, (s, sw, se, nv, _) = _stage_setup(m, e, topk, dim, inter, bs, 100 + m + bs, cuda, fp8)
     x = to_bf16_f32(rng.standard_normal((m, dim)).astype(np.float32))
     qfn = O.quant_mxfp8 if fp8 else O.quant_mxfp4
@@ -146,7 +158,7 @@ def test_stage1(cuda, bs, fp8, act, doweight, m):
     a_dev = _dev(aq, cuda).view(torch.float8_e4m3fn) if fp8 else _dev(aq, cuda)
     out = torch.empty((m, topk, inter), dtype=torch.bfloat16, device=cuda)
     aiter_amd.ck_moe_stage1(a_dev, w1d, None, s, se, nv, out, topk, "", w1sd, _dev(a_sorted, cuda), bs,
-                            sw if doweight else None, 3, act)
+                            sw if doweight else None, 3, act, splitk=splitk)
     torch.cuda.synchronize()
     adeq = O.dequant_mxfp8(aq, a_s) if fp8 else O.dequant_mxfp4(aq, a_s)
     ref = MO.moe_stage1_ref(adeq, MO.dequant_experts(w1q, w1s), ids, w, act, doweight)
@@ -155,7 +167,7 @@ def test_stage1(cuda, bs, fp8, act, doweight, m):
     assert ok, msg
 
 
-def _stage2_run(cuda, m, e, topk, dim, inter, bs, fp8, seed):
+def _stage2_run(cuda, m, e, topk, dim, inter, bs, fp8, seed, per_pair=False, tile=""):
     import aiter_amd
 
     rng, ids, w, (s, sw, se, nv, buf) = _stage_setup(m, e, topk, dim, inter, bs, seed, cuda, fp8)
@@ -166,19 +178,30 @@ def _stage2_run(cuda, m, e, topk, dim, inter, bs, fp8, seed):
     w2q, w2s = _weights(e, dim, inter, rng)
     w2d, w2sd = _w_dev(w2q, w2s, cuda)
     a_dev = _dev(aq, cuda).view(torch.float8_e4m3fn) if fp8 else _dev(aq, cuda)
-    aiter_amd.ck_moe_stage2(a_dev, None, w2d, s, se, nv, buf, topk, "", w2sd, _dev(a_sorted, cuda), bs, sw, 3)
+    out = torch.empty((m, topk, dim), dtype=torch.bfloat16, device=cuda) if per_pair else buf
+    aiter_amd.ck_moe_stage2(a_dev, None, w2d, s, se, nv, out, topk, tile, w2sd, _dev(a_sorted, cuda), bs, sw, 3)
     torch.cuda.synchronize()
     adeq = O.dequant_mxfp8(aq, a_s) if fp8 else O.dequant_mxfp4(aq, a_s)
-    ref = MO.moe_stage2_ref(adeq.reshape(m, topk, inter), MO.dequant_experts(w2q, w2s), ids, w, True)
-    return buf.float().cpu().numpy(), O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref))
+    w2f = MO.dequant_experts(w2q, w2s)
+    if per_pair:
+        # each routed pair's weighted row: weight * (a2 row @ w2[e]^T)
+        ref = np.stack([np.stack([w[t, k] * (adeq[t * topk + k] @ w2f[ids[t, k]].T) for k in range(topk)])
+                        for t in range(m)])
+        return out, O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref))
+    ref = MO.moe_stage2_ref(adeq.reshape(m, topk, inter), w2f, ids, w, True)
+    return out.float().cpu().numpy(), O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref))
 
 
-@pytest.mark.parametrize("bs", [32, 64, 128])
+STAGE2_TILES = [(32, ""), (64, ""), (64, "moe_m32"), (128, ""), (128, "moe_m32"), (128, "moe_m128")]
+
+
+@pytest.mark.parametrize("bs,tile", STAGE2_TILES)
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("m", [3, 150])
-def test_stage2_topk1(cuda, bs, fp8, m):
-    announce(f"moe stage2 topk=1 m={m} bs={bs} fp8={fp8}")
-    got, ref = _stage2_run(cuda, m, 8, 1, 512, 256, bs, fp8, 200 + m + bs)
+def test_stage2_topk1(cuda, bs, tile, fp8, m):
+    """GEMM row blocks smaller than the sort's block (kernelName moe_mNN)."""
+    announce(f"moe stage2 topk=1 m={m} bs={bs} tile={tile} fp8={fp8}")
+    got, ref = _stage2_run(cuda, m, 8, 1, 512, 256, bs, fp8, 200 + m + bs, tile=tile)
     ok, msg = allclose_report(got, ref)
     assert ok, msg
 
@@ -190,6 +213,28 @@ def _accept(got, ref, max_diff=1e-4, min_close=0.98):
     d = MO.logits_diff(ref, got)
     assert np.all(np.isfinite(got)), "non-finite output"
     assert d <= max_diff and close >= min_close, f"logits_diff {d:.3g}, within 1e-2: {close:.4f}"
+
+
+@pytest.mark.parametrize("bs,tile", STAGE2_TILES)
+@pytest.mark.parametrize("fp8", [False, True])
+def test_stage2_per_pair_and_moe_sum(cuda, bs, tile, fp8):
+    """Per-pair rows (no atomics): every row within 1e-2 of its oracle row;
+    moe_sum of those rows bit-exact against an f32 slot-order sum."""
+    import aiter_amd
+
+    m, topk, dim = 70, 6, 512
+    announce(f"moe stage2 per-pair topk={topk} bs={bs} tile={tile} fp8={fp8}")
+    out, ref = _stage2_run(cuda, m, 16, topk, dim, 256, bs, fp8, 350 + bs, per_pair=True, tile=tile)
+    got = out.float().cpu().numpy()
+    ok, msg = allclose_report(got, ref)
+    assert ok, msg
+    summed = torch.empty((m, dim), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.moe_sum(out, summed)
+    torch.cuda.synchronize()
+    acc = np.zeros((m, dim), dtype=np.float32)
+    for k in range(topk):
+        acc = (acc + got[:, k]).astype(np.float32)
+    np.testing.assert_array_equal(summed.view(torch.int16).cpu().numpy().view(np.uint16), O.f32_to_bf16_bits(acc))
 
 
 @pytest.mark.parametrize("bs", [32, 128])
