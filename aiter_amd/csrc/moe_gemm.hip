@@ -10,6 +10,7 @@
 #include "gemm_kernels.h"
 #include "mfma32.h"
 #include "gemm_flat.h"
+#include "moe_stage2.h"
 
 namespace {
 
@@ -58,17 +59,28 @@ void launch_bm(int bm, dim3 grid, const GemmParams& p, const MoeParams& mq, hipS
     }
 }
 
-// GEMM row block: kernelName "moe_m32" / "moe_m64" / "moe_m128" picks it;
+// GEMM row block: kernelName "moe_m32" / "moe_m64" / "moe_m128" picks it
+// (a "_flat" suffix keeps stage 2 on the flat tile kernel);
 // otherwise the sort's block for stage 1 and at most 64 rows for stage 2
 // (K is one or two stages there, so the tile is latency-bound and the smaller
 // tile's lower register count lets two workgroups share a CU)
 int tile_from_name(const char* name, int stage, int block_m) {
     if (name && name[0]) {
         const std::string n(name);
-        AA_CHECK(n.rfind("moe_m", 0) == 0, "unknown MoE kernel name '", n, "' (moe_m32 / moe_m64 / moe_m128)");
+        AA_CHECK(n.rfind("moe_m", 0) == 0, "unknown MoE kernel name '", n,
+                 "' (moe_m32 / moe_m64 / moe_m128, optional suffix _flat)");
         return std::atoi(n.c_str() + 5);
     }
     return stage == 1 ? block_m : std::min(block_m, 64);
+}
+
+template <int KA, int BM>
+void launch_s2_kw(int kw, dim3 grid, const GemmParams& p, const MoeParams& mq, const MoeS2Params& sp, hipStream_t st) {
+    switch (kw) {
+        case 1: moe_stage2_stream_kernel<KA, BM, 1><<<grid, 256, 0, st>>>(p, mq, sp); break;
+        case 2: moe_stage2_stream_kernel<KA, BM, 2><<<grid, 256, 0, st>>>(p, mq, sp); break;
+        default: fail("moe", "stream stage 2: K / 256 must be 1 or 2");
+    }
 }
 
 void run_stage(const StageArgs& s, hipStream_t st) {
@@ -229,6 +241,30 @@ void run_stage(const StageArgs& s, hipStream_t st) {
             AA_HIP(hipGetLastError());
             const int64_t n = mq.ws_rows * (mq.inter / 4);
             moe_stage1_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
+        }
+    } else if ((bm == 32 || bm == 64) && (K == 256 || (K == 512 && bm == 64 && a_fp8)) &&
+               !(s.kernel_name && std::string(s.kernel_name).find("flat") != std::string::npos)) {
+        // short K: the streaming kernel (A in registers, a group of N tiles per
+        // workgroup, about 2048 workgroups in all).  Enabled where it fits in
+        // registers and is parity-tested: K = 256, and K = 512 for MXFP8 A with
+        // 64-row blocks.  (K = 512 with 32-row blocks gave wrong results on the
+        // GPU although a CPU emulation of its addressing matches the oracle;
+        // those shapes take the flat kernel until the cause is found.)
+        MoeS2Params sp{};
+        const int64_t total_tiles = used * tiles_n;
+        sp.tiles_per_group = (int)std::min<int64_t>(tiles_n, std::max<int64_t>(1, (total_tiles + 2047) / 2048));
+        sp.groups = (tiles_n + sp.tiles_per_group - 1) / sp.tiles_per_group;
+        sp.row_blocks = (int)used;
+        sp.a_scale_rows = sorted_rows;
+        const int64_t wgs = (int64_t)sp.row_blocks * sp.groups;
+        const dim3 g2((unsigned)((wgs + 7) / 8 * 8));
+        const int kw = (int)(K / 256);
+        if (a_fp8) {
+            if (bm == 32) launch_s2_kw<kFp8, 32>(kw, g2, p, mq, sp, st);
+            else launch_s2_kw<kFp8, 64>(kw, g2, p, mq, sp, st);
+        } else {
+            if (bm == 32) launch_s2_kw<kFp4, 32>(kw, g2, p, mq, sp, st);
+            else launch_s2_kw<kFp4, 64>(kw, g2, p, mq, sp, st);
         }
     } else {
         if (a_fp8) launch_bm<kFp8, kMoeStage2>(bm, grid, p, mq, st);

@@ -219,6 +219,49 @@ def bench_extra(dev):
     out["fused_rms_mxfp4_quant_8192x8192"] = {"us": round(tf * 1e6, 1),
                                               "GBps": round(8192 * 8192 * (2 + 0.5 + 1 / 32) / tf / 1e9, 1),
                                               "unfused_us": round(tu * 1e6, 1)}
+    del xa
+    out["fused_moe_a4w4_deepseek"] = bench_moe(dev)
+    return out
+
+
+def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
+    """fused_moe A4W4 at the reference test's DeepSeek shape (op_tests/test_moe_2stage.py
+    defaults: model_dim 7168, inter_dim 256, 257 experts, topk 9), graph-captured
+    so that host time is excluded.  Weights are random fp4 bytes with scale
+    bytes near 2^-6 (preshuffled); routing softmax-top-9 of random scores.
+    Roofline: HBM bytes of the experts a call touches (w1 + w2 + scales, each
+    read once) and of the activations, against 8 TB/s; FLOPs against the
+    dense MXFP4 peak."""
+    import aiter_amd
+
+    E, topk, dim, inter = 257, 9, 7168, 256
+    g = torch.Generator(device=dev).manual_seed(11)
+    w1 = torch.randint(0, 256, (E * 2 * inter, dim // 2), dtype=torch.uint8, device=dev, generator=g)
+    w2 = torch.randint(0, 256, (E * dim, inter // 2), dtype=torch.uint8, device=dev, generator=g)
+    w1s = aiter_amd.shuffle_scale(torch.randint(119, 123, (E * 2 * inter, dim // 32), dtype=torch.uint8, device=dev,
+                                                generator=g))
+    w2s = aiter_amd.shuffle_scale(torch.randint(119, 123, (E * dim, inter // 32), dtype=torch.uint8, device=dev,
+                                                generator=g))
+    w1 = aiter_amd.shuffle_weight(w1).view(E, 2 * inter, dim // 2)
+    w2 = aiter_amd.shuffle_weight(w2).view(E, dim, inter // 2)
+    per_expert = 2 * inter * dim // 2 + dim * inter // 2 + 2 * inter * dim // 32 + dim * inter // 32
+    out = []
+    for m in tokens:
+        x = torch.randn(m, dim, device=dev, generator=g).to(torch.bfloat16)
+        tw, ti = torch.topk(torch.softmax(torch.randn(m, E, device=dev, generator=g), -1), topk, -1)
+        tw = (tw / tw.sum(-1, keepdim=True)).float()
+        ti = ti.to(torch.int32)
+        fn = lambda: aiter_amd.fused_moe(x, w1, w2, tw, ti, quant_type=aiter_amd.QuantType.per_1x32, w1_scale=w1s,
+                                         w2_scale=w2s)
+        t = time_graph(fn, 10, 2)
+        touched = int(torch.unique(ti).numel())
+        nbytes = touched * per_expert + m * dim * 2 * 2
+        flop = 2 * m * topk * (2 * inter * dim + dim * inter)
+        out.append({"tokens": m, "us": round(t * 1e6, 1), "TFLOPs": round(flop / t / 1e12, 1),
+                    "frac_mxfp4_peak": round(flop / t / 1e12 / PEAK_MXFP4, 4), "experts_touched": touched,
+                    "GBps": round(nbytes / t / 1e9, 1), "frac_hbm": round(nbytes / t / 1e9 / PEAK_HBM, 4),
+                    "block_m": aiter_amd.get_block_size_M(m, topk, E, inter)})
+        log(f"fused_moe tokens={m}: {out[-1]}")
     return out
 
 
@@ -338,6 +381,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=400)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only")
+    ap.add_argument("--moe", action="store_true", help="only the fused-MoE workloads (for profiling)")
     ap.add_argument("--pmc", action="store_true",
                     help="only the launches of the HBM-traffic counter runs (copy calibration + A4W4 8192^3)")
     args = ap.parse_args()
@@ -352,6 +396,9 @@ def main():
     import aiter_amd  # noqa: F401  (fails loudly if the HIP library is missing)
     if args.pmc:
         pmc_workload(dev)
+        return
+    if args.moe:
+        print(json.dumps({"fused_moe_a4w4_deepseek": bench_moe(dev)}), flush=True)
         return
 
     log("prefill A4W4 8192^3")

@@ -192,7 +192,10 @@ def _stage2_run(cuda, m, e, topk, dim, inter, bs, fp8, seed, per_pair=False, til
     return out.float().cpu().numpy(), O.bf16_bits_to_f32(O.f32_to_bf16_bits(ref))
 
 
-STAGE2_TILES = [(32, ""), (64, ""), (64, "moe_m32"), (128, ""), (128, "moe_m32"), (128, "moe_m128")]
+# (sort block, kernelName): "" = library choice (streaming kernel, row block <= 64);
+# moe_mNN picks the row block, "_flat" keeps the flat tile kernel
+STAGE2_TILES = [(32, ""), (64, ""), (64, "moe_m32"), (128, ""), (128, "moe_m32"), (128, "moe_m128"),
+                (32, "moe_m32_flat"), (64, "moe_m64_flat")]
 
 
 @pytest.mark.parametrize("bs,tile", STAGE2_TILES)
@@ -213,6 +216,16 @@ def _accept(got, ref, max_diff=1e-4, min_close=0.98):
     d = MO.logits_diff(ref, got)
     assert np.all(np.isfinite(got)), "non-finite output"
     assert d <= max_diff and close >= min_close, f"logits_diff {d:.3g}, within 1e-2: {close:.4f}"
+
+
+@pytest.mark.parametrize("inter,bs,tile", [(512, 32, ""), (512, 64, ""), (512, 64, "moe_m64_flat"), (768, 32, "")])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_stage2_longer_k(cuda, inter, bs, tile, fp8):
+    """inter_dim 512 (two K windows in the streaming kernel) and 768 (flat kernel)."""
+    announce(f"moe stage2 inter={inter} bs={bs} tile={tile} fp8={fp8}")
+    got, ref = _stage2_run(cuda, 40, 8, 1, 512, inter, bs, fp8, 260 + inter + bs, tile=tile)
+    ok, msg = allclose_report(got, ref)
+    assert ok, msg
 
 
 @pytest.mark.parametrize("bs,tile", STAGE2_TILES)
