@@ -110,17 +110,12 @@ __device__ void scan_experts(const SortParams& p, SortSmem& sm, int n_tokens) {
     __syncthreads();
     const int total = sm.off[p.E];
     const int pad_id = (p.topk << 24) | p.M;
-    if (live) {
+    (void)c;
+    (void)pad_id;
+    // padding entries: the whole list was filled with the padding id before
+    // (fill_padding); placement overwrites the real entries
+    if (live)
         for (int b = start / p.bs; b < (start + padded) / p.bs && b < p.max_blocks; ++b) p.sorted_eids[b] = lid;
-        for (int q = start + c; q < start + padded && q < p.max_padded; ++q) {
-            p.sorted_ids[q] = pad_id;
-            p.sorted_w[q] = 0.0f;
-        }
-    }
-    for (int q = total + threadIdx.x; q < p.max_padded; q += kThreads) {
-        p.sorted_ids[q] = pad_id;
-        p.sorted_w[q] = 0.0f;
-    }
     for (int b = total / p.bs + threadIdx.x; b < p.max_blocks; b += kThreads) p.sorted_eids[b] = -1;
     if (threadIdx.x == 0) {
         p.num_valid[0] = total;
@@ -128,14 +123,25 @@ __device__ void scan_experts(const SortParams& p, SortSmem& sm, int n_tokens) {
     }
 }
 
-// places entries [c0, c0 + 1024) at sm.base[e] onward and advances sm.base
-__device__ void place_chunk(const SortParams& p, SortSmem& sm, int c0, int n) {
+// positions [q0, q1) of sorted_ids / sorted_weights <- padding id / 0
+// (coalesced; threads of `nthreads` starting at `t`)
+__device__ void fill_padding(const SortParams& p, int64_t q0, int64_t q1, int t, int nthreads) {
+    const int pad_id = (p.topk << 24) | p.M;
+    for (int64_t q = q0 + t; q < q1; q += nthreads) {
+        p.sorted_ids[q] = pad_id;
+        p.sorted_w[q] = 0.0f;
+    }
+}
+
+// places entries [c0, c0 + 1024) at sm.base[e] onward and advances sm.base;
+// e_in >= -1: this thread's entry already resolved (expert, weight w_in)
+__device__ void place_chunk(const SortParams& p, SortSmem& sm, int c0, int n, int e_in = -2, float w_in = 0.0f) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     reinterpret_cast<i32x4_t*>(&sm.wcnt[0][0])[tid] = i32x4_t{0, 0, 0, 0};
     static_assert(sizeof(sm.wcnt) == kThreads * 16, "one 16-byte clear per thread");
     __syncthreads();
     const int i = c0 + tid;
-    const int e = expert_of(p, i, n);
+    const int e = e_in >= -1 ? e_in : expert_of(p, i, n);
     // rank among the lanes of this wave with the same expert and a lower lane
     uint64_t act = __ballot(e >= 0);
     const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
@@ -155,7 +161,7 @@ __device__ void place_chunk(const SortParams& p, SortSmem& sm, int c0, int n) {
         const int t = i / p.topk, s = i - t * p.topk;
         if (pos < p.max_padded) {
             p.sorted_ids[pos] = (s << 24) | t;
-            p.sorted_w[pos] = p.topk_w[(int64_t)t * p.w_stride + s];
+            p.sorted_w[pos] = e_in >= -1 ? w_in : p.topk_w[(int64_t)t * p.w_stride + s];
         }
     }
     __syncthreads();
@@ -167,26 +173,46 @@ __device__ void place_chunk(const SortParams& p, SortSmem& sm, int c0, int n) {
     __syncthreads();
 }
 
-__global__ __launch_bounds__(kThreads) void moe_sort_single(SortParams p) {
+__global__ __launch_bounds__(kThreads) void moe_sort_single(SortParams p, uint8_t* zero_buf, int64_t zero_bytes) {
     __shared__ SortSmem sm;
     const int nt = local_tokens(p);
     const int n = nt * p.topk;
-    for (int x = threadIdx.x; x < kMaxE; x += kThreads) sm.cnt[x] = 0;
+    // the first chunk's entries stay in registers from one load (expert id
+    // and weight issued together); later chunks reload theirs
+    const int tid = threadIdx.x;
+    const int e0 = expert_of(p, tid, n);
+    float w0 = 0.0f;
+    if (tid < n) {
+        const int t = tid / p.topk, s = tid - t * p.topk;
+        w0 = p.topk_w[(int64_t)t * p.w_stride + s];
+    }
+    // a small moe_buf is cleared here rather than by a second launch
+    for (int64_t b = (int64_t)tid * 16; b + 16 <= zero_bytes; b += kThreads * 16)
+        *reinterpret_cast<i32x4_t*>(zero_buf + b) = i32x4_t{0, 0, 0, 0};
+    for (int64_t b = zero_bytes / 16 * 16 + tid; b < zero_bytes; b += kThreads) zero_buf[b] = 0;
+    fill_padding(p, 0, p.max_padded, tid, kThreads);   // ordered before placement by the barriers below
+    for (int x = tid; x < kMaxE; x += kThreads) sm.cnt[x] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < n; i += kThreads) {
+    if (e0 >= 0) atomicAdd(&sm.cnt[e0], 1);
+    for (int i = tid + kThreads; i < n; i += kThreads) {
         const int e = expert_of(p, i, n);
         if (e >= 0) atomicAdd(&sm.cnt[e], 1);
     }
     __syncthreads();
     scan_experts(p, sm, nt);
-    for (int x = threadIdx.x; x < p.E; x += kThreads) sm.base[x] = sm.off[x];
+    for (int x = tid; x < p.E; x += kThreads) sm.base[x] = sm.off[x];
     __syncthreads();
-    for (int c0 = 0; c0 < n; c0 += kThreads) place_chunk(p, sm, c0, n);
+    place_chunk(p, sm, 0, n, e0, w0);
+    for (int c0 = kThreads; c0 < n; c0 += kThreads) place_chunk(p, sm, c0, n);
 }
 
 __global__ __launch_bounds__(kThreads) void moe_sort_count(SortParams p) {
     __shared__ int cnt[kMaxE];
     const int n = local_tokens(p) * p.topk;
+    // this chunk's share of the padding fill (placement runs in a later launch)
+    const int64_t share = ((int64_t)p.max_padded + gridDim.x - 1) / gridDim.x;
+    fill_padding(p, blockIdx.x * share, min<int64_t>((int64_t)(blockIdx.x + 1) * share, p.max_padded), threadIdx.x,
+                 kThreads);
     for (int x = threadIdx.x; x < p.E; x += kThreads) cnt[x] = 0;
     __syncthreads();
     const int e = expert_of(p, blockIdx.x * kThreads + threadIdx.x, n);
@@ -301,8 +327,13 @@ int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aite
         p.max_blocks = (int)max_blocks;
         const int64_t entries = (int64_t)M * topk;
         p.nchunks = (int)((entries + kThreads - 1) / kThreads);
+        const int64_t buf_bytes =
+            (moe_buf && moe_buf->numel > 0) ? (int64_t)moe_buf->numel * (int64_t)dtype_size(moe_buf->dtype) : 0;
+        const bool zero_inside = p.nchunks <= kSingleChunks && buf_bytes <= (1 << 20);
         if (p.nchunks <= kSingleChunks) {
-            moe_sort_single<<<1, kThreads, 0, st>>>(p);
+            moe_sort_single<<<1, kThreads, 0, st>>>(p, zero_inside && buf_bytes ? static_cast<uint8_t*>(moe_buf->ptr)
+                                                                                  : nullptr,
+                                                    zero_inside ? buf_bytes : 0);
         } else {
             p.ws = static_cast<int*>(
                 lib_workspace(topk_ids->device_id, st, (size_t)(p.nchunks + 1) * num_experts * sizeof(int)));
@@ -311,8 +342,8 @@ int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aite
             moe_sort_place<<<p.nchunks, kThreads, 0, st>>>(p);
         }
         AA_HIP(hipGetLastError());
-        if (moe_buf && moe_buf->numel > 0) {
-            const int64_t bytes = (int64_t)moe_buf->numel * (int64_t)dtype_size(moe_buf->dtype);
+        if (buf_bytes > 0 && !zero_inside) {
+            const int64_t bytes = buf_bytes;
             const int64_t blocks = std::min<int64_t>((bytes / 16 + 255) / 256 + 1, 4096);
             fill_zero_kernel<<<(unsigned)blocks, 256, 0, st>>>(static_cast<uint8_t*>(moe_buf->ptr), bytes);
             AA_HIP(hipGetLastError());

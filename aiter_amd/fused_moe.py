@@ -215,14 +215,15 @@ def moe_sum(input: torch.Tensor, output: torch.Tensor) -> None:
 # -------------------------------------------------------------------- fused
 @functools.lru_cache(maxsize=2048)
 def get_block_size_M(token: int, topk: int, expert: int, inter_dim: int) -> int:
-    """Row block of the sorted list: the smallest of 32 / 64 / 128 that the
-    average routed rows per expert fill (decode -> 32, prefill -> 128); the
-    reference picks from its tuned table with the same candidates
+    """Row block of the sorted list, from the average routed rows per expert:
+    32 up to 24 rows, 64 up to 512, 128 above (measured at the DeepSeek shape,
+    257 experts x topk 9: 64 is fastest from ~1000 to 8192 tokens, 32 below);
+    the reference picks from its tuned table with the same candidates
     (aiter/fused_moe.py:1178-1193)."""
     per_expert = token * topk / max(expert, 1)
     if per_expert <= 24:
         return 32
-    if per_expert <= 96:
+    if per_expert <= 512:
         return 64
     return 128
 
