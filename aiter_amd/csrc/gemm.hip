@@ -20,6 +20,7 @@
 #include "gemm_flat.h"
 #include "gemm_flat_persist.h"
 #include "gemm_t32.h"
+#include "out_quant.h"
 
 namespace aiter_amd {
 
@@ -222,6 +223,21 @@ std::vector<Instance>& registry() {
         // 16 contiguous bytes of one row per lane) ----
         tile(kA4W4, 256, 256, plain, launch_flat<kFp4, 256, false, false>, "a4w4");
         persist(kA4W4, 256, plain, launch_flat_persist<kFp4, 256, false, false>, "a4w4");
+        // ---- a4w4 with f32 output (the tile that mxfp4_gemm_asm quantises to
+        // e2m1 / MXFP8) ----
+        // (no 256x256 flat f32 tile: its epilogue spills; the persistent form does not)
+        const Variant pre32{false, true, true};
+        tile(kA4W4, 128, 256, pre32, launch_flat<kFp4, 128, true>, "a4w4");
+        tile(kA4W4, 128, 128, pre32, launch_t32<kFp4, true, 128, 128, 2, true>, "a4w4");
+        tile(kA4W4, 64, 128, pre32, launch_t32<kFp4, true, 64, 128, 1, true>, "a4w4");
+        skinny(kA4W4, 1, false, pre32, launch_skinny<kFp4, 1, true, false, true>, "a4w4");
+        skinny(kA4W4, 2, false, pre32, launch_skinny<kFp4, 2, true, false, true>, "a4w4");
+        skinny(kA4W4, 4, false, pre32, launch_skinny<kFp4, 4, true, false, true>, "a4w4");
+        skinny(kA4W4, 1, true, pre32, launch_skinny<kFp4, 1, true, true, true>, "a4w4");
+        skinny(kA4W4, 2, true, pre32, launch_skinny<kFp4, 2, true, true, true>, "a4w4");
+        skinny(kA4W4, 4, true, pre32, launch_skinny<kFp4, 4, true, true, true>, "a4w4");
+        tsplit(kA4W4, 64, 128, pre32, launch_t32<kFp4, true, 64, 128, 1, true, true>, "a4w4");
+        persist(kA4W4, 256, pre32, launch_flat_persist<kFp4, 256, true>, "a4w4");
     });
     return reg;
 }
@@ -318,22 +334,33 @@ const Instance* map_reference_name(const std::string& nm, Family f, const Varian
     return nullptr;
 }
 
+__global__ __launch_bounds__(256) void fill_byte_kernel(uint8_t* p, int64_t n, int v) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+    const int w = v * 0x01010101;
+    if (i + 16 <= n) *reinterpret_cast<i32x4_t*>(p + i) = i32x4_t{w, w, w, w};
+    else
+        for (int64_t j = i; j < n; ++j) p[j] = (uint8_t)v;
+}
+
 // ---- per-(device, stream) f32 workspace for split-K ----------------------
 struct WsKey {
     int dev;
     hipStream_t st;
-    bool operator<(const WsKey& o) const { return dev != o.dev ? dev < o.dev : st < o.st; }
+    int slot;   // 0: split-K partials, 1: low-precision-output f32 tile, 2: unit scales
+    bool operator<(const WsKey& o) const {
+        return dev != o.dev ? dev < o.dev : (st != o.st ? st < o.st : slot < o.slot);
+    }
 };
 struct WsVal {
     float* ptr = nullptr;
     size_t bytes = 0;
 };
 
-float* workspace(int dev, hipStream_t st, size_t bytes) {
+float* workspace(int dev, hipStream_t st, size_t bytes, int slot = 0) {
     static std::mutex mu;
     static std::map<WsKey, WsVal> ws;
     std::lock_guard<std::mutex> lk(mu);
-    WsVal& w = ws[{dev, st}];
+    WsVal& w = ws[{dev, st, slot}];
     if (w.bytes < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         AA_HIP(hipStreamIsCapturing(st, &cs));
@@ -590,6 +617,94 @@ int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
         GemmCall c{kA4W4, {false, bpreshuffle != 0, false}, A, B, A_scale, B_scale, out, bias,
                    alpha, beta, kernelName, -1, log2_k_split > 0 ? log2_k_split : -1};
         run_gemm(c, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+// gfx1250 f4gemm entry (aiter/ops/gemm_op_a4w4.py:290-304, dispatch :80-124):
+// the output dtype picks the form: bf16 [M, N] (gemm_a4w4), fp4x2 [M, N/2]
+// (e2m1 with conversion scale 1; the reference's packed-fp4 kernel ignores the
+// input scales, op_tests/test_f4gemm.py:213-215, and so does this one: it runs
+// with unit scales), or fp8 [M, N] + out_scale (MXFP8, per-128-column e8m0 in
+// the packed layout).  The low-precision forms run the f32-output GEMM into a
+// library-owned tile, then out_quant_kernel.
+int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA, aiter_tensor_t* ScaleB,
+                   aiter_tensor_t* out, aiter_tensor_t* out_scale, const char* kernelName, int a_preshuffle,
+                   aiter_stream_t stream) {
+    return safe_call([&] {
+        check_tensor(A, "A", 2);
+        check_tensor(B, "B", 2);
+        check_tensor(out, "out", 2);
+        DeviceGuard g(A->device_id);
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        AA_CHECK(!a_preshuffle, "mxfp4_gemm_asm: preshuffled A is a gfx1250 layout; pass a_preshuffle=0");
+        const int odt = out->dtype;
+        if (odt == AITER_DTYPE_bf16) {
+            GemmCall c{kA4W4, {false, true, false}, A, B, ScaleA, ScaleB, out, nullptr, 1.0f, 0.0f, kernelName, -1, -1};
+            run_gemm(c, st);
+            return;
+        }
+        const bool fp8 = odt == AITER_DTYPE_fp8;
+        AA_CHECK(fp8 || odt == AITER_DTYPE_fp4x2 || odt == AITER_DTYPE_u8,
+                 "mxfp4_gemm_asm: out must be bf16, fp4x2 or fp8");
+        const int64_t M = rows_2d(A), N = rows_2d(B), K = cols_2d(A) * 2;
+        AA_CHECK(rows_2d(out) == M && cols_2d(out) == (fp8 ? N : N / 2) && out->strides[out->ndim - 1] == 1,
+                 "mxfp4_gemm_asm: out must be [M, ", fp8 ? "N" : "N/2", "]");
+        const int64_t out_stride = out->ndim >= 2 ? out->strides[out->ndim - 2] : cols_2d(out);
+        AA_CHECK(N % 8 == 0 && out_stride % 4 == 0, "mxfp4_gemm_asm: N must be a multiple of 8");
+        if (fp8) {
+            AA_CHECK(out_scale, "mxfp4_gemm_asm: MXFP8 output needs out_scale");
+            AA_CHECK(N % 128 == 0 && M % 64 == 0, "mxfp4_gemm_asm: MXFP8 output needs N % 128 == 0 and M % 64 == 0");
+            AA_CHECK(is_byte_type(out_scale->dtype) && (int64_t)out_scale->numel >= M * (N / 128),
+                     "mxfp4_gemm_asm: out_scale must hold M * N / 128 e8m0 bytes");
+        }
+        // f32 tile
+        float* tile = workspace(A->device_id, st, (size_t)M * N * sizeof(float), 1);
+        aiter_tensor_t t{};
+        t.ptr = tile;
+        t.numel = (size_t)(M * N);
+        t.ndim = 2;
+        t.shape[0] = M;
+        t.shape[1] = N;
+        t.strides[0] = N;
+        t.strides[1] = 1;
+        t.dtype = AITER_DTYPE_fp32;
+        t.device_id = A->device_id;
+        aiter_tensor_t usa{}, usb{};
+        const aiter_tensor_t *sa = ScaleA, *sb = ScaleB;
+        if (!fp8) {
+            // unit scales (byte 127): shuffled or not, every byte is 127
+            const int64_t sn = (K / 32 + 7) / 8 * 8;
+            const int64_t rows = (std::max(M, N) + 255) / 256 * 256;
+            uint8_t* ones = reinterpret_cast<uint8_t*>(workspace(A->device_id, st, (size_t)(rows * sn), 2));
+            fill_byte_kernel<<<(unsigned)((rows * sn / 16 + 255) / 256 + 1), 256, 0, st>>>(ones, rows * sn, 127);
+            AA_HIP(hipGetLastError());
+            for (aiter_tensor_t* u : {&usa, &usb}) {
+                u->ptr = ones;
+                u->ndim = 2;
+                u->dtype = AITER_DTYPE_u8;
+                u->device_id = A->device_id;
+                u->strides[1] = 1;
+                u->strides[0] = sn;
+                u->shape[1] = sn;
+            }
+            usa.shape[0] = (M + 255) / 256 * 256;
+            usb.shape[0] = (N + 255) / 256 * 256;
+            usa.numel = usa.shape[0] * sn;
+            usb.numel = usb.shape[0] * sn;
+            sa = &usa;
+            sb = &usb;
+        }
+        GemmCall c{kA4W4, {false, true, true}, A, B, sa, sb, &t, nullptr, 1.0f, 0.0f, kernelName, -1, -1};
+        run_gemm(c, st);
+        const int64_t n = M * (N / 8);
+        const dim3 grid((unsigned)((n + 255) / 256));
+        if (fp8)
+            out_quant_kernel<true><<<grid, 256, 0, st>>>(tile, M, N, N, static_cast<uint8_t*>(out->ptr), out_stride,
+                                                          static_cast<uint8_t*>(out_scale->ptr));
+        else
+            out_quant_kernel<false><<<grid, 256, 0, st>>>(tile, M, N, N, static_cast<uint8_t*>(out->ptr), out_stride,
+                                                           nullptr);
+        AA_HIP(hipGetLastError());
     });
 }
 

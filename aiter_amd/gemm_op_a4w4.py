@@ -126,3 +126,95 @@ def gemm_a4w4_blockscale_tune(XQ: Tensor, WQ: Tensor, x_scale: Tensor, w_scale: 
     (csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale_tune.cu:58-90)."""
     call("gemm_a4w4_blockscale", XQ, WQ, x_scale, w_scale, Out, int(splitK), int(kernelId))
     return Out
+
+
+# ---------------------------------------------------------------- low-precision outputs
+# (aiter/ops/gemm_op_a4w4.py:290-409,457-567: gfx1250-only in the reference;
+# here on gfx950 as the f32-output GEMM followed by one output-quant kernel)
+MXFP8_OUT_SCALE_BLOCK = 128
+
+
+def _is_mxfp8_out(dtype: torch.dtype) -> bool:
+    return dtype == dtypes.fp8
+
+
+def _alloc_f4gemm_out(M: int, N: int, dtype: torch.dtype, device) -> Tensor:
+    """fp4x2 [M, N/2] (packed e2m1), fp8 [M, N] or bf16 [M, N]."""
+    if dtype == dtypes.fp4x2:
+        assert N % 2 == 0, "packed fp4 output requires even N"
+        return torch.empty((M, N // 2), dtype=dtypes.fp4x2, device=device)
+    return torch.empty((M, N), dtype=dtype, device=device)
+
+
+def _alloc_f4gemm_out_scale(M: int, N: int, dtype: torch.dtype, device) -> Tensor | None:
+    """MXFP8 output scale: M * N/128 e8m0 bytes in the packed (M/64, N/128, 16, 4) layout."""
+    if not _is_mxfp8_out(dtype):
+        return None
+    assert N % MXFP8_OUT_SCALE_BLOCK == 0, f"mxfp8 output requires N % {MXFP8_OUT_SCALE_BLOCK} == 0, got N={N}"
+    assert M % 64 == 0, f"mxfp8 output-scale packing requires M % 64 == 0, got M={M}"
+    return torch.empty((M, N // MXFP8_OUT_SCALE_BLOCK), dtype=dtypes.fp8_e8m0, device=device)
+
+
+def unpack_mxfp8_out_scale(packed: Tensor, M: int, N: int) -> Tensor:
+    """Packed (M/64, N/128, 16, 4) -> row-major [M, N/128] (aiter/ops/gemm_op_a4w4.py:365-380)."""
+    assert M % 64 == 0 and N % MXFP8_OUT_SCALE_BLOCK == 0
+    scale_n = N // MXFP8_OUT_SCALE_BLOCK
+    u8 = packed.reshape(-1).view(torch.uint8)[: (M // 64) * scale_n * 16 * 4]
+    rm = u8.reshape(M // 64, scale_n, 16, 4).permute(0, 3, 2, 1).reshape(M, scale_n)
+    return rm.contiguous().view(dtypes.fp8_e8m0)
+
+
+def _mxfp4_gemm_asm(A: Tensor, B: Tensor, ScaleA: Tensor, ScaleB: Tensor, out: Tensor,
+                    out_scale: Tensor | None = None, kernelName: str | None = None, a_preshuffle: int = 1) -> None:
+    """C entry mxfp4_gemm_asm (aiter/ops/gemm_op_a4w4.py:290-304)."""
+    o = out if out.dtype in (dtypes.bf16, dtypes.fp8) else out.view(torch.uint8)
+    call("mxfp4_gemm_asm", A.view(torch.uint8), B.view(torch.uint8), ScaleA.view(torch.uint8),
+         ScaleB.view(torch.uint8), o, None if out_scale is None else out_scale.view(torch.uint8),
+         kernelName or None, int(a_preshuffle))
+
+
+def gemm_mxfp4_asm(A: Tensor, B: Tensor, ScaleA: Tensor, ScaleB: Tensor, dtype: torch.dtype = dtypes.bf16,
+                   a_preshuffle: bool = True, kernelName: str = ""):
+    """MXFP4 GEMM with bf16 ``[M, N]``, packed-fp4 ``[M, N/2]`` (e2m1, conversion
+    scale 1, input scales ignored as by the reference's packed-fp4 kernel) or
+    MXFP8 ``(fp8 [M, N], packed e8m0)`` output.  A is row-major on gfx950
+    (``a_preshuffle=True``, the reference's gfx1250 default, raises)."""
+    M, N = A.shape[0], B.shape[0]
+    out = _alloc_f4gemm_out(M, N, dtype, A.device)
+    out_scale = _alloc_f4gemm_out_scale(M, N, dtype, A.device)
+    _mxfp4_gemm_asm(A, B, ScaleA, ScaleB, out, out_scale, kernelName or None, int(bool(a_preshuffle)))
+    return (out, out_scale) if out_scale is not None else out
+
+
+def _lowp_dispatch(A, B, A_scale, B_scale, dtype, bias, alpha, beta, apreshuffle, global_A_scale, global_B_scale):
+    if bias is not None or (alpha is not None and alpha != 1.0) or (beta is not None and beta != 0.0):
+        logger.warning("gemm_a4w4o4/o8 ignore bias/alpha/beta (as the reference's F4GEMM kernels do)")
+    if global_A_scale is not None or global_B_scale is not None:
+        raise NotImplementedError("NVFP4 (per-tensor global scales) is not part of this library")
+    m = A.numel() // A.shape[-1]
+    return gemm_mxfp4_asm(A.view(m, A.shape[-1]), B, A_scale, B_scale, dtype=dtype,
+                          a_preshuffle=bool(apreshuffle))
+
+
+def gemm_a4w4o4(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, bias: Tensor | None = None,
+                alpha: float | None = 1.0, beta: float | None = 0.0, bpreshuffle: bool | None = True,
+                apreshuffle: bool | None = False, global_A_scale: Tensor | None = None,
+                global_B_scale: Tensor | None = None) -> Tensor:
+    """A4W4 GEMM with packed FP4 (e2m1, conversion scale 1) output ``[*lead, N//2]``
+    (aiter/ops/gemm_op_a4w4.py:477-501)."""
+    out = _lowp_dispatch(A, B, A_scale, B_scale, dtypes.fp4x2, bias, alpha, beta, apreshuffle, global_A_scale,
+                         global_B_scale)
+    return out.view(*A.shape[:-1], out.shape[-1])
+
+
+def gemm_a4w4o8(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, bias: Tensor | None = None,
+                alpha: float | None = 1.0, beta: float | None = 0.0, bpreshuffle: bool | None = True,
+                apreshuffle: bool | None = False, global_A_scale: Tensor | None = None,
+                global_B_scale: Tensor | None = None) -> tuple[Tensor, Tensor]:
+    """A4W4 GEMM with MXFP8 output: ``(fp8 e4m3 [*lead, N], e8m0 scale)``, the
+    scale in the packed (M/64, N/128, 16, 4) layout (``unpack_mxfp8_out_scale``)
+    (aiter/ops/gemm_op_a4w4.py:533-567)."""
+    o, s = _lowp_dispatch(A, B, A_scale, B_scale, dtypes.fp8, bias, alpha, beta, apreshuffle, global_A_scale,
+                          global_B_scale)
+    lead = A.shape[:-1]
+    return o.view(*lead, o.shape[-1]), s.view(*lead, s.shape[-1])

@@ -220,6 +220,14 @@ def bench_extra(dev):
                                               "GBps": round(8192 * 8192 * (2 + 0.5 + 1 / 32) / tf / 1e9, 1),
                                               "unfused_us": round(tu * 1e6, 1)}
     del xa
+    # low-precision outputs of the 8192^3 A4W4 GEMM (e2m1 / MXFP8), against the bf16-output call
+    aq, as_, bq, bs_ = quantised_operands(8192, 8192, 8192, 4, dev)
+    t16 = time_graph(lambda: aiter_amd.gemm_a4w4(aq, bq, as_, bs_), 10, 2)
+    for tag, fn in (("a4w4o4_8192x8192x8192", aiter_amd.gemm_a4w4o4), ("a4w4o8_8192x8192x8192", aiter_amd.gemm_a4w4o8)):
+        t = time_graph(lambda fn=fn: fn(aq, bq, as_, bs_), 10, 2)
+        out[tag] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * 8192 ** 3 / t / 1e12, 1),
+                    "bf16_out_us": round(t16 * 1e6, 1)}
+    del aq, as_, bq, bs_
     out["fused_moe_a4w4_deepseek"] = bench_moe(dev)
     return out
 

@@ -156,6 +156,18 @@ int fused_rms_mx_quant(aiter_tensor_t* x1, aiter_tensor_t* x1_weight, float eps1
                        aiter_tensor_t* out_scale, aiter_tensor_t* out1, aiter_tensor_t* out2,
                        aiter_tensor_t* out_res1, int shuffle, int pad_scale, aiter_stream_t stream);
 
+/* Low-precision outputs: replaces mxfp4_gemm_asm (aiter/ops/gemm_op_a4w4.py:290-304;
+ * gfx1250-only in the reference, whose gemm_a4w4o4 / gemm_a4w4o8 call it).
+ * out bf16 [M, N]: as gemm_a4w4_asm without bias; fp4x2 [M, N/2]: e2m1 of the
+ * product with conversion scale 1, input scales ignored (the reference's
+ * packed-fp4 kernel is scale-free, op_tests/test_f4gemm.py:213-215); fp8
+ * [M, N] + out_scale (M * N/128 e8m0 bytes, packed (M/64, N/128, 16, 4)):
+ * per-128-column RoundUp e8m0 and e4m3 data, M % 64 == 0, N % 128 == 0.
+ * a_preshuffle must be 0 (row-major A on gfx950). */
+int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA, aiter_tensor_t* ScaleB,
+                   aiter_tensor_t* out, aiter_tensor_t* out_scale, const char* kernelName, int a_preshuffle,
+                   aiter_stream_t stream);
+
 /* ---- fused MoE (MXFP4 weights, per-1x32 e8m0 scales) ---------------------
  * Routing sort: replaces moe_sorting_fwd (aiter/ops/moe_sorting.py:12-27,
  * called from aiter/fused_moe.py:171-285).  topk_ids int32 [M, topk],

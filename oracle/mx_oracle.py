@@ -527,6 +527,60 @@ def fused_rms_mx_quant_ref(x, w, eps, fp8: bool, res=None):
 
 
 # How each function above is pinned (checked by tests/test_oracle.py).
+# --------------------------------------------------------------------------
+# Low-precision GEMM outputs (gemm_a4w4o4 / gemm_a4w4o8)
+# --------------------------------------------------------------------------
+
+MXFP8_OUT_BLOCK = 128
+
+
+def gemm_a4w4o4_ref(a_packed, b_packed) -> np.ndarray:
+    """Packed e2m1 output with conversion scale 1 and the input scales ignored
+    (the reference's packed-fp4 kernel is scale-free: run_torch_mxfp4(noscale=True)
+    then fp4_utils.f32_to_mxfp4, op_tests/test_f4gemm.py:108-116,224-225)."""
+    c = mxfp4_to_f32(a_packed).astype(np.float64) @ mxfp4_to_f32(b_packed).astype(np.float64).T
+    return pack_fp4(e2m1_encode_rne(c.astype(np.float32)))
+
+
+def quant_mxfp8_block_n(x: np.ndarray, block: int = MXFP8_OUT_BLOCK):
+    """``_quant_mxfp8_blockN`` of op_tests/test_f4gemm.py:70-83: per row and
+    128-column block, amax (at least the smallest normal f32) -> RoundUp e8m0
+    for e4m3 (ceil_pow2(amax / 448)), data = e4m3(x / scale).  Returns
+    (q [M, N] u8, scale [M, N/128] u8 row-major)."""
+    x = np.asarray(x, dtype=np.float32)
+    m, n = x.shape
+    xb = x.reshape(m, n // block, block)
+    amax = np.maximum(np.abs(xb).max(axis=-1), np.float32(np.finfo(np.float32).tiny))
+    byte = e8m0_scale_hip(amax, ROUND_UP, "fp8")
+    q = _scaled_by_inverse(xb, byte)
+    return e4m3_encode_rne(q.reshape(m, n)), byte
+
+
+def pack_mxfp8_out_scale(scale_rm: np.ndarray) -> np.ndarray:
+    """Row-major [M, N/128] -> the packed (M/64, N/128, 16, 4) byte layout,
+    the inverse of unpack_mxfp8_out_scale (aiter/ops/gemm_op_a4w4.py:365-380):
+    unpack views (M/64, N/128, 16, 4) and permutes (0, 3, 2, 1)."""
+    s = np.asarray(scale_rm, dtype=np.uint8)
+    m, nb = s.shape
+    return np.ascontiguousarray(s.reshape(m // 64, 4, 16, nb).transpose(0, 3, 2, 1)).reshape(-1)
+
+
+def unpack_mxfp8_out_scale(packed: np.ndarray, m: int, n: int) -> np.ndarray:
+    """aiter/ops/gemm_op_a4w4.py:365-380."""
+    nb = n // MXFP8_OUT_BLOCK
+    u8 = np.asarray(packed, dtype=np.uint8).reshape(-1)[: (m // 64) * nb * 64]
+    return np.ascontiguousarray(u8.reshape(m // 64, nb, 16, 4).transpose(0, 3, 2, 1)).reshape(m, nb)
+
+
+def gemm_a4w4o8_ref(a_packed, b_packed, a_scale, b_scale):
+    """MXFP8 output: f32 product of the dequantised operands
+    (run_torch_mxfp4, op_tests/test_f4gemm.py:108-119), then quant_mxfp8_block_n.
+    Returns (q [M, N] u8, scale row-major [M, N/128] u8)."""
+    a = dequant_mxfp4(a_packed, a_scale)
+    b = dequant_mxfp4(b_packed, b_scale)
+    return quant_mxfp8_block_n((a.astype(np.float64) @ b.astype(np.float64).T).astype(np.float32))
+
+
 PINNED = {
     "e2m1_decode": "OCP closed form 2**(e-1)*(1+m/2) + FP4 grid known answer",
     "e2m1_encode_rne": "brute-force nearest-grid search (ties to even code) and the "
@@ -547,4 +601,10 @@ PINNED = {
                     "(constant-magnitude power-of-two rows, eps 0: the factor is an exact power of two)",
     "fused_rms_mx_quant_ref": "composition of rms_norm_f32 and the pinned Even quants; exact case "
                               "bit-equal to quantising +-weight directly",
+    "gemm_a4w4o4_ref": "integer brute force: fp4 codes times 4 are integers, so the product is exact and "
+                       "its e2m1 code follows from the pinned encoder; float64 product",
+    "quant_mxfp8_block_n": "composition of the pinned e8m0_scale_hip(RoundUp, fp8) and e4m3_encode_rne; "
+                           "|q| <= 448 and dequant error <= half an e4m3 step per element",
+    "pack/unpack_mxfp8_out_scale": "hand-worked known answer of the packed index and mutual inverses",
+    "gemm_a4w4o8_ref": "composition of gemm_a4w4_ref's f32 product and quant_mxfp8_block_n",
 }

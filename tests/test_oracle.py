@@ -335,3 +335,45 @@ def test_fused_rms_quant_exact_case():
         q2, s2 = O.quant_mxfp8(signs * w, O.EVEN) if fp8 else O.quant_mxfp4_triton_even(signs * w)
         np.testing.assert_array_equal(q, q2)
         np.testing.assert_array_equal(s, s2)
+
+
+# ---------------------------------------------------------------- low-precision outputs
+def test_pack_mxfp8_out_scale_known_answer():
+    m, n = 128, 256
+    rm = np.arange(m * (n // 128), dtype=np.int64).reshape(m, n // 128).astype(np.uint8)
+    packed = O.pack_mxfp8_out_scale(rm)
+    # byte (row r, block b) at ((r/64 * N/128 + b) * 16 + r%16) * 4 + (r%64)/16
+    for r in (0, 1, 15, 16, 17, 63, 64, 100, 127):
+        for b in (0, 1):
+            assert packed[((r // 64 * 2 + b) * 16 + r % 16) * 4 + (r % 64) // 16] == rm[r, b]
+    np.testing.assert_array_equal(O.unpack_mxfp8_out_scale(packed, m, n), rm)
+
+
+def test_quant_mxfp8_block_n_properties():
+    rng = np.random.default_rng(31)
+    x = (rng.standard_normal((64, 384)) * np.exp2(rng.integers(-6, 7, (64, 1)))).astype(np.float32)
+    q, s = O.quant_mxfp8_block_n(x)
+    v = O.e4m3_decode(q).reshape(64, 3, 128)
+    scale = np.exp2(s.astype(np.float64) - 127)[..., None]
+    assert np.abs(v).max() <= 448
+    xb = x.reshape(64, 3, 128) / scale
+    # RNE: each value within half an e4m3 step (3 mantissa bits) of the scaled input
+    step = np.exp2(np.floor(np.log2(np.maximum(np.abs(xb), 2.0 ** -6))) - 3)
+    assert np.all(np.abs(v - xb) <= step / 2 + 1e-12)
+    # RoundUp: the block amax fits, one power of two less would not
+    amax = np.abs(x.reshape(64, 3, 128)).max(-1)
+    assert np.all(amax / scale[..., 0] <= 448) and np.all(amax / (scale[..., 0] / 2) > 448)
+
+
+def test_gemm_a4w4o4_ref_integer_brute_force():
+    rng = np.random.default_rng(32)
+    a = rng.integers(0, 256, (5, 16), dtype=np.uint8)
+    b = rng.integers(0, 256, (8, 16), dtype=np.uint8)
+    got = O.unpack_fp4(O.gemm_a4w4o4_ref(a, b))
+    ai = (O.mxfp4_to_f32(a) * 2).astype(np.int64)      # codes * 2 are integers
+    bi = (O.mxfp4_to_f32(b) * 2).astype(np.int64)
+    exact = (ai @ bi.T) / 4.0
+    np.testing.assert_array_equal(got, O.e2m1_encode_rne(exact.astype(np.float32)))
+    # saturation: |c| > 6 maps to code 7 / 15
+    big = np.abs(exact) > 6
+    assert np.all((got[big] & 7) == 7)
