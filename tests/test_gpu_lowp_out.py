@@ -98,3 +98,20 @@ def test_bf16_form_matches_gemm_a4w4(cuda):
     o2 = aiter_amd.gemm_a4w4(*args)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2[:m])
+
+
+@pytest.mark.parametrize("kname", ["a4w4_tile_128x256_f32", "a4w4_tile_256x256_f32_persist",
+                                   "a4w4_tile_128x128_f32", "a4w4_tile_64x128_f32", "a4w4_tile_64x128_splitk_f32"])
+def test_f32_tile_kernels_by_name(cuda, kname):
+    """Each f32-output A4W4 kernel behind the low-precision forms, picked by name."""
+    import aiter_amd
+    from aiter_amd.gemm_op_a4w4 import _alloc_f4gemm_out, _mxfp4_gemm_asm
+
+    m, n, k = 320, 768, 1024
+    announce(f"mxfp4_gemm_asm fp4 out via {kname} {m}x{n}x{k}")
+    aq, bq, a_s, b_s = _operands(m, n, k, 13)
+    out = _alloc_f4gemm_out(m, n, aiter_amd.dtypes.fp4x2, cuda)
+    _mxfp4_gemm_asm(_dev(aq, cuda), _dev(O.shuffle_weight(bq), cuda), _dev(O.shuffle_scale(a_s), cuda),
+                    _dev(O.shuffle_scale(b_s), cuda), out, None, kname, 0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.view(torch.uint8).cpu().numpy(), O.gemm_a4w4o4_ref(aq, bq))

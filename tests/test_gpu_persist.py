@@ -22,7 +22,8 @@ def _persist_rows():
     try:
         from aiter_amd._lib import kernel_table
 
-        return [r for r in kernel_table() if r[1].endswith("_persist")]
+        # bf16-output forms (the f32-output one is tested by name in test_gpu_lowp_out.py)
+        return [r for r in kernel_table() if r[1].endswith("_persist") and not r[9]]
     except Exception:  # library not built: collected, then skipped by the cuda fixture
         return []
 

@@ -29,7 +29,7 @@ def _dev(x, cuda):
     return torch.from_numpy(np.ascontiguousarray(x)).to(cuda)
 
 
-A4W4_ROWS = _rows("a4w4")
+A4W4_ROWS = _rows("a4w4", out_f32=False)   # the f32 form feeds gemm_a4w4o4 / o8 (test_gpu_lowp_out.py)
 
 
 @pytest.mark.parametrize("row", A4W4_ROWS, ids=[r[1] for r in A4W4_ROWS])
@@ -55,7 +55,7 @@ def test_a4w4_split_tiles(cuda, row, log2_split):
     assert ok, f"{name}: {msg}"
 
 
-A8W4_ROWS = _rows("a8w4")
+A8W4_ROWS = _rows("a8w4", out_f32=False)
 
 
 @pytest.mark.parametrize("row", A8W4_ROWS, ids=[r[1] for r in A8W4_ROWS])
