@@ -16,6 +16,7 @@ from .gemm_common import get_padded_m
 from .gemm_op_a4w4 import (MXFP8_OUT_SCALE_BLOCK, gemm_a4w4o4, gemm_a4w4o8, gemm_mxfp4_asm, unpack_mxfp8_out_scale,
                            compute_gemm_SplitK, gemm_a4w4, gemm_a4w4_asm, gemm_a4w4_blockscale,
                            gemm_a4w4_blockscale_tune, get_GEMM_config)
+from .batched_gemm_op_bf16 import batched_gemm_bf16, batched_gemm_bf16_CK, batched_gemm_bf16_tune
 from .fused_quant import fused_rms_mxfp4_quant, fused_rms_mxfp8_quant
 from .fused_moe import (ActivationType, ck_moe_stage1, ck_moe_stage2, fused_dynamic_mx_quant_moe_sort,
                         fused_dynamic_mxfp4_quant_moe_sort, fused_dynamic_mxfp8_quant_moe_sort, fused_moe,

@@ -112,6 +112,8 @@ SIGNATURES = {
                       + [ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
     "moe_sum": ([_T, _T, _S], ctypes.c_int),
     "mxfp4_gemm_asm": ([_T] * 6 + [ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
+    "batched_gemm_bf16": ([_T] * 4 + [ctypes.c_int, _S], ctypes.c_int),
+    "batched_gemm_bf16_tune": ([_T] * 3 + [ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
     "aiter_amd_num_kernels": ([], ctypes.c_int),
     "aiter_amd_kernel_info": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
     "gemm_workspace_reserve": ([ctypes.c_int, _S, ctypes.c_size_t], ctypes.c_int),

@@ -384,6 +384,10 @@ struct GemmCall {
     const char* kernel_name;
     int kernel_id;    // < 0: use name / heuristic
     int log2_split;   // < 0: heuristic
+    // batch > 1: one launch with gridDim.z = batch; A, B, out describe batch 0
+    // and the strides (bytes; bias in elements) step to the next batch
+    int batch = 1;
+    int64_t bs_a = 0, bs_b = 0, bs_d = 0, bs_bias = 0;
 };
 
 void run_gemm(const GemmCall& c, hipStream_t stream) {
@@ -473,6 +477,12 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     const int cus = device_cu_count(dev);
 
     const Instance* inst = nullptr;
+    p.bs_a = c.bs_a;
+    p.bs_b = c.bs_b;
+    p.bs_d = c.bs_d;
+    p.bs_bias = c.bs_bias;
+    AA_CHECK(c.batch >= 1 && c.batch < 65536, "batch must be in [1, 65535]");
+    const bool batched = c.batch > 1;   // one-pass, one-tile-per-workgroup kernels only
     int splits = 1;
     if (c.kernel_id >= 0) {
         inst = find_by_id(c.kernel_id);
@@ -501,6 +511,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             // split-K tile: stages of K over gridDim.y, f32 slices, then a sum
             const int nst = (int)(K / (scaled ? 256 : 64));
             int sp = c.log2_split >= 0 ? (1 << c.log2_split) : tile_splits(tiles, nst, cus);
+            if (batched) sp = 1;
             sp = std::max(1, std::min(sp, nst));
             p.k_steps_per_split = (nst + sp - 1) / sp;
             sp = (nst + p.k_steps_per_split - 1) / p.k_steps_per_split;
@@ -525,7 +536,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             AA_CHECK(twin, "no non-split twin of ", inst->name);
             inst = twin;
         }
-        if (inst->persistent && p.bias) {
+        if (inst->persistent && (p.bias || batched)) {
             // the persistent epilogue has no bias term: its one-tile-per-workgroup twin
             const Instance* twin = nullptr;
             for (auto& in : registry())
@@ -535,11 +546,11 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             AA_CHECK(twin, "no non-persistent twin of ", inst->name);
             inst = twin;
         }
-        inst->fn(p, dim3(inst->persistent ? std::min(tiles, cus) : tiles), stream);
+        inst->fn(p, dim3(inst->persistent ? std::min(tiles, cus) : tiles, 1, c.batch), stream);
     } else {
         // the skinny kernels split K in k-pairs (one scale dword each)
         const int kpairs = ksteps / 2;
-        splits = std::max(1, std::min(splits, kpairs));
+        splits = batched ? 1 : std::max(1, std::min(splits, kpairs));
         p.k_steps_per_split = (kpairs + splits - 1) / splits;
         splits = (kpairs + p.k_steps_per_split - 1) / p.k_steps_per_split;
         const dim3 grid((unsigned)((N + 15) / 16), (unsigned)splits);
@@ -560,10 +571,10 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
                 if (in.skinny && !in.split && variant_ok(in, c.fam, c.var) && in.bm == inst->bm) twin = &in;
             AA_CHECK(twin, "no non-split twin for ", inst->name);
             p.k_steps_per_split = kpairs;
-            twin->fn(p, dim3(grid.x, 1), stream);
+            twin->fn(p, dim3(grid.x, 1, c.batch), stream);
         } else {
             p.k_steps_per_split = kpairs;
-            inst->fn(p, dim3(grid.x, 1), stream);
+            inst->fn(p, dim3(grid.x, 1, c.batch), stream);
         }
     }
     AA_HIP(hipGetLastError());
@@ -754,49 +765,57 @@ int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
     });
 }
 
+// [b, M, K] x [b, N, K] -> [b, M, N] (+ bias [N] or [b, N]) as one launch
+// with gridDim.z = b: the 2-D descriptors of batch 0 plus batch strides (any
+// strides with unit last-dimension stride, e.g. the reference test's [m, b, k]
+// transposed layout)
 static void opus_batched(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias,
                          int kernelId, int splitK, hipStream_t st) {
     check_tensor(XQ, "XQ", 2);
     check_tensor(WQ, "WQ", 2);
     check_tensor(Y, "Y", 2);
-    // [b, M, K] / [b, N, K] / [b, M, N]; a 2-D call is batch 1
     const int nd = XQ->ndim;
     const int64_t batch = nd == 3 ? XQ->shape[0] : 1;
     AA_CHECK(WQ->ndim == nd && Y->ndim == nd, "XQ, WQ, Y must have the same rank");
     AA_CHECK(nd == 2 || nd == 3, "opus a16w16 expects 2-D or 3-D tensors");
     if (nd == 3) AA_CHECK(WQ->shape[0] == batch && Y->shape[0] == batch, "batch mismatch");
-    for (int64_t b = 0; b < batch; ++b) {
-        aiter_tensor_t a = *XQ, w = *WQ, y = *Y, bb{};
-        auto slice = [&](aiter_tensor_t& t, const aiter_tensor_t* src, size_t esz) {
-            if (nd == 3) {
-                t.ptr = static_cast<uint8_t*>(src->ptr) + b * src->strides[0] * esz;
-                t.ndim = 2;
-                t.shape[0] = src->shape[1];
-                t.shape[1] = src->shape[2];
-                t.strides[0] = src->strides[1];
-                t.strides[1] = src->strides[2];
-                t.numel = src->shape[1] * src->shape[2];
-            }
-        };
-        slice(a, XQ, 2);
-        slice(w, WQ, 2);
-        slice(y, Y, dtype_size(Y->dtype));
-        aiter_tensor_t* bptr = nullptr;
-        if (bias) {
-            bb = *bias;
-            if (bias->ndim == 2 && bias->shape[0] == batch && batch > 1) {
-                bb.ptr = static_cast<uint8_t*>(bias->ptr) + b * bias->strides[0] * 4;
-                bb.ndim = 1;
-                bb.shape[0] = bias->shape[1];
-                bb.strides[0] = bias->strides[1];
-                bb.numel = bias->shape[1];
-            }
-            bptr = &bb;
+    aiter_tensor_t a = *XQ, w = *WQ, y = *Y, bb{};
+    auto slice0 = [&](aiter_tensor_t& t, const aiter_tensor_t* src) {
+        if (nd == 3) {
+            t.ndim = 2;
+            t.shape[0] = src->shape[1];
+            t.shape[1] = src->shape[2];
+            t.strides[0] = src->strides[1];
+            t.strides[1] = src->strides[2];
+            t.numel = src->shape[1] * src->shape[2];
         }
-        GemmCall c{kA16W16, {false, false, Y->dtype == AITER_DTYPE_fp32}, &a, &w, nullptr, nullptr, &y, bptr,
-                   1.0f, 1.0f, nullptr, kernelId, splitK > 0 ? splitK : -1};
-        run_gemm(c, st);
+    };
+    slice0(a, XQ);
+    slice0(w, WQ);
+    slice0(y, Y);
+    aiter_tensor_t* bptr = nullptr;
+    int64_t bs_bias = 0;
+    if (bias) {
+        bb = *bias;
+        if (bias->ndim == 2 && bias->shape[0] == batch && batch > 1) {
+            bb.ndim = 1;
+            bb.shape[0] = bias->shape[1];
+            bb.strides[0] = bias->strides[1];
+            bb.numel = bias->shape[1];
+            bs_bias = bias->strides[0];
+        }
+        bptr = &bb;
     }
+    GemmCall c{kA16W16, {false, false, Y->dtype == AITER_DTYPE_fp32}, &a, &w, nullptr, nullptr, &y, bptr,
+               1.0f, 1.0f, nullptr, kernelId, splitK > 0 ? splitK : -1};
+    if (batch > 1) {
+        c.batch = (int)batch;
+        c.bs_a = XQ->strides[0] * 2;
+        c.bs_b = WQ->strides[0] * 2;
+        c.bs_d = Y->strides[0] * (int64_t)dtype_size(Y->dtype);
+        c.bs_bias = bs_bias;
+    }
+    run_gemm(c, st);
 }
 
 int opus_gemm(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias,
@@ -812,6 +831,28 @@ int opus_gemm_a16w16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t
     return safe_call([&] {
         DeviceGuard g(XQ ? XQ->device_id : -1);
         opus_batched(XQ, WQ, Y, bias, kernelId, splitK, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+// CK batched bf16 API (aiter/ops/batched_gemm_op_bf16.py:28-36,127-134):
+// XQ [B, M, K], WQ [B, N, K], Y [B, M, N] (bf16 or fp32), bias [N] or [B, N];
+// one batched launch.  splitK is the log2 split request of the reference
+// (ignored when the batch already fills the GPU: batched launches are one-pass).
+int batched_gemm_bf16(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias, int splitK,
+                      aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(XQ ? XQ->device_id : -1);
+        AA_CHECK(XQ && XQ->ndim == 3, "batched_gemm_bf16: XQ must be [B, M, K]");
+        opus_batched(XQ, WQ, Y, bias, -1, splitK, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int batched_gemm_bf16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, int kernelId, int splitK,
+                           aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(XQ ? XQ->device_id : -1);
+        AA_CHECK(XQ && XQ->ndim == 3, "batched_gemm_bf16_tune: XQ must be [B, M, K]");
+        opus_batched(XQ, WQ, Y, nullptr, kernelId, splitK, reinterpret_cast<hipStream_t>(stream));
     });
 }
 

@@ -145,6 +145,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         b_base += (int64_t)e * mq.b_expert_bytes;
         bs_base += (int64_t)e * mq.bs_expert_bytes;
     } else {
+        apply_batch(p);
         tile_coords(blockIdx.x, gridDim.x, p.tiles_m, p.tiles_n, tm, tn);
     }
     // stage 1: 128 output columns per tile (128 gate + 128 up rows of B)

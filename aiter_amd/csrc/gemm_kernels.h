@@ -61,7 +61,20 @@ struct GemmParams {
     int tiles_m, tiles_n;
     int k_steps_per_split;         // split-K: k-pairs (skinny) or stages (tiles) per split
     float alpha, beta;
+    // batched launches (gridDim.z = batch): per-batch offsets of A, B, D in
+    // bytes and of the bias in elements (0: shared by every batch)
+    int64_t bs_a, bs_b, bs_d, bs_bias;
 };
+
+// moves the operand pointers to batch blockIdx.z (no-op for unbatched grids)
+AA_DEV void apply_batch(GemmParams& p) {
+    const int64_t z = blockIdx.z;
+    if (z == 0) return;
+    p.A += z * p.bs_a;
+    p.B += z * p.bs_b;
+    p.D = static_cast<uint8_t*>(p.D) + z * p.bs_d;
+    if (p.bias) p.bias += z * p.bs_bias;
+}
 
 // ---------------------------------------------------------------------------
 // MFMA wrappers.  op_sel bytes must be immediates: the switch folds away once
@@ -161,6 +174,7 @@ AA_DEV void store_frag(const GemmParams& p, f32x4_t acc, int m, int n) {
 // ---------------------------------------------------------------------------
 template <int KA, int KB, int BM, int BN, bool A_PRE, bool B_PRE, bool OUT_F32>
 __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemmParams p) {
+    apply_batch(p);
     constexpr int FA = OpTraits<KA>::frags_per_step;
     constexpr int FB = OpTraits<KB>::frags_per_step;
     constexpr bool SCALED = OpTraits<KA>::scaled;
@@ -406,6 +420,7 @@ AA_DEV void skinny_mma(const SkinnyPair<KA, MF>& d, f32x4_t* acc, int bhalf) {
 
 template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32>
 __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
+    apply_batch(p);
     constexpr bool SCALED = OpTraits<KA>::scaled;
     constexpr int KPAIR = SCALED ? 256 : 64;               // elements per k-pair
     constexpr int SGRP = (MF + 1) / 2;                     // 32-row A scale groups

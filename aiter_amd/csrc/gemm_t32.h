@@ -47,6 +47,7 @@ struct T32Cfg {
 // second kernel sums the slices (fixed order, so results are deterministic).
 template <int KA, bool BPRE, int BM, int BN, int WAVES_M, bool OUT_F32, bool SPLIT = false>
 __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
+    apply_batch(p);
     using Cfg = T32Cfg<KA, BPRE, BM, BN>;
     constexpr bool MX = Cfg::MX;
     constexpr int NS = Cfg::NS;

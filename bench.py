@@ -228,6 +228,20 @@ def bench_extra(dev):
         out[tag] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * 8192 ** 3 / t / 1e12, 1),
                     "bf16_out_us": round(t16 * 1e6, 1)}
     del aq, as_, bq, bs_
+    # batched bf16 (op_tests/test_batched_gemm_bf16.py defaults: b = 16, N = 1024, K = 4096):
+    # one batched launch against a loop of per-batch calls
+    bt = []
+    for mb in (1, 32, 512):
+        xb = torch.randn((16, mb, 4096), generator=g).to(torch.bfloat16).to(dev)
+        wb = torch.randn((16, 1024, 4096), generator=g).to(torch.bfloat16).to(dev)
+        yb = torch.empty((16, mb, 1024), dtype=torch.bfloat16, device=dev)
+        t = time_graph(lambda: aiter_amd.batched_gemm_bf16(xb, wb, yb), 10, 2)
+        tl = time_graph(lambda: [aiter_amd.gemm_a16w16(xb[i], wb[i]) for i in range(16)], 10, 2)
+        flop = 2 * 16 * mb * 1024 * 4096
+        bt.append({"b": 16, "M": mb, "N": 1024, "K": 4096, "us": round(t * 1e6, 1),
+                   "TFLOPs": round(flop / t / 1e12, 1), "GBps": round(2 * 16 * (mb * 4096 + 1024 * 4096 + mb * 1024) / t / 1e9, 1),
+                   "loop_us": round(tl * 1e6, 1)})
+    out["batched_bf16"] = bt
     out["fused_moe_a4w4_deepseek"] = bench_moe(dev)
     return out
 

@@ -156,6 +156,16 @@ int fused_rms_mx_quant(aiter_tensor_t* x1, aiter_tensor_t* x1_weight, float eps1
                        aiter_tensor_t* out_scale, aiter_tensor_t* out1, aiter_tensor_t* out2,
                        aiter_tensor_t* out_res1, int shuffle, int pad_scale, aiter_stream_t stream);
 
+/* Batched bf16: replace the CK ops batched_gemm_bf16 / batched_gemm_bf16_tune
+ * (aiter/ops/batched_gemm_op_bf16.py:28-36,127-134): XQ [B, M, K], WQ [B, N, K]
+ * (row-major per batch), Y [B, M, N] bf16 or fp32, bias [N] or [B, N] fp32;
+ * any batch and row strides with a unit last-dimension stride.  One launch with
+ * gridDim.z = B.  opus_gemm / opus_gemm_a16w16_tune use the same path. */
+int batched_gemm_bf16(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias, int splitK,
+                      aiter_stream_t stream);
+int batched_gemm_bf16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, int kernelId, int splitK,
+                           aiter_stream_t stream);
+
 /* Low-precision outputs: replaces mxfp4_gemm_asm (aiter/ops/gemm_op_a4w4.py:290-304;
  * gfx1250-only in the reference, whose gemm_a4w4o4 / gemm_a4w4o8 call it).
  * out bf16 [M, N]: as gemm_a4w4_asm without bias; fp4x2 [M, N/2]: e2m1 of the
