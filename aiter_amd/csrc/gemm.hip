@@ -705,7 +705,13 @@ int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
             sa = &usa;
             sb = &usb;
         }
-        GemmCall c{kA4W4, {false, true, true}, A, B, sa, sb, &t, nullptr, 1.0f, 0.0f, kernelName, -1, -1};
+        // f32 tile: the persistent 256x256 kernel when its tiles fill the CUs
+        // (8192^3: 297 vs 338 us through the heuristic's 128x256 tile), else
+        // the heuristic
+        const char* kn = kernelName;
+        if ((!kn || !kn[0]) && ((M + 255) / 256) * ((N + 255) / 256) >= device_cu_count(A->device_id))
+            kn = "a4w4_tile_256x256_f32_persist";
+        GemmCall c{kA4W4, {false, true, true}, A, B, sa, sb, &t, nullptr, 1.0f, 0.0f, kn, -1, -1};
         run_gemm(c, st);
         const int64_t n = M * (N / 8);
         const dim3 grid((unsigned)((n + 255) / 256));
