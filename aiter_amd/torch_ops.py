@@ -153,5 +153,121 @@ def _(x, shuffle=False):
             x.new_empty(_scale_shape(m, k, shuffle), dtype=dtypes.fp8_e8m0))
 
 
+# ------------------------------------------------------ low-precision outputs
+@torch.library.custom_op(f"{NS}::gemm_a4w4o4", mutates_args=(), device_types="cuda")
+def gemm_a4w4o4(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor) -> Tensor:
+    from .gemm_op_a4w4 import gemm_a4w4o4 as op
+
+    return op(A, B, A_scale, B_scale)
+
+
+@gemm_a4w4o4.register_fake
+def _(A, B, A_scale, B_scale):
+    return A.new_empty((*A.shape[:-1], B.shape[0] // 2), dtype=dtypes.fp4x2)
+
+
+@torch.library.custom_op(f"{NS}::gemm_a4w4o8", mutates_args=(), device_types="cuda")
+def gemm_a4w4o8(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor) -> Tuple[Tensor, Tensor]:
+    from .gemm_op_a4w4 import gemm_a4w4o8 as op
+
+    q, s = op(A, B, A_scale, B_scale)
+    return q, s
+
+
+@gemm_a4w4o8.register_fake
+def _(A, B, A_scale, B_scale):
+    n = B.shape[0]
+    return (A.new_empty((*A.shape[:-1], n), dtype=dtypes.fp8),
+            A.new_empty((*A.shape[:-1], n // 128), dtype=dtypes.fp8_e8m0))
+
+
+# ------------------------------------------------------------- batched bf16
+@torch.library.custom_op(f"{NS}::batched_gemm_bf16", mutates_args=(), device_types="cuda")
+def batched_gemm_bf16(XQ: Tensor, WQ: Tensor, bias: Optional[Tensor] = None,
+                      dtype: torch.dtype = dtypes.bf16) -> Tensor:
+    from .batched_gemm_op_bf16 import batched_gemm_bf16_CK as op
+
+    return op(XQ, WQ, bias, dtype)
+
+
+@batched_gemm_bf16.register_fake
+def _(XQ, WQ, bias=None, dtype=dtypes.bf16):
+    return XQ.new_empty((XQ.shape[0], XQ.shape[1], WQ.shape[1]), dtype=dtype)
+
+
+# --------------------------------------------------------------------- MoE
+@torch.library.custom_op(f"{NS}::moe_sorting", mutates_args=(), device_types="cuda")
+def moe_sorting(topk_ids: Tensor, topk_weights: Tensor, num_experts: int, model_dim: int,
+                moebuf_dtype: torch.dtype = dtypes.bf16, block_size: int = 32
+                ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    from .fused_moe import moe_sorting as op
+
+    return op(topk_ids, topk_weights, num_experts, model_dim, moebuf_dtype, block_size)
+
+
+@moe_sorting.register_fake
+def _(topk_ids, topk_weights, num_experts, model_dim, moebuf_dtype=dtypes.bf16, block_size=32):
+    m, topk = topk_ids.shape
+    padded = m * topk + num_experts * block_size - topk
+    return (topk_ids.new_empty((padded,), dtype=torch.int32), topk_ids.new_empty((padded,), dtype=torch.float32),
+            topk_ids.new_empty(((padded + block_size - 1) // block_size,), dtype=torch.int32),
+            topk_ids.new_empty((2,), dtype=torch.int32), topk_ids.new_empty((m, model_dim), dtype=moebuf_dtype))
+
+
+@torch.library.custom_op(f"{NS}::fused_moe", mutates_args=(), device_types="cuda")
+def fused_moe(hidden_states: Tensor, w1: Tensor, w2: Tensor, topk_weight: Tensor, topk_ids: Tensor,
+              w1_scale: Tensor, w2_scale: Tensor, expert_mask: Optional[Tensor] = None, activation: int = 0,
+              doweight_stage1: bool = False, block_size_M: int = -1) -> Tensor:
+    """QuantType.per_1x32 with MXFP4 weights (the schema keeps the arguments
+    this library implements; see aiter_amd.fused_moe)."""
+    from .fused_moe import ActivationType, fused_moe as op
+    from .quant import QuantType
+
+    return op(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=expert_mask,
+              activation=ActivationType(activation), quant_type=QuantType.per_1x32,
+              doweight_stage1=doweight_stage1, w1_scale=w1_scale, w2_scale=w2_scale,
+              block_size_M=block_size_M if block_size_M > 0 else None)
+
+
+@fused_moe.register_fake
+def _(hidden_states, w1, w2, topk_weight, topk_ids, w1_scale, w2_scale, expert_mask=None, activation=0,
+      doweight_stage1=False, block_size_M=-1):
+    return hidden_states.new_empty((hidden_states.shape[0], w2.shape[1]), dtype=dtypes.bf16)
+
+
+# ------------------------------------------------------- fused RMSNorm quant
+@torch.library.custom_op(f"{NS}::fused_rms_mxfp4_quant", mutates_args=(), device_types="cuda")
+def fused_rms_mxfp4_quant(x1: Tensor, x1_weight: Tensor, x1_epsilon: float,
+                          shuffle: bool = False) -> Tuple[Tensor, Tensor]:
+    """The single-input form of aiter_amd.fused_rms_mxfp4_quant: (fp4x2, e8m0)."""
+    from .fused_quant import fused_rms_mxfp4_quant as op
+
+    (q, s), _, _, _ = op(x1, x1_weight, x1_epsilon, shuffle=shuffle)
+    return q, s
+
+
+@fused_rms_mxfp4_quant.register_fake
+def _(x1, x1_weight, x1_epsilon, shuffle=False):
+    m, n = x1.shape
+    sn = (n + 31) // 32
+    shape = ((m + 255) // 256 * 256, (sn + 7) // 8 * 8) if shuffle else (m, sn)
+    return x1.new_empty((m, n // 2), dtype=torch.uint8), x1.new_empty(shape, dtype=torch.uint8)
+
+
+@torch.library.custom_op(f"{NS}::fused_rms_mxfp8_quant", mutates_args=(), device_types="cuda")
+def fused_rms_mxfp8_quant(x: Tensor, weight: Tensor, eps: float) -> Tuple[Tensor, Tensor]:
+    from .fused_quant import fused_rms_mxfp8_quant as op
+
+    y, s = op(x, weight, eps)
+    return y, s
+
+
+@fused_rms_mxfp8_quant.register_fake
+def _(x, weight, eps):
+    m, k = x.shape
+    return x.new_empty((m, k), dtype=dtypes.fp8), x.new_empty((m, k // 32), dtype=torch.uint8)
+
+
 OPS = ("gemm_a4w4", "gemm_a4w4_asm", "gemm_a8w4_mxfp8", "gemm_a16w16", "gemm_a16w16_opus", "dynamic_mxfp4_quant",
-       "dynamic_mxfp8_quant", "per_1x32_f4_quant_hip")
+       "dynamic_mxfp8_quant", "per_1x32_f4_quant_hip", "gemm_a4w4o4", "gemm_a4w4o8", "batched_gemm_bf16",
+       "moe_sorting", "fused_moe", "fused_rms_mxfp4_quant", "fused_rms_mxfp8_quant")

@@ -85,3 +85,89 @@ def test_opcheck_quant(cuda, shuffle):
     assert torch.equal(y.view(torch.uint8), y2.view(torch.uint8))
     rows = (100 + 31) // 32 * 32 if shuffle else 100      # rows past pad32(M) are never written
     assert torch.equal(s.view(torch.uint8)[:rows], s2.view(torch.uint8)[:rows])
+
+
+META_ONLY = ("test_schema", "test_autograd_registration", "test_faketensor")
+
+
+def test_opcheck_lowp_outputs(cuda):
+    import aiter_amd
+
+    announce("opcheck gemm_a4w4o4 / gemm_a4w4o8")
+    _, aq, as_, bq, bs = _mx_operands(cuda, m=128)
+    # fp4x2 / e4m3 / e8m0 outputs: metadata checks, then byte equality with the Python entry points
+    torch.library.opcheck(torch.ops.aiter_amd.gemm_a4w4o4.default, (aq, bq, as_, bs), test_utils=META_ONLY)
+    torch.library.opcheck(torch.ops.aiter_amd.gemm_a4w4o8.default, (aq, bq, as_, bs), test_utils=META_ONLY)
+    o4 = torch.ops.aiter_amd.gemm_a4w4o4(aq, bq, as_, bs)
+    assert torch.equal(o4.view(torch.uint8), aiter_amd.gemm_a4w4o4(aq, bq, as_, bs).view(torch.uint8))
+    q, s = torch.ops.aiter_amd.gemm_a4w4o8(aq, bq, as_, bs)
+    q2, s2 = aiter_amd.gemm_a4w4o8(aq, bq, as_, bs)
+    assert torch.equal(q.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(s.view(torch.uint8), s2.view(torch.uint8))
+
+
+def test_opcheck_batched_bf16(cuda):
+    import aiter_amd
+
+    announce("opcheck batched_gemm_bf16")
+    g = torch.Generator().manual_seed(83)
+    x = torch.randn((4, 40, 512), generator=g).to(dtypes.bf16).to(cuda)
+    w = torch.randn((4, 256, 512), generator=g).to(dtypes.bf16).to(cuda)
+    torch.library.opcheck(torch.ops.aiter_amd.batched_gemm_bf16.default, (x, w))
+    assert torch.equal(torch.ops.aiter_amd.batched_gemm_bf16(x, w), aiter_amd.batched_gemm_bf16_CK(x, w))
+
+
+def test_opcheck_moe(cuda):
+    import numpy as np
+
+    import aiter_amd
+    from oracle import mx_oracle as O
+
+    announce("opcheck moe_sorting / fused_moe")
+    rng = np.random.default_rng(84)
+    m, e, topk, dim, inter = 20, 8, 2, 256, 256
+    ids = torch.from_numpy(np.stack([rng.choice(e, topk, replace=False) for _ in range(m)]).astype(np.int32)).to(cuda)
+    wts = torch.from_numpy(rng.random((m, topk)).astype(np.float32)).to(cuda)
+    # sorted lists hold unwritten tails past num_valid_ids: metadata checks only
+    torch.library.opcheck(torch.ops.aiter_amd.moe_sorting.default, (ids, wts, e, dim, dtypes.bf16, 32),
+                          test_utils=META_ONLY)
+    s, sw, se, nv, _ = torch.ops.aiter_amd.moe_sorting(ids, wts, e, dim, dtypes.bf16, 32)
+    s2, sw2, se2, nv2, _ = aiter_amd.moe_sorting(ids, wts, e, dim, dtypes.bf16, 32)
+    n = int(nv[0])
+    assert torch.equal(nv, nv2) and torch.equal(s[:n], s2[:n]) and torch.equal(sw[:n], sw2[:n])
+    assert torch.equal(se[: n // 32], se2[: n // 32])
+
+    def w_dev(rows, k):
+        q = rng.integers(0, 256, (e * rows, k // 2), dtype=np.uint8)
+        sc = rng.integers(119, 123, (e * rows, k // 32), dtype=np.uint8)
+        return (torch.from_numpy(O.shuffle_weight(q).reshape(e, rows, k // 2)).to(cuda),
+                torch.from_numpy(O.shuffle_scale(sc)).to(cuda))
+
+    w1, s1 = w_dev(2 * inter, dim)
+    w2, s2_ = w_dev(dim, inter)
+    x = torch.from_numpy(rng.standard_normal((m, dim)).astype(np.float32)).to(dtypes.bf16).to(cuda)
+    # stage 2 may sum slots in either order: metadata checks, then closeness
+    torch.library.opcheck(torch.ops.aiter_amd.fused_moe.default, (x, w1, w2, wts, ids, s1, s2_), test_utils=META_ONLY)
+    got = torch.ops.aiter_amd.fused_moe(x, w1, w2, wts, ids, s1, s2_)
+    want = aiter_amd.fused_moe(x, w1, w2, wts, ids, quant_type=aiter_amd.QuantType.per_1x32, w1_scale=s1,
+                               w2_scale=s2_)
+    torch.testing.assert_close(got.float(), want.float(), rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_opcheck_fused_rms_quant(cuda, shuffle):
+    import aiter_amd
+
+    announce(f"opcheck fused_rms_mxfp4/8_quant shuffle={shuffle}")
+    g = torch.Generator().manual_seed(85)
+    x = torch.randn((256, 1024), generator=g).to(dtypes.bf16).to(cuda)
+    w = torch.randn((1024,), generator=g).to(dtypes.bf16).to(cuda)
+    torch.library.opcheck(torch.ops.aiter_amd.fused_rms_mxfp4_quant.default, (x, w, 1e-6, shuffle),
+                          test_utils=META_ONLY)
+    q, s = torch.ops.aiter_amd.fused_rms_mxfp4_quant(x, w, 1e-6, shuffle)
+    (q2, s2), _, _, _ = aiter_amd.fused_rms_mxfp4_quant(x, w, 1e-6, shuffle=shuffle)
+    assert torch.equal(q, q2) and torch.equal(s, s2)
+    torch.library.opcheck(torch.ops.aiter_amd.fused_rms_mxfp8_quant.default, (x, w, 1e-6), test_utils=META_ONLY)
+    y, s8 = torch.ops.aiter_amd.fused_rms_mxfp8_quant(x, w, 1e-6)
+    y2, s82 = aiter_amd.fused_rms_mxfp8_quant(x, w, 1e-6)
+    assert torch.equal(y.view(torch.uint8), y2.view(torch.uint8)) and torch.equal(s8, s82)

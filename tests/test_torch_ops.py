@@ -52,3 +52,45 @@ def test_cpu_tensors_fail_loudly():
         torch.ops.aiter_amd.gemm_a16w16(x, torch.zeros(16, 64, dtype=dtypes.bf16))
     with pytest.raises(NotImplementedError):
         torch.ops.aiter_amd.dynamic_mxfp4_quant(x)
+
+
+def test_fake_lowp_and_batched_shapes():
+    a = torch.empty(128, 256, dtype=torch.uint8, device=META)
+    b = torch.empty(512, 256, dtype=torch.uint8, device=META)
+    sa = torch.empty(128, 16, dtype=torch.uint8, device=META)
+    sb = torch.empty(512, 16, dtype=torch.uint8, device=META)
+    o4 = torch.ops.aiter_amd.gemm_a4w4o4(a, b, sa, sb)
+    assert o4.shape == (128, 256) and o4.dtype == dtypes.fp4x2
+    q, s = torch.ops.aiter_amd.gemm_a4w4o8(a, b, sa, sb)
+    assert q.shape == (128, 512) and q.dtype == dtypes.fp8
+    assert s.shape == (128, 4) and s.dtype == dtypes.fp8_e8m0
+    x = torch.empty(16, 7, 256, dtype=dtypes.bf16, device=META)
+    w = torch.empty(16, 96, 256, dtype=dtypes.bf16, device=META)
+    y = torch.ops.aiter_amd.batched_gemm_bf16(x, w)
+    assert y.shape == (16, 7, 96) and y.dtype == dtypes.bf16
+
+
+def test_fake_moe_shapes():
+    ids = torch.empty(5, 9, dtype=torch.int32, device=META)
+    wts = torch.empty(5, 9, dtype=torch.float32, device=META)
+    s, sw, se, nv, buf = torch.ops.aiter_amd.moe_sorting(ids, wts, 257, 7168, dtypes.bf16, 32)
+    padded = 5 * 9 + 257 * 32 - 9
+    assert s.shape == (padded,) and sw.shape == (padded,) and se.shape == ((padded + 31) // 32,)
+    assert nv.shape == (2,) and buf.shape == (5, 7168) and buf.dtype == dtypes.bf16
+    h = torch.empty(5, 512, dtype=dtypes.bf16, device=META)
+    w1 = torch.empty(8, 512, 256, dtype=torch.uint8, device=META)
+    w2 = torch.empty(8, 512, 128, dtype=torch.uint8, device=META)
+    s1 = torch.empty(8 * 512, 16, dtype=torch.uint8, device=META)
+    s2 = torch.empty(8 * 512, 8, dtype=torch.uint8, device=META)
+    out = torch.ops.aiter_amd.fused_moe(h, w1, w2, wts[:, :2], ids[:, :2], s1, s2)
+    assert out.shape == (5, 512) and out.dtype == dtypes.bf16
+
+
+@pytest.mark.parametrize("shuffle", [False, True])
+def test_fake_fused_rms_quant_shapes(shuffle):
+    x = torch.empty(300, 1056, dtype=dtypes.bf16, device=META)
+    w = torch.empty(1056, dtype=dtypes.bf16, device=META)
+    q, s = torch.ops.aiter_amd.fused_rms_mxfp4_quant(x, w, 1e-6, shuffle)
+    assert q.shape == (300, 528) and s.shape == ((512, 40) if shuffle else (300, 33))
+    y, s8 = torch.ops.aiter_amd.fused_rms_mxfp8_quant(x[:, :1024], w[:1024], 1e-6)
+    assert y.shape == (300, 1024) and y.dtype == dtypes.fp8 and s8.shape == (300, 32)
