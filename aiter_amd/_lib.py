@@ -117,6 +117,7 @@ SIGNATURES = {
     "aiter_amd_num_kernels": ([], ctypes.c_int),
     "aiter_amd_kernel_info": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
     "gemm_workspace_reserve": ([ctypes.c_int, _S, ctypes.c_size_t], ctypes.c_int),
+    "hbm_stream_read": ([_T, _T, ctypes.c_int, _S], ctypes.c_int),
 }
 
 

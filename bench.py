@@ -42,7 +42,7 @@ PEAK_MXFP8 = 5000.0
 PEAK_BF16 = 2500.0
 PEAK_HBM = 8000.0      # GB/s
 COPY_BYTES = 1 << 30    # calibration copy of the traffic counter runs
-REF_A4W4_8192 = 5089.97  # TFLOP/s, aiter/configs/a4w4_blockscale_tuned_gemm.csv:1284 (BASELINE.md)
+REF_A4W4_8192 = 5089.97  # TFLOP/s, aiter/configs/a4w4_blockscale_tuned_gemm.csv:1284
 
 
 def log(msg):
@@ -127,6 +127,33 @@ def bench_prefill(steps, warmup, dev):
     return sec, flop / sec / 1e12, kname
 
 
+_CEIL = {}
+
+
+def read_ceiling(dev, nbytes, grid=1024):
+    """Seconds per call of the calibration streaming read (`hbm_stream_read`,
+    nothing but 16-byte loads) over ``nbytes``, cold: the buffers rotate
+    through > 512 MiB.  The attainable HBM read time at that byte count,
+    launch and ramp included, that a bandwidth-bound GEMM is compared to."""
+    from aiter_amd._lib import call
+
+    n = (nbytes + 15) // 16 * 16
+    if n not in _CEIL:
+        copies = max(2, -(-(600 << 20) // n))
+        bufs = [torch.ones(n, dtype=torch.uint8, device=dev) for _ in range(copies)]
+        sink = torch.zeros(1, dtype=torch.int32, device=dev)
+        it = {"i": 0}
+
+        def run():
+            b = bufs[it["i"] % copies]
+            it["i"] += 1
+            call("hbm_stream_read", b, sink, grid)
+
+        _CEIL[n] = time_graph(run, copies * (4 if copies <= 100 else 1), 3)
+        del bufs
+    return _CEIL[n]
+
+
 def bench_decode(dev, steps=50):
     import aiter_amd
 
@@ -163,6 +190,7 @@ def bench_decode(dev, steps=50):
         t_cold = time_graph(cold, min(steps, copies), 3)
         t_warm = time_graph(warm, steps, 3)
         byts = a4w4_bytes(m, n, k)
+        t_ceil = read_ceiling(dev, byts)
         ref_bw = (m * k / 2 + n * k / 2 + 2 * m * n)  # reference `bw` formula (scales excluded)
         res.append({
             "M": m, "N": n, "K": k, "kernel": kname or "heuristic",
@@ -170,9 +198,75 @@ def bench_decode(dev, steps=50):
             "GBps_cold": round(byts / t_cold / 1e9, 1), "GBps_warm": round(byts / t_warm / 1e9, 1),
             "hbm_frac_cold": round(byts / t_cold / 1e9 / PEAK_HBM, 4),
             "ref_formula_GBps_cold": round(ref_bw / t_cold / 1e9, 1),
+            "read_ceiling_us": round(t_ceil * 1e6, 3), "frac_of_read_ceiling": round(t_ceil / t_cold, 4),
         })
         log(f"decode M={m}: cold {t_cold*1e6:.2f} us ({byts/t_cold/1e9:.0f} GB/s), warm {t_warm*1e6:.2f} us")
     return res
+
+
+SWEEP_NK = ((4096, 4096), (14336, 4096), (4096, 14336), (28672, 8192), (8192, 28672))
+
+
+def bench_decode_sweep(dev, ms=(1, 32)):
+    """Decode rows of the dispatch sweep (BASELINE configs[4]): M in {1, 32}
+    over its five (N, K), A4W4 (MXFP4 activations, preshuffled B) and bf16,
+    cold: the weights rotate through > 512 MiB of copies so every call reads
+    them from HBM.  GB/s counts A, B, their scales and C once;
+    ``frac_of_read_ceiling`` = the calibration read's time over as many bytes
+    / the GEMM's time."""
+    import aiter_amd
+
+    rows = []
+    g = torch.Generator(device="cpu").manual_seed(3)
+    for n, k in SWEEP_NK:
+        b = torch.randn((n, k), generator=g).to(dev)
+        bq, bs = aiter_amd.dynamic_mxfp4_quant(b, shuffle=True)
+        bq = aiter_amd.shuffle_weight(bq)
+        b16 = b.to(torch.bfloat16)
+        del b
+        for fam in ("a4w4", "bf16"):
+            per = bq.numel() + bs.numel() if fam == "a4w4" else b16.numel() * 2
+            copies = max(2, -(-(600 << 20) // per))
+            if fam == "a4w4":
+                ws = [(bq.clone(), bs.clone()) for _ in range(copies)]
+            else:
+                ws = [b16.clone() for _ in range(copies)]
+            for m in ms:
+                a = torch.randn((m, k), generator=g).to(dev)
+                it = {"i": 0}
+                if fam == "a4w4":
+                    aq, as_ = aiter_amd.dynamic_mxfp4_quant(a, shuffle=True)
+                    cfg = aiter_amd.get_GEMM_config(m, n, k)
+                    kname = str(cfg["kernelName"]) if cfg else ""
+                    l2 = int(cfg.get("splitK", 0) or 0) if cfg else 0
+                    out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=dev)
+                    byts = a4w4_bytes(m, n, k)
+
+                    def cold():
+                        w, sc = ws[it["i"] % copies]
+                        it["i"] += 1
+                        aiter_amd.gemm_a4w4_asm(aq, w, as_, sc, out, kernelName=kname, log2_k_split=l2)
+                else:
+                    a16 = a.to(torch.bfloat16)
+                    kname = "tuned/heuristic"
+                    byts = 2 * (m * k + n * k + m * n)
+
+                    def cold():
+                        w = ws[it["i"] % copies]
+                        it["i"] += 1
+                        aiter_amd.gemm_a16w16(a16, w)
+                t = time_graph(cold, copies * 4, 3)
+                t_ceil = read_ceiling(dev, byts)
+                rows.append({"fam": fam, "M": m, "N": n, "K": k, "kernel": kname or "heuristic",
+                             "us_cold": round(t * 1e6, 2), "GBps_cold": round(byts / t / 1e9, 1),
+                             "hbm_frac_cold": round(byts / t / 1e9 / PEAK_HBM, 4),
+                             "read_ceiling_us": round(t_ceil * 1e6, 2),
+                             "frac_of_read_ceiling": round(t_ceil / t, 4)})
+                log(f"decode sweep {fam} M={m} N={n} K={k}: {t*1e6:.2f} us, {byts/t/1e9:.0f} GB/s")
+            del ws
+        del bq, bs, b16
+        torch.cuda.empty_cache()
+    return rows
 
 
 def bench_extra(dev):
@@ -404,6 +498,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--moe", action="store_true", help="only the fused-MoE workloads (for profiling)")
+    ap.add_argument("--decode", action="store_true", help="only the decode workloads (configs[1] and configs[4])")
     ap.add_argument("--pmc", action="store_true",
                     help="only the launches of the HBM-traffic counter runs (copy calibration + A4W4 8192^3)")
     args = ap.parse_args()
@@ -422,11 +517,15 @@ def main():
     if args.moe:
         print(json.dumps({"fused_moe_a4w4_deepseek": bench_moe(dev)}), flush=True)
         return
+    if args.decode:
+        print(json.dumps({"decode": bench_decode(dev), "decode_sweep": bench_decode_sweep(dev)}), flush=True)
+        return
 
     log("prefill A4W4 8192^3")
     sec, tflops, kname = bench_prefill(args.steps, args.warmup, dev)
     log(f"prefill: {sec*1e6:.1f} us/step, {tflops:.0f} TFLOP/s ({kname or 'heuristic'})")
     decode = [] if args.quick else bench_decode(dev)
+    sweep = [] if args.quick else bench_decode_sweep(dev)
     extra = {} if args.quick else bench_extra(dev)
     cpu = None if (args.no_cpu or args.quick) else cpu_baseline()
     m = n = k = 8192
@@ -449,6 +548,7 @@ def main():
                      "frac": round(tflops / PEAK_MXFP4, 4), "traffic": traffic_from_profiles()},
         "cpu_baseline": cpu,
         "decode": decode,
+        "decode_sweep": sweep,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

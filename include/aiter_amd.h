@@ -261,6 +261,14 @@ int aiter_amd_kernel_info(int id, char* buf, int buflen);
  * aiter/ops/opus/gemm_op_opus.py (opus_gemm_workspace_init). */
 int gemm_workspace_reserve(int device, aiter_stream_t stream, size_t bytes);
 
+/* ---- calibration ---------------------------------------------------------
+ * No counterpart in the reference: a plain streaming read of src (contiguous
+ * 1-D, 16-byte aligned, any dtype) with `grid` workgroups of 256 threads and
+ * nothing else in the kernel.  Its rate at a given byte count is the
+ * attainable HBM read rate that the bandwidth-bound decode GEMMs are
+ * compared against; sink (one int32) only keeps the reads live. */
+int hbm_stream_read(aiter_tensor_t* src, aiter_tensor_t* sink, int grid, aiter_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

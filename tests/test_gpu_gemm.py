@@ -348,3 +348,18 @@ def test_bf16_cpu_plumbing_config(cuda):
         torch.cuda.synchronize()
         ok, msg = allclose_report(got.float().cpu().numpy(), ref)
         assert ok, msg
+
+
+def test_hbm_stream_read_calibration(cuda):
+    """The calibration read runs over a buffer, leaves the sink alone (the
+    xor of an even number of equal words is 0) and rejects a strided view."""
+    from aiter_amd._lib import call
+
+    announce("hbm_stream_read 1 MiB")
+    buf = torch.ones(1 << 20, dtype=torch.uint8, device=cuda)
+    sink = torch.zeros(1, dtype=torch.int32, device=cuda)
+    call("hbm_stream_read", buf, sink, 64)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    with pytest.raises(RuntimeError, match="contiguous"):
+        call("hbm_stream_read", buf[::2], sink, 64)
