@@ -86,9 +86,9 @@ void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT><<<grid, 256, 0, s>>>(p);
 }
 
-template <int KA, int MF, bool BP, bool SPLIT, bool OF>
+template <int KA, int MF, bool BP, bool SPLIT, bool OF, int NB = 1>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
+    gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
 }
 
 std::vector<Instance>& registry() {
@@ -103,13 +103,14 @@ std::vector<Instance>& registry() {
             if (v.out_f32) nm += "_f32";
             reg.push_back({id++, nm, f, false, bm, bn, false, v, fn});
         };
-        auto skinny = [&](Family f, int mf, bool split, Variant v, LaunchFn fn, const char* fam) {
+        auto skinny = [&](Family f, int mf, bool split, Variant v, LaunchFn fn, const char* fam, int bn = 16) {
             std::string nm = std::string(fam) + "_skinny_m" + std::to_string(16 * mf);
+            if (bn != 16) nm += "_n" + std::to_string(bn);
             if (split) nm += "_splitk";
             if (v.a_pre) nm += "_apre";
             if (!v.b_pre) nm += "_bplain";
             if (v.out_f32) nm += "_f32";
-            reg.push_back({id++, nm, f, true, 16 * mf, 16, split, v, fn});
+            reg.push_back({id++, nm, f, true, 16 * mf, bn, split, v, fn});
         };
         // ---- a4w4 (B preshuffled): 32x32x64 tile kernels; the 256-column
         // tiles read B straight into registers (gemm_flat.h), the others stage
@@ -238,6 +239,13 @@ std::vector<Instance>& registry() {
         skinny(kA4W4, 4, true, pre32, launch_skinny<kFp4, 4, true, true, true>, "a4w4");
         tsplit(kA4W4, 64, 128, pre32, launch_t32<kFp4, true, 64, 128, 1, true, true>, "a4w4");
         persist(kA4W4, 256, pre32, launch_flat_persist<kFp4, 256, true>, "a4w4");
+        // ---- skinny with 32 columns per workgroup (one A fragment serves two
+        // B blocks); appended last so that earlier kernel ids stay put ----
+        skinny(kA4W4, 1, false, pre, launch_skinny<kFp4, 1, true, false, false, 2>, "a4w4", 32);
+        skinny(kA4W4, 2, false, pre, launch_skinny<kFp4, 2, true, false, false, 2>, "a4w4", 32);
+        const Variant a8n{false, true, false};
+        skinny(kA8W4, 1, false, a8n, launch_skinny<kFp8, 1, true, false, false, 2>, "a8w4", 32);
+        skinny(kA8W4, 2, false, a8n, launch_skinny<kFp8, 2, true, false, false, 2>, "a8w4", 32);
     });
     return reg;
 }
@@ -283,8 +291,15 @@ const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int c
         const int mf = M <= 16 ? 1 : 2;
         const int nblk = (N + 15) / 16;
         const int s = skinny_splits(nblk, ksteps, cus);
+        // 32-column workgroups when M > 8 and they still cover ~3/4 of the
+        // CUs: each A fragment then serves two B blocks (A's L2 traffic per
+        // B byte halves); measured 4.3 -> 4.0 us at M=16 and 5.4 -> 4.4 us at
+        // M=32 for N=7168, K=2048, and no gain at M=1
+        if (M > 8 && s == 1 && (N + 31) / 32 * 4 >= cus * 3)
+            for (auto& in : registry())
+                if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.bn == 32 && !in.split) return &in;
         for (auto& in : registry())
-            if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.split == (s > 1)) {
+            if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.bn == 16 && in.split == (s > 1)) {
                 *splits = s;
                 return &in;
             }
@@ -553,7 +568,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         splits = batched ? 1 : std::max(1, std::min(splits, kpairs));
         p.k_steps_per_split = (kpairs + splits - 1) / splits;
         splits = (kpairs + p.k_steps_per_split - 1) / p.k_steps_per_split;
-        const dim3 grid((unsigned)((N + 15) / 16), (unsigned)splits);
+        const dim3 grid((unsigned)((N + inst->bn - 1) / inst->bn), (unsigned)splits);
         if (inst->split && splits > 1) {
             const size_t need = (size_t)M * N * sizeof(float);
             p.ws = workspace(dev, stream, need);
@@ -568,7 +583,8 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             // a split instance asked for one split runs its non-split twin
             const Instance* twin = nullptr;
             for (auto& in : registry())
-                if (in.skinny && !in.split && variant_ok(in, c.fam, c.var) && in.bm == inst->bm) twin = &in;
+                if (in.skinny && !in.split && variant_ok(in, c.fam, c.var) && in.bm == inst->bm && in.bn == inst->bn)
+                    twin = &in;
             AA_CHECK(twin, "no non-split twin for ", inst->name);
             p.k_steps_per_split = kpairs;
             twin->fn(p, dim3(grid.x, 1, c.batch), stream);

@@ -363,27 +363,29 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(GemmParams p) {
 // blocks (gridDim.y > 1) the block result is atomically added to an f32
 // workspace that a second kernel converts.
 // ---------------------------------------------------------------------------
-template <int KA, int MF>
+template <int KA, int MF, int NB>
 struct SkinnyPair {
     static constexpr int FA = OpTraits<KA>::frags_per_step;
     static constexpr bool SCALED = OpTraits<KA>::scaled;
     static constexpr int SGRP = (MF + 1) / 2;
-    i32x4_t b[2];
+    static constexpr int SBN = (NB + 1) / 2;   // 32-row B scale groups
+    i32x4_t b[2][NB];
     i32x4_t a[2][MF][FA];
-    int sb;
+    int sb[SBN];
     int sa[SGRP];
 };
 
-template <int KA, int MF, bool B_PRE>
-AA_DEV void skinny_load(SkinnyPair<KA, MF>& d, int pr, const uint8_t* bsrc, const uint8_t* const* asrc,
-                        const bool* arow_ok, const uint8_t* sbp, const uint8_t* const* sap) {
-    using P = SkinnyPair<KA, MF>;
+template <int KA, int MF, int NB, bool B_PRE>
+AA_DEV void skinny_load(SkinnyPair<KA, MF, NB>& d, int pr, const uint8_t* const* bsrc, const uint8_t* const* asrc,
+                        const bool* arow_ok, const uint8_t* const* sbp, const uint8_t* const* sap) {
+    using P = SkinnyPair<KA, MF, NB>;
     constexpr int A_STEP_BYTES = KA == kFp8 ? 128 : 64;
     constexpr int BSTEP = B_PRE ? 1024 : 64;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const int s = 2 * pr + h;
-        d.b[h] = *reinterpret_cast<const i32x4_t*>(bsrc + (int64_t)s * BSTEP);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) d.b[h][j] = *reinterpret_cast<const i32x4_t*>(bsrc[j] + (int64_t)s * BSTEP);
 #pragma unroll
         for (int i = 0; i < MF; ++i)
 #pragma unroll
@@ -393,50 +395,67 @@ AA_DEV void skinny_load(SkinnyPair<KA, MF>& d, int pr, const uint8_t* bsrc, cons
             }
     }
     if constexpr (P::SCALED) {
-        d.sb = *reinterpret_cast<const int*>(sbp + (int64_t)pr * 256);
+#pragma unroll
+        for (int g = 0; g < P::SBN; ++g) d.sb[g] = *reinterpret_cast<const int*>(sbp[g] + (int64_t)pr * 256);
 #pragma unroll
         for (int g = 0; g < P::SGRP; ++g) d.sa[g] = *reinterpret_cast<const int*>(sap[g] + (int64_t)pr * 256);
     }
 }
 
-template <int KA, int MF>
-AA_DEV void skinny_mma(const SkinnyPair<KA, MF>& d, f32x4_t* acc, int bhalf) {
+// BHALF0: which 16-column half of its 32-row B scale group the first
+// column block covers (block j covers half BHALF0 + j)
+template <int KA, int MF, int NB, int BHALF0>
+AA_DEV void skinny_mma(const SkinnyPair<KA, MF, NB>& d, f32x4_t (*acc)[NB]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h)
 #pragma unroll
-        for (int i = 0; i < MF; ++i) {
-            if constexpr (OpTraits<KA>::scaled) {
-                if (bhalf)
-                    acc[i] = mma_step<KA, kFp4>(&d.b[h], d.a[h][i], acc[i], d.sb, h * 2 + 1, d.sa[i >> 1],
-                                                h * 2 + (i & 1));
-                else
-                    acc[i] = mma_step<KA, kFp4>(&d.b[h], d.a[h][i], acc[i], d.sb, h * 2, d.sa[i >> 1],
-                                                h * 2 + (i & 1));
-            } else {
-                acc[i] = mma_step<KA, KA>(&d.b[h], d.a[h][i], acc[i], 0, 0, 0, 0);
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                if constexpr (OpTraits<KA>::scaled) {
+                    const int bh = (BHALF0 + j) & 1;
+                    const int g = (BHALF0 + j) >> 1;
+                    if (bh)
+                        acc[i][j] = mma_step<KA, kFp4>(&d.b[h][j], d.a[h][i], acc[i][j], d.sb[g], h * 2 + 1,
+                                                       d.sa[i >> 1], h * 2 + (i & 1));
+                    else
+                        acc[i][j] = mma_step<KA, kFp4>(&d.b[h][j], d.a[h][i], acc[i][j], d.sb[g], h * 2,
+                                                       d.sa[i >> 1], h * 2 + (i & 1));
+                } else {
+                    acc[i][j] = mma_step<KA, KA>(&d.b[h][j], d.a[h][i], acc[i][j], 0, 0, 0, 0);
+                }
             }
-        }
 }
 
-template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32>
+// NB column blocks of 16 per workgroup share each A fragment (NB = 2: the
+// two halves of one 32-row B scale group, so one scale dword serves both)
+template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB = 1>
 __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
+    static_assert(NB == 1 || NB == 2, "one or two column blocks per workgroup");
     apply_batch(p);
     constexpr bool SCALED = OpTraits<KA>::scaled;
     constexpr int KPAIR = SCALED ? 256 : 64;               // elements per k-pair
     constexpr int SGRP = (MF + 1) / 2;                     // 32-row A scale groups
+    constexpr int SBN = (NB + 1) / 2;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * NB;
     const int total_pairs = p.K / KPAIR;
     const int p_begin = blockIdx.y * p.k_steps_per_split;   // k_steps_per_split counts pairs here
     const int p_end = min(total_pairs, p_begin + p.k_steps_per_split);
 
-    const uint8_t* bsrc;
-    if constexpr (B_PRE)
-        bsrc = p.B + (int64_t)n0 * p.ldb + lane * 16;
-    else
-        bsrc = p.B + (int64_t)min(n0 + (lane & 15), p.N - 1) * p.ldb + (lane >> 4) * 16;
+    const uint8_t* bsrc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        // a block past N (odd block count, NB = 2) reads the last valid rows;
+        // its columns are never stored
+        const int nb0 = min(n0 + 16 * j, (p.N - 1) / 16 * 16);
+        if constexpr (B_PRE)
+            bsrc[j] = p.B + (int64_t)nb0 * p.ldb + lane * 16;
+        else
+            bsrc[j] = p.B + (int64_t)min(nb0 + (lane & 15), p.N - 1) * p.ldb + (lane >> 4) * 16;
+    }
     const uint8_t* asrc[MF];
     bool arow_ok[MF];
 #pragma unroll
@@ -445,46 +464,60 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
         arow_ok[i] = row < p.M;
         asrc[i] = p.A + (int64_t)min(row, p.M - 1) * p.lda + (lane >> 4) * 16;
     }
-    const uint8_t* sbp = nullptr;
+    const uint8_t* sbp[SBN];
     const uint8_t* sap[SGRP];
     if constexpr (SCALED) {
-        sbp = p.Bs + (int64_t)(n0 / 32) * 32 * p.sb_stride + lane * 4;
+#pragma unroll
+        for (int g = 0; g < SBN; ++g) {
+            const int nb0 = min(n0 + 32 * g, (p.N - 1) / 16 * 16);
+            sbp[g] = p.Bs + (int64_t)(nb0 / 32) * 32 * p.sb_stride + lane * 4;
+        }
 #pragma unroll
         for (int g = 0; g < SGRP; ++g)
             sap[g] = p.As + (int64_t)min(g, p.sa_groups - 1) * 32 * p.sa_stride + lane * 4;
     }
-    const int bhalf = (n0 / 16) & 1;
 
-    f32x4_t acc[MF];
+    f32x4_t acc[MF][NB];
 #pragma unroll
-    for (int i = 0; i < MF; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // software pipeline: the next pair's loads are in flight while the
     // current pair is multiplied
-    int pr = p_begin + wave;
-    if (pr < p_end) {
-        SkinnyPair<KA, MF> cur;
-        skinny_load<KA, MF, B_PRE>(cur, pr, bsrc, asrc, arow_ok, sbp, sap);
-        for (pr += NW; pr < p_end; pr += NW) {
-            SkinnyPair<KA, MF> nxt;
-            skinny_load<KA, MF, B_PRE>(nxt, pr, bsrc, asrc, arow_ok, sbp, sap);
-            skinny_mma<KA, MF>(cur, acc, bhalf);
-            cur = nxt;
+    auto run = [&](auto bh) {
+        constexpr int BH = decltype(bh)::value;
+        int pr = p_begin + wave;
+        if (pr < p_end) {
+            SkinnyPair<KA, MF, NB> cur;
+            skinny_load<KA, MF, NB, B_PRE>(cur, pr, bsrc, asrc, arow_ok, sbp, sap);
+            for (pr += NW; pr < p_end; pr += NW) {
+                SkinnyPair<KA, MF, NB> nxt;
+                skinny_load<KA, MF, NB, B_PRE>(nxt, pr, bsrc, asrc, arow_ok, sbp, sap);
+                skinny_mma<KA, MF, NB, BH>(cur, acc);
+                cur = nxt;
+            }
+            skinny_mma<KA, MF, NB, BH>(cur, acc);
         }
-        skinny_mma<KA, MF>(cur, acc, bhalf);
-    }
+    };
+    // NB = 2 starts on a 32-row group boundary; NB = 1 on either half
+    if (NB == 1 && ((n0 / 16) & 1)) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 0>{});
 
-    __shared__ f32x4_t red[NW][MF][64];
+    __shared__ f32x4_t red[NW][MF * NB][64];
 #pragma unroll
-    for (int i = 0; i < MF; ++i) red[wave][i][lane] = acc[i];
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) red[wave][i * NB + j][lane] = acc[i][j];
     __syncthreads();
-    for (int t = threadIdx.x; t < MF * 64; t += 64 * NW) {
-        const int i = t / 64, l = t % 64;
-        f32x4_t s = red[0][i][l];
+    for (int t = threadIdx.x; t < MF * NB * 64; t += 64 * NW) {
+        const int ij = t / 64, l = t % 64;
+        const int i = ij / NB, j = ij % NB;
+        f32x4_t s = red[0][ij][l];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) s += red[w][i][l];
+        for (int w = 1; w < NW; ++w) s += red[w][ij][l];
         const int m = i * 16 + (l & 15);
-        const int n = n0 + 4 * (l >> 4);
+        const int n = n0 + 16 * j + 4 * (l >> 4);
         if constexpr (SPLIT) {
             if (m < p.M && n < p.N) {
                 float* w = p.ws + (int64_t)m * p.N + n;

@@ -31,7 +31,7 @@ def _dev(x, cuda):
 
 A4W4_SHAPES = [(1, 256, 256), (5, 512, 512), (16, 1024, 1024), (32, 7168, 2048), (33, 640, 1280),
                (64, 7168, 2048), (65, 256, 512), (128, 1024, 1024), (256, 512, 2048), (300, 1040, 768),
-               (512, 512, 512)]
+               (512, 512, 512), (24, 8208, 512)]
 
 
 @pytest.mark.parametrize("m,n,k", A4W4_SHAPES)
@@ -152,7 +152,7 @@ def test_gemm_a4w4_full_size_spot_check(cuda):
 
 
 # ----------------------------------------------------------------------------- a8w4
-A8W4_SHAPES = [(1, 256, 512), (17, 512, 1024), (64, 7168, 2048), (100, 640, 512), (256, 1024, 2048)]
+A8W4_SHAPES = [(1, 256, 512), (17, 512, 1024), (64, 7168, 2048), (100, 640, 512), (256, 1024, 2048), (20, 8208, 512)]
 
 
 def _a8w4_case(m, n, k, seed=0):
