@@ -246,6 +246,11 @@ std::vector<Instance>& registry() {
         const Variant a8n{false, true, false};
         skinny(kA8W4, 1, false, a8n, launch_skinny<kFp8, 1, true, false, false, 2>, "a8w4", 32);
         skinny(kA8W4, 2, false, a8n, launch_skinny<kFp8, 2, true, false, false, 2>, "a8w4", 32);
+        const Variant b16p{false, true, false}, b16r{false, false, false};
+        skinny(kA16W16, 1, false, b16p, launch_skinny<kBf16, 1, true, false, false, 2>, "a16w16", 32);
+        skinny(kA16W16, 2, false, b16p, launch_skinny<kBf16, 2, true, false, false, 2>, "a16w16", 32);
+        skinny(kA16W16, 1, false, b16r, launch_skinny<kBf16, 1, false, false, false, 2>, "a16w16", 32);
+        skinny(kA16W16, 2, false, b16r, launch_skinny<kBf16, 2, false, false, false, 2>, "a16w16", 32);
     });
     return reg;
 }
