@@ -408,6 +408,10 @@ struct GemmCall {
     // and the strides (bytes; bias in elements) step to the next batch
     int batch = 1;
     int64_t bs_a = 0, bs_b = 0, bs_d = 0, bs_bias = 0;
+    // packed e2m1 output through the 256x256 persistent kernel's epilogue:
+    // `out` then describes [M, N] elements (row stride in elements) at the
+    // packed bytes, with a bf16 dtype tag; only mxfp4_gemm_asm sets it
+    bool out_fp4 = false;
 };
 
 void run_gemm(const GemmCall& c, hipStream_t stream) {
@@ -566,6 +570,15 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             AA_CHECK(twin, "no non-persistent twin of ", inst->name);
             inst = twin;
         }
+        if (c.out_fp4) {
+            AA_CHECK(inst->persistent && inst->fam == kA4W4 && inst->bm == 256 && inst->bn == 256 && c.var.b_pre &&
+                         !c.var.out_f32 && !p.bias && !batched,
+                     "packed-fp4 epilogue: only the 256x256 persistent A4W4 tile, no bias or batch");
+            gemm_flat_persist_kernel<kFp4, 256, false, true, true>
+                <<<dim3(std::min(tiles, cus), 1, 1), 256, 0, stream>>>(p);
+            AA_HIP(hipGetLastError());
+            return;
+        }
         inst->fn(p, dim3(inst->persistent ? std::min(tiles, cus) : tiles, 1, c.batch), stream);
     } else {
         // the skinny kernels split K in k-pairs (one scale dword each)
@@ -657,7 +670,9 @@ int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
 // (e2m1 with conversion scale 1; the reference's packed-fp4 kernel ignores the
 // input scales, op_tests/test_f4gemm.py:213-215, and so does this one: it runs
 // with unit scales), or fp8 [M, N] + out_scale (MXFP8, per-128-column e8m0 in
-// the packed layout).  The low-precision forms run the f32-output GEMM into a
+// the packed layout).  e2m1 output on shapes whose 256x256 tiles fill the CUs
+// (N % 32 == 0, no kernel named) is converted in the persistent kernel's
+// epilogue; the other low-precision forms run the f32-output GEMM into a
 // library-owned tile, then out_quant_kernel.
 int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA, aiter_tensor_t* ScaleB,
                    aiter_tensor_t* out, aiter_tensor_t* out_scale, const char* kernelName, int a_preshuffle,
@@ -726,11 +741,31 @@ int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
             sa = &usa;
             sb = &usb;
         }
+        const bool fill = ((M + 255) / 256) * ((N + 255) / 256) >= device_cu_count(A->device_id);
+        if (!fp8 && (!kernelName || !kernelName[0]) && fill && N % 32 == 0) {
+            // e2m1 straight from the persistent 256x256 kernel's epilogue: no
+            // f32 tile, no second pass
+            aiter_tensor_t o{};
+            o.ptr = out->ptr;
+            o.ndim = 2;
+            o.shape[0] = M;
+            o.shape[1] = N;
+            o.strides[0] = out_stride * 2;
+            o.strides[1] = 1;
+            o.numel = (size_t)(M * N);
+            o.dtype = AITER_DTYPE_bf16;   // tag only: the fp4 epilogue writes packed bytes
+            o.device_id = A->device_id;
+            GemmCall c{kA4W4, {false, true, false}, A, B, sa, sb, &o, nullptr, 1.0f, 0.0f,
+                       "a4w4_tile_256x256_persist", -1, -1};
+            c.out_fp4 = true;
+            run_gemm(c, st);
+            return;
+        }
         // f32 tile: the persistent 256x256 kernel when its tiles fill the CUs
         // (8192^3: 297 vs 338 us through the heuristic's 128x256 tile), else
         // the heuristic
         const char* kn = kernelName;
-        if ((!kn || !kn[0]) && ((M + 255) / 256) * ((N + 255) / 256) >= device_cu_count(A->device_id))
+        if ((!kn || !kn[0]) && fill)
             kn = "a4w4_tile_256x256_f32_persist";
         GemmCall c{kA4W4, {false, true, true}, A, B, sa, sb, &t, nullptr, 1.0f, 0.0f, kn, -1, -1};
         run_gemm(c, st);

@@ -40,7 +40,7 @@ struct FlatPersistCfg {
 };
 
 // BPRE = false: row-major B, loaded straight into VGPRs as in gemm_flat_kernel.
-template <int KA, int BM, bool OUT_F32, bool BPRE = true>
+template <int KA, int BM, bool OUT_F32, bool BPRE = true, bool OUT_FP4 = false>
 __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p) {
     using Cfg = FlatPersistCfg<KA, BM>;
     constexpr int NS = 4;
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     constexpr int NBL = NB * 4;
     constexpr int STAGE_BYTES = Cfg::STAGE_KB * 1024;
     constexpr int A_ROW_BYTES = 128 * FA;
-    constexpr int EB = OUT_F32 ? 4 : 2;
+    constexpr int EB2 = OUT_FP4 ? 1 : (OUT_F32 ? 8 : 4);   // output bytes per two elements
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES];
 
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     constexpr int LOADS_ITER = NDMA + NBL;
     constexpr int WAIT_N = (NS - 3) * LOADS_ITER + NDMA + 3 * NB;
     // epilogue store instructions per wave
-    constexpr int NST = BM * 64 * EB / 1024;
+    constexpr int NST = BM * 64 * EB2 / 2048;
     // the first two waits of a tile after an epilogue: the stores were issued
     // after the copies waited for and may stay outstanding
     constexpr int WAIT_T = (WAIT_N + NST) > 63 ? 63 : (WAIT_N + NST);
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     fence();
 
     // epilogue row tiles per pass: a quarter ring slot per wave
-    constexpr int EP_ROW_TILE = 32 * 64 * EB;
+    constexpr int EP_ROW_TILE = 32 * 32 * EB2;
     constexpr int EP_MP = (MA * EP_ROW_TILE <= STAGE_BYTES / 4)         ? MA
                           : ((MA / 2) * EP_ROW_TILE <= STAGE_BYTES / 4) ? MA / 2
                           : ((MA / 4) * EP_ROW_TILE <= STAGE_BYTES / 4) ? MA / 4
@@ -342,7 +342,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         // epilogue through ring slot 3: every wave finished reading it before
         // the last stage's barrier, and its next copy is issued in the next
         // tile's first stage, after the barrier below
-        store_block<MA, NB, EP_MP, false, true, OUT_F32, true>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
+        store_block<MA, NB, EP_MP, false, true, OUT_F32, true, OUT_FP4>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
                                                               lane, cm0, cn0 + wave * 64);
         wait_vmcnt_lgkm0<63>();
         asm volatile("" ::: "memory");

@@ -14,6 +14,7 @@
 // 256-element window, selected from a 32-bit register by op_sel (byte 0..3).
 #pragma once
 #include "gemm_kernels.h"
+#include "mx_quant.h"
 
 namespace aiter_amd {
 
@@ -82,12 +83,16 @@ AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f
 // bias reads are clamped into the bias tensor.  SCALED = false skips the
 // alpha multiply (alpha == 1, no bias).  FENCED = true converts one 32x32
 // block per scheduling region, for epilogues inside a loop where the other
-// live registers leave no room for all accumulator reads at once.
-template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false, bool FENCED = false>
+// live registers leave no room for all accumulator reads at once.  OUT_FP4
+// = true writes packed e2m1 (conversion scale 1, RNE, saturating: two values
+// per byte, the lower column in the low nibble; p.ldd still counts elements).
+template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false, bool FENCED = false,
+          bool OUT_FP4 = false>
 AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     static_assert(MA % MP == 0, "whole passes");
-    constexpr int EB = OUT_F32 ? 4 : 2;         // output bytes per element
-    constexpr int RB = 32 * NB * EB;            // bytes per block row
+    static_assert(!(OUT_FP4 && OUT_F32), "one output format");
+    constexpr int EB2 = OUT_FP4 ? 1 : (OUT_F32 ? 8 : 4);   // output bytes per two elements
+    constexpr int RB = 16 * NB * EB2;           // bytes per block row
     constexpr int P = RB / 16;                  // 16-byte pieces per row
     static_assert(P <= 64, "one row per read instruction at most");
     constexpr int SWM = (P < 8 ? P : 8) - 1;    // swizzle mask
@@ -97,10 +102,10 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
     // opaque copy of the lane index: keeps the compiler from hoisting this
     // epilogue's address arithmetic out of an enclosing loop
     asm volatile("" : "+v"(lane));
-    const __amdgpu_buffer_rsrc_t d_rsrc = make_rsrc(p.D, (int64_t)p.M * p.ldd * EB);
+    const __amdgpu_buffer_rsrc_t d_rsrc = make_rsrc(p.D, (int64_t)p.M * p.ldd * EB2 / 2);
     const int pc = lane % P;
-    const int n_out = nb + pc * (16 / EB);
-    const int col_off = n_out < p.N ? n_out * EB : 0x7fffffff;   // outside D when past N
+    const int n_out = nb + pc * (32 / EB2);
+    const int col_off = n_out < p.N ? n_out * EB2 / 2 : 0x7fffffff;   // outside D when past N
 #pragma unroll
     for (int i0 = 0; i0 < MA; i0 += MP) {
 #pragma unroll
@@ -124,9 +129,13 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
                     }
-                    const int byte = nl * EB;
+                    const int byte = nl * EB2 / 2;
                     const int piece = (byte >> 4) ^ ((r >> RSH) & SWM);
-                    if constexpr (OUT_F32) {
+                    if constexpr (OUT_FP4) {
+                        uint32_t w = mx::cvt_fp4_pair<float>(0u, 0u, v[0], v[1], 1.0f, 0);
+                        w = mx::cvt_fp4_pair<float>(w, 0u, v[2], v[3], 1.0f, 1);
+                        *reinterpret_cast<uint16_t*>(cb + r * RB + piece * 16 + (byte & 15)) = (uint16_t)w;
+                    } else if constexpr (OUT_F32) {
                         *reinterpret_cast<f32x4_t*>(cb + r * RB + piece * 16) = f32x4_t{v[0], v[1], v[2], v[3]};
                     } else {
                         *reinterpret_cast<u32x2_t*>(cb + r * RB + piece * 16 + (byte & 15)) =
@@ -141,7 +150,7 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
             const int r = rr + lane / P;
             const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
             const int m = mb + i0 * 32 + r;
-            const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * EB + col_off;
+            const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * EB2 / 2 + col_off;
             __builtin_amdgcn_raw_buffer_store_b128(v, d_rsrc, off, 0, 0);
         }
     }
