@@ -384,8 +384,9 @@ float* workspace(int dev, hipStream_t st, size_t bytes, int slot = 0) {
     if (w.bytes < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         AA_HIP(hipStreamIsCapturing(st, &cs));
-        AA_CHECK(cs == hipStreamCaptureStatusNone,
-                 "split-K workspace must be sized before graph capture (call gemm_workspace_reserve)");
+        AA_CHECK(cs == hipStreamCaptureStatusNone, "library workspace slot ", slot,
+                 " must be sized before graph capture (split-K: gemm_workspace_reserve; low-precision outputs: "
+                 "one eager call of the same shape)");
         if (w.ptr) {
             AA_HIP(hipStreamSynchronize(st));
             AA_HIP(hipFree(w.ptr));
