@@ -699,6 +699,7 @@ int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
                  "mxfp4_gemm_asm: out must be [M, ", fp8 ? "N" : "N/2", "]");
         const int64_t out_stride = out->ndim >= 2 ? out->strides[out->ndim - 2] : cols_2d(out);
         AA_CHECK(N % 8 == 0 && out_stride % 4 == 0, "mxfp4_gemm_asm: N must be a multiple of 8");
+        if (M == 0 || N == 0) return;
         if (fp8) {
             AA_CHECK(out_scale, "mxfp4_gemm_asm: MXFP8 output needs out_scale");
             AA_CHECK(N % 128 == 0 && M % 64 == 0, "mxfp4_gemm_asm: MXFP8 output needs N % 128 == 0 and M % 64 == 0");
