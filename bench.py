@@ -286,6 +286,15 @@ def bench_extra(dev):
                     "frac_bf16_peak": round(2 * m * n * k / t / 1e12 / PEAK_BF16, 4)}
     del a, b, bs
     out["bf16_cpu_plumbing"] = bf16_plumbing(dev)
+    # A4W4 prefill, the K=16384, N=2048 variant of BASELINE configs[2]
+    m, n, k = 8192, 2048, 16384
+    aq, as_, bq, bs_ = quantised_operands(m, n, k, 6, dev)
+    t = time_graph(lambda: aiter_amd.gemm_a4w4(aq, bq, as_, bs_), 20, 2)
+    cfg = aiter_amd.get_GEMM_config(m, n, k)
+    out["a4w4_8192x2048x16384"] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1),
+                                   "frac_mxfp4_peak": round(2 * m * n * k / t / 1e12 / PEAK_MXFP4, 4),
+                                   "kernel": str(cfg["kernelName"]) if cfg else "heuristic"}
+    del aq, as_, bq, bs_
     # MXFP8 x MXFP4 M=4096 N=7168 K=16384 (+ dynamic quant of the bf16 activation)
     m, n, k = 4096, 7168, 16384
     x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
