@@ -227,7 +227,8 @@ AA_DEV int64_t sorted_source_row(const SortQuant& s, int64_t x, int& valid) {
 }
 
 // fused quant + sort (csrc/kernels/quant_kernels.cu:1733-1880): RoundUp e8m0
-// from the running max 1e-10, one thread per (sorted position, 32-block)
+// from the running max 1e-10, one thread per (sorted position, 32-block);
+// workgroup (x, y) covers sorted positions 32x.. and scale columns 32y..
 template <typename InT, bool OUT_FP8>
 __global__ __launch_bounds__(256) void mx_quant_sorted_kernel(QuantParams p, SortQuant s) {
     const int64_t g0 = (int64_t)blockIdx.x * 32;
@@ -242,11 +243,15 @@ __global__ __launch_bounds__(256) void mx_quant_sorted_kernel(QuantParams p, Sor
         valid_of[threadIdx.x] = v;
     }
     __syncthreads();
-    const int items = 32 * p.scale_n_pad;
+    // columns split over gridDim.y in runs of 32 blocks: a few items per
+    // thread instead of a long serial loop at large K
+    const int y0 = blockIdx.y * 32;
+    const int ny = min(32, p.scale_n_pad - y0);
+    const int items = 32 * ny;
     for (int it = threadIdx.x; it < items; it += 256) {
-        const int xr = it / p.scale_n_pad;
+        const int xr = it / ny;
         const int64_t x = g0 + xr;
-        const int y = it % p.scale_n_pad;
+        const int y = y0 + it % ny;
         const int valid = valid_of[xr];
         const int64_t row = rows[xr];
         uint8_t* sc = p.scale + scale_shuffle_idx(p.scale_n_pad, (int)x, y);
@@ -517,7 +522,7 @@ int fused_dynamic_mx_quant_moe_sort_hip(aiter_tensor_t* out, aiter_tensor_t* sca
         s.sorted_rows = sorted_rows;
         s.token_num = token_num;
         s.topk = (int)(rows / token_num);
-        const dim3 grid((unsigned)(sorted_rows / 32));
+        const dim3 grid((unsigned)(sorted_rows / 32), (unsigned)((scale_n_pad + 31) / 32));
         hipStream_t st = reinterpret_cast<hipStream_t>(stream);
         if (in_dt == AITER_DTYPE_bf16) {
             if (fp8) mx_quant_sorted_kernel<uint16_t, true><<<grid, 256, 0, st>>>(p, s);
