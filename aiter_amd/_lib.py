@@ -12,6 +12,7 @@ no fallback: if the library is missing or cannot be loaded, every op raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 
@@ -116,6 +117,8 @@ SIGNATURES = {
     "batched_gemm_bf16_tune": ([_T] * 3 + [ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
     "aiter_amd_num_kernels": ([], ctypes.c_int),
     "aiter_amd_kernel_info": ([ctypes.c_int, ctypes.c_char_p, ctypes.c_int], ctypes.c_int),
+    "aiter_amd_resolve_kernel_name": ([ctypes.c_char_p] + [ctypes.c_int] * 4 + [ctypes.c_int64], ctypes.c_int),
+    "aiter_amd_resolve_opus_kid": ([ctypes.c_int, ctypes.c_int, ctypes.c_int64], ctypes.c_int),
     "gemm_workspace_reserve": ([ctypes.c_int, _S, ctypes.c_size_t], ctypes.c_int),
     "hbm_stream_read": ([_T, _T, ctypes.c_int, _S], ctypes.c_int),
 }
@@ -194,3 +197,9 @@ def kernel_table():
             out.append((int(f[0]), f[1], f[2], bool(int(f[3])), int(f[4]), int(f[5]),
                         bool(int(f[6])), bool(int(f[7])), bool(int(f[8])), bool(int(f[9]))))
     return out
+
+
+@functools.lru_cache(maxsize=1)
+def kernel_names() -> frozenset:
+    """Names of this library's kernel instances."""
+    return frozenset(row[1] for row in kernel_table())

@@ -339,19 +339,132 @@ const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int c
     return best;
 }
 
-// Reference kernel names (hsa/gfx950/f4gemm manifest, "..._<tM>x<tN>E") map to
-// the tile instance of the same shape when one exists.
-const Instance* map_reference_name(const std::string& nm, Family f, const Variant& v) {
-    const size_t e = nm.rfind('E');
-    const size_t u = nm.rfind('_');
-    if (u == std::string::npos || e == std::string::npos || e < u) return nullptr;
-    const std::string dims = nm.substr(u + 1, e - u - 1);
-    const size_t x = dims.find('x');
-    if (x == std::string::npos) return nullptr;
-    const int tm = atoi(dims.substr(0, x).c_str()), tn = atoi(dims.substr(x + 1).c_str());
-    for (auto& in : registry())
-        if (!in.skinny && variant_ok(in, f, v) && in.bm == tm && in.bn == tn) return &in;
+// The block tile a kernel of the reference is built for, read from its name.
+struct RefTile {
+    int tm = 0, tn = 0;
+    bool split = false;
+};
+
+// Parses "<a>x<b>[x<c>...]" starting at s[i]; returns the number of fields.
+int parse_dims(const std::string& s, size_t i, int* out, int max_fields) {
+    int n = 0;
+    while (n < max_fields && i < s.size() && isdigit((unsigned char)s[i])) {
+        int v = 0;
+        while (i < s.size() && isdigit((unsigned char)s[i])) v = v * 10 + (s[i++] - '0');
+        out[n++] = v;
+        if (i < s.size() && s[i] == 'x') ++i;
+        else break;
+    }
+    return n;
+}
+
+// Reference kernel names carry their tile:
+//  * ASM manifests (hsa/gfx950/f4gemm/f4gemm_bf16_per1x32Fp4.csv,
+//    hsa/gfx950/bf16gemm/*.csv): mangled "_ZN5aiter<len><stem>_<tM>x<tN>[_tags]E",
+//    split-K kernels tagged "splitk";
+//  * CK A4W4 instances (csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale_common.py:27-58):
+//    "a4w4_blockscale_<block>x<tM>x<tN>x<tK>_...".
+bool parse_reference_tile(const std::string& nm, RefTile* t) {
+    static const std::string ck = "a4w4_blockscale_";
+    if (nm.compare(0, ck.size(), ck) == 0) {
+        int d[4];
+        if (parse_dims(nm, ck.size(), d, 4) != 4 || d[1] <= 0 || d[2] <= 0) return false;
+        t->tm = d[1];
+        t->tn = d[2];
+        t->split = false;
+        return true;
+    }
+    if (nm.compare(0, 3, "_ZN") != 0 || nm.back() != 'E') return false;
+    // the first "_<digits>x<digits>" field after the namespace prefix
+    for (size_t i = nm.find('_', 3); i != std::string::npos && i + 1 < nm.size(); i = nm.find('_', i + 1)) {
+        int d[2];
+        if (parse_dims(nm, i + 1, d, 2) == 2 && d[0] > 0 && d[1] > 0) {
+            t->tm = d[0];
+            t->tn = d[1];
+            t->split = nm.find("splitk") != std::string::npos;
+            return true;
+        }
+    }
+    return false;
+}
+
+// opus a16w16 kernel ids (csrc/opus_gemm/opus_gemm_common.py:238-513): the
+// tile of each kid.  Offsets: +1000 no-OOB mirror, +2000/+3000/+4000 cache
+// policy variants of kids 4-9, +5000 the >4 GiB-safe form; 4-9 mfma tiles,
+// 200-223 flatmm split-K tiles, 300-315 persistent tiles, 1400-1404 mono
+// tiles.  Returns false for ids outside the gfx950 table.
+bool decode_opus_kid(int kid, RefTile* t) {
+    if (kid < 0 || kid >= 10000) return false;   // >= 10000: the gfx942 table
+    int k = kid >= 5000 ? kid - 5000 : kid;
+    static const int mono[5][2] = {{192, 256}, {128, 256}, {192, 128}, {128, 128}, {64, 128}};
+    if (k >= 1400 && k <= 1404) {
+        t->tm = mono[k - 1400][0];
+        t->tn = mono[k - 1400][1];
+        t->split = false;
+        return true;
+    }
+    if (k >= 2000) {
+        if (k % 1000 < 4 || k % 1000 > 9) return false;
+        k %= 1000;   // cache-policy variants (and their no-OOB mirrors) of kids 4-9
+    } else if (k >= 1000) {
+        k -= 1000;
+    }
+    static const int mfma[6][2] = {{128, 256}, {256, 128}, {128, 128}, {256, 128}, {128, 256}, {256, 256}};
+    static const int flat[24][2] = {{64, 64},  {32, 32}, {32, 32}, {32, 64}, {32, 128}, {64, 32},
+                                    {64, 32},  {128, 32}, {64, 64}, {256, 32}, {32, 256}, {32, 96},
+                                    {32, 96},  {32, 96}, {64, 96}, {64, 96}, {64, 96},  {96, 32},
+                                    {96, 32},  {96, 32}, {96, 64}, {96, 64}, {96, 64},  {96, 96}};
+    static const int pers[4][2] = {{256, 256}, {128, 256}, {256, 128}, {128, 128}};
+    if (k >= 4 && k <= 9) {
+        t->tm = mfma[k - 4][0];
+        t->tn = mfma[k - 4][1];
+        t->split = false;
+    } else if (k >= 200 && k <= 223) {
+        t->tm = flat[k - 200][0];
+        t->tn = flat[k - 200][1];
+        t->split = true;
+    } else if (k >= 300 && k <= 315) {
+        t->tm = pers[(k - 300) % 4][0];
+        t->tn = pers[(k - 300) % 4][1];
+        t->split = false;
+    } else {
+        return false;
+    }
+    return true;
+}
+
+// This library's instance for a reference tile: the one-tile kernel of the
+// same block shape (its split-K form for a split-K reference kernel) when
+// there is one and M is beyond the skinny range; otherwise nullptr, and the
+// caller takes its own heuristic choice for the shape (the reference's
+// tiles were tuned for the reference's kernels; a tile this library lacks is
+// not approximated by a neighbour).
+const Instance* reference_tile_instance(const RefTile& t, Family f, const Variant& v, int64_t M) {
+    if (M <= 32) return nullptr;
+    for (int pass = 0; pass < 2; ++pass) {
+        const bool want_split = pass == 0 ? t.split : false;
+        if (pass == 1 && !t.split) break;
+        for (auto& in : registry())
+            if (!in.skinny && !in.persistent && in.split == want_split && in.bm == t.tm && in.bn == t.tn &&
+                variant_ok(in, f, v))
+                return &in;
+    }
     return nullptr;
+}
+
+// A kernel name: this library's instance of that name (even when it does
+// not fit the call: the caller reports that), or for a reference kernel name
+// the instance reference_tile_instance picks (nullptr: the heuristic).
+// *known is false when the name is neither.
+const Instance* resolve_name(const std::string& nm, Family f, const Variant& v, int64_t M, bool* known) {
+    *known = true;
+    if (const Instance* in = find_by_name(nm)) return in;
+    RefTile t;
+    if (!parse_reference_tile(nm, &t)) {
+        *known = false;
+        return nullptr;
+    }
+    return reference_tile_instance(t, f, v, M);
 }
 
 __global__ __launch_bounds__(256) void fill_byte_kernel(uint8_t* p, int64_t n, int v) {
@@ -413,6 +526,8 @@ struct GemmCall {
     // `out` then describes [M, N] elements (row stride in elements) at the
     // packed bytes, with a bf16 dtype tag; only mxfp4_gemm_asm sets it
     bool out_fp4 = false;
+    // an opus kernel id of the reference, decoded to its tile (tm > 0)
+    RefTile ref_tile;
 };
 
 void run_gemm(const GemmCall& c, hipStream_t stream) {
@@ -513,9 +628,12 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         inst = find_by_id(c.kernel_id);
         AA_CHECK(inst && variant_ok(*inst, c.fam, c.var), "kernel id ", c.kernel_id, " does not fit this GEMM");
     } else if (c.kernel_name && c.kernel_name[0]) {
-        inst = find_by_name(c.kernel_name);
-        if (!inst) inst = map_reference_name(c.kernel_name, c.fam, c.var);
-        AA_CHECK(inst && variant_ok(*inst, c.fam, c.var), "unknown kernel name '", c.kernel_name, "'");
+        bool known = false;
+        inst = resolve_name(c.kernel_name, c.fam, c.var, M, &known);
+        AA_CHECK(known, "unknown kernel name '", c.kernel_name, "'");
+        if (inst) AA_CHECK(variant_ok(*inst, c.fam, c.var), "kernel '", c.kernel_name, "' does not fit this GEMM");
+    } else if (c.ref_tile.tm > 0) {
+        inst = reference_tile_instance(c.ref_tile, c.fam, c.var, M);
     }
     const int ksteps = (int)(K / (scaled ? 128 : 32));
     if (!inst) {
@@ -706,18 +824,6 @@ int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
             AA_CHECK(is_byte_type(out_scale->dtype) && (int64_t)out_scale->numel >= M * (N / 128),
                      "mxfp4_gemm_asm: out_scale must hold M * N / 128 e8m0 bytes");
         }
-        // f32 tile
-        float* tile = workspace(A->device_id, st, (size_t)M * N * sizeof(float), 1);
-        aiter_tensor_t t{};
-        t.ptr = tile;
-        t.numel = (size_t)(M * N);
-        t.ndim = 2;
-        t.shape[0] = M;
-        t.shape[1] = N;
-        t.strides[0] = N;
-        t.strides[1] = 1;
-        t.dtype = AITER_DTYPE_fp32;
-        t.device_id = A->device_id;
         aiter_tensor_t usa{}, usb{};
         const aiter_tensor_t *sa = ScaleA, *sb = ScaleB;
         if (!fp8) {
@@ -763,6 +869,18 @@ int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
             run_gemm(c, st);
             return;
         }
+        // f32 tile (library workspace), then the output quant
+        float* tile = workspace(A->device_id, st, (size_t)M * N * sizeof(float), 1);
+        aiter_tensor_t t{};
+        t.ptr = tile;
+        t.numel = (size_t)(M * N);
+        t.ndim = 2;
+        t.shape[0] = M;
+        t.shape[1] = N;
+        t.strides[0] = N;
+        t.strides[1] = 1;
+        t.dtype = AITER_DTYPE_fp32;
+        t.device_id = A->device_id;
         // f32 tile: the persistent 256x256 kernel when its tiles fill the CUs
         // (8192^3: 297 vs 338 us through the heuristic's 128x256 tile), else
         // the heuristic
@@ -833,8 +951,10 @@ int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
 // with gridDim.z = b: the 2-D descriptors of batch 0 plus batch strides (any
 // strides with unit last-dimension stride, e.g. the reference test's [m, b, k]
 // transposed layout)
+// kernelId: with opus_kid an opus kernel id of the reference (decoded to its
+// tile, decode_opus_kid), else an id of this library's table; < 0 heuristic.
 static void opus_batched(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y, aiter_tensor_t* bias,
-                         int kernelId, int splitK, hipStream_t st) {
+                         int kernelId, int splitK, hipStream_t st, bool opus_kid = false) {
     check_tensor(XQ, "XQ", 2);
     check_tensor(WQ, "WQ", 2);
     check_tensor(Y, "Y", 2);
@@ -871,7 +991,10 @@ static void opus_batched(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t*
         bptr = &bb;
     }
     GemmCall c{kA16W16, {false, false, Y->dtype == AITER_DTYPE_fp32}, &a, &w, nullptr, nullptr, &y, bptr,
-               1.0f, 1.0f, nullptr, kernelId, splitK > 0 ? splitK : -1};
+               1.0f, 1.0f, nullptr, opus_kid ? -1 : kernelId, splitK > 0 ? splitK : -1};
+    if (opus_kid && kernelId >= 0)
+        AA_CHECK(decode_opus_kid(kernelId, &c.ref_tile), "unknown opus kernel id ", kernelId,
+                 " (not in the gfx950 opus table)");
     if (batch > 1) {
         c.batch = (int)batch;
         c.bs_a = XQ->strides[0] * 2;
@@ -894,7 +1017,7 @@ int opus_gemm_a16w16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t
                           aiter_tensor_t* bias, int kernelId, int splitK, aiter_stream_t stream) {
     return safe_call([&] {
         DeviceGuard g(XQ ? XQ->device_id : -1);
-        opus_batched(XQ, WQ, Y, bias, kernelId, splitK, reinterpret_cast<hipStream_t>(stream));
+        opus_batched(XQ, WQ, Y, bias, kernelId, splitK, reinterpret_cast<hipStream_t>(stream), true);
     });
 }
 
@@ -933,6 +1056,20 @@ int aiter_amd_kernel_info(int id, char* buf, int buflen) {
              (int)in->skinny, in->bm, in->bn, (int)in->split, (int)in->var.a_pre, (int)in->var.b_pre,
              (int)in->var.out_f32);
     return 0;
+}
+
+int aiter_amd_resolve_kernel_name(const char* name, int family, int a_pre, int b_pre, int out_f32, int64_t M) {
+    if (!name || !name[0] || family < 0 || family > 2) return -2;
+    bool known = false;
+    const Instance* in = resolve_name(name, (Family)family, Variant{a_pre != 0, b_pre != 0, out_f32 != 0}, M, &known);
+    return !known ? -2 : (in ? in->id : -1);
+}
+
+int aiter_amd_resolve_opus_kid(int kid, int out_f32, int64_t M) {
+    RefTile t;
+    if (!decode_opus_kid(kid, &t)) return -2;
+    const Instance* in = reference_tile_instance(t, kA16W16, Variant{false, false, out_f32 != 0}, M);
+    return in ? in->id : -1;
 }
 
 // Pre-size the split-K workspace of (device, stream) before graph capture.

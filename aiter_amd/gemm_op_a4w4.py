@@ -83,9 +83,41 @@ def gemm_a4w4(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, bias: Tens
     if cfg is not None:
         split_k = int(cfg.get("splitK", 0) or 0)
         kernel_name = str(cfg["kernelName"])
-    gemm_a4w4_asm(A.view(m, k // 2), B, A_scale, B_scale, out, kernel_name, bias, alpha, beta,
-                  bpreshuffle, log2_k_split=split_k)
+        if kernel_name in _UNRESOLVED_NAMES:
+            kernel_name = ""
+    try:
+        if kernel_name and "_ZN" not in kernel_name and not _is_library_name(kernel_name):
+            # a CK instance row: the reference sends every non-ASM name to the
+            # CK entry, which takes no bias/alpha/beta (aiter/ops/gemm_op_a4w4.py:207-221)
+            return gemm_a4w4_blockscale(A.view(m, k // 2), B, A_scale, B_scale, out, splitK=split_k,
+                                        kernelName=kernel_name)[:m].view(*A.shape[:-1], n)
+        gemm_a4w4_asm(A.view(m, k // 2), B, A_scale, B_scale, out, kernel_name, bias, alpha, beta,
+                      bpreshuffle, log2_k_split=split_k)
+    except RuntimeError as e:
+        if not kernel_name or "unknown kernel name" not in str(e):
+            raise
+        _warn_unresolved(kernel_name, m, n, k)
+        gemm_a4w4_asm(A.view(m, k // 2), B, A_scale, B_scale, out, "", bias, alpha, beta, bpreshuffle,
+                      log2_k_split=0)
     return out[:m].view(*A.shape[:-1], n)
+
+
+# names read from a tuned CSV that name no kernel of this library or of the
+# reference: warned about once, then served by the heuristic
+_UNRESOLVED_NAMES: set = set()
+
+
+def _warn_unresolved(name: str, m: int, n: int, k: int) -> None:
+    if name not in _UNRESOLVED_NAMES:
+        _UNRESOLVED_NAMES.add(name)
+        logger.warning(f"tuned kernel '{name}' (shape M:{m} N:{n} K:{k}) is not a kernel of this library or a "
+                       f"reference tile name; using the heuristic choice")
+
+
+def _is_library_name(name: str) -> bool:
+    from ._lib import kernel_names
+
+    return name in kernel_names()
 
 
 def gemm_a4w4_asm(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, out: Tensor,
@@ -94,9 +126,10 @@ def gemm_a4w4_asm(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, out: T
                   log2_k_split: int | None = None) -> Tensor:
     """ctypes entry (aiter/ops/gemm_op_a4w4.py:241-287 ->
     csrc/py_itfs_cu/asm_gemm_a4w4.cu:158-278).  ``kernelName`` is one of this
-    library's kernel names, or a reference ASM name whose ``_<tM>x<tN>E``
-    tile maps onto the same tile here; empty selects the heuristic.
-    D = alpha * A B^T + beta * bias."""
+    library's kernel names, or a reference ASM name
+    (``_ZN5aiter..._<tM>x<tN>E``): the same tile here when this library has it
+    and M > 32, else the heuristic choice; empty selects the heuristic; any
+    other name raises.  D = alpha * A B^T + beta * bias."""
     call("gemm_a4w4_asm", A, B, A_scale, B_scale, out, kernelName if kernelName else None, bias,
          float(alpha if alpha is not None else 1.0), float(beta if beta is not None else 0.0),
          int(bpreshuffle) if bpreshuffle is not None else 1,
@@ -107,8 +140,12 @@ def gemm_a4w4_asm(A: Tensor, B: Tensor, A_scale: Tensor, B_scale: Tensor, out: T
 def gemm_a4w4_blockscale(XQ: Tensor, WQ: Tensor, x_scale: Tensor, w_scale: Tensor, Out: Tensor,
                          splitK: int = 0, kernelName: str = "") -> Tensor:
     """CK-instance entry (csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale.cu:69-93).
-    A kernel name of this library selects that instance; other names use the
-    heuristic choice (as the reference's empty-name default)."""
+    ``splitK`` is log2 of the K split (KBatch = 2^splitK).  A kernel name of
+    this library selects that instance; a CK instance name
+    (``a4w4_blockscale_<block>x<tM>x<tN>x<tK>_...``) the tile of the same
+    block shape here, or the heuristic choice when this library has no such
+    tile; an empty name the heuristic.  Other names raise, as in the
+    reference."""
     from ._lib import kernel_table
 
     kid = -1
@@ -116,6 +153,11 @@ def gemm_a4w4_blockscale(XQ: Tensor, WQ: Tensor, x_scale: Tensor, w_scale: Tenso
         for row in kernel_table():
             if row[1] == kernelName:
                 kid = row[0]
+        if kid < 0:
+            # resolved by name in the library (B preshuffled, no bias)
+            call("gemm_a4w4_asm", XQ, WQ, x_scale, w_scale, Out, kernelName, None, 1.0, 0.0, 1,
+                 int(splitK) if splitK else 0)
+            return Out
     call("gemm_a4w4_blockscale", XQ, WQ, x_scale, w_scale, Out, int(splitK), int(kid))
     return Out
 

@@ -2,12 +2,19 @@
 
 ``gemm_a16w16(A, B, bias, otype)`` computes ``A @ B.T (+ bias)``.  The CSV row
 keyed (gfx, cu_num, padded M, N, K, bias, dtype, outdtype, scaleAB,
-bpreshuffle) names a backend ``libtype`` and solution; this library's own
-rows use libtype ``aiter_amd`` with ``solidx`` = kernel id of
-libaiter_amd.so.  Rows of the reference's backends (asm / opus / flydsl /
-triton / skinny / hipblaslt / torch) are served by this library's heuristic
-choice, since those kernels are not part of it.  Scaled bf16 (scale_a /
-scale_b) is out of scope and rejected.
+bpreshuffle) names a backend ``libtype`` and solution (the reference's
+``solMap``, aiter/tuned_gemm.py:672-680):
+
+* ``aiter_amd``: ``solidx`` = kernel id of libaiter_amd.so (this library's
+  tuner writes these rows);
+* ``asm``: a reference ASM ``kernelName`` (``..._tn_<tM>x<tN>...E``) and
+  ``splitK``: the same tile here when there is one, else the heuristic;
+* ``opus``: ``solidx`` = a reference opus kernel id, decoded to its tile the
+  same way (csrc/opus_gemm/opus_gemm_common.py:238-513);
+* ``torch`` / ``hipblaslt`` / ``skinny`` / ``triton`` / ``flydsl``: backends
+  that are not part of this library; the heuristic choice serves them.
+
+Scaled bf16 (scale_a / scale_b) is out of scope and rejected.
 """
 from __future__ import annotations
 
@@ -52,11 +59,20 @@ def get_GEMM_A16W16_config(M: int, N: int, K: int, bias: bool, dtype: str, otype
 def _run(inp: Tensor, B: Tensor, bias: Tensor | None, otype: torch.dtype, bpreshuffle: bool, config) -> Tensor:
     m, n = inp.shape[0], B.shape[0]
     out = torch.empty((m, n), dtype=otype if otype == torch.float32 else dtypes.bf16, device=inp.device)
-    kid = int(config.get("solidx", -1)) if config.get("libtype") == "aiter_amd" else -1
-    name = str(config.get("kernelName", "")) if kid >= 0 else ""
-    split = int(config.get("splitK", 0) or 0) if kid >= 0 else 0
+    libtype = config.get("libtype")
     if bias is not None and bias.dtype != torch.float32:
         bias = bias.float()
+    split = int(config.get("splitK", 0) or 0)
+    if libtype == "opus" and not bpreshuffle:
+        call("opus_gemm_a16w16_tune", inp.unsqueeze(0), B.unsqueeze(0), out.unsqueeze(0), bias,
+             int(config.get("solidx", -1)), split)
+        return out
+    if libtype == "aiter_amd" and int(config.get("solidx", -1)) >= 0:
+        name = str(config.get("kernelName", ""))
+    elif libtype == "asm":
+        name = str(config.get("kernelName", "") or "")
+    else:
+        name, split = "", 0
     call("gemm_a16w16_asm", inp, B, out, torch.empty(0, dtype=torch.uint32, device=inp.device), bias,
          split, name or None, int(bpreshuffle))
     return out

@@ -69,9 +69,12 @@ int getPaddedM(int M, int N, int K, int gl);
  * shuffle_weight layout (16,16)) or row-major (bpreshuffle=0);
  * A_scale [>=pad32(M), >=K/32] / B_scale [>=pad32(N), >=K/32] e8m0 in the
  * shuffled MFMA layout; out [>=M, N] bf16 (aiter allocates pad32(M) rows);
- * bias optional f32 [N], [1,N] or [M,N].  kernelName selects a kernel id
- * from this library's table ("" or NULL = heuristic); log2_k_split < 0 lets
- * the heuristic choose the split-K factor. */
+ * bias optional f32 [N], [1,N] or [M,N].  kernelName: a name from this
+ * library's table; or a reference kernel name (ASM "_ZN5aiter..._<tM>x<tN>E",
+ * CK "a4w4_blockscale_<block>x<tM>x<tN>x<tK>_..."), which runs the tile of
+ * the same shape here when there is one and M > 32, else the heuristic
+ * choice; "" or NULL = heuristic; any other name is an error.
+ * log2_k_split <= 0 lets the heuristic choose the split-K factor. */
 int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
                   aiter_tensor_t* B_scale, aiter_tensor_t* out, const char* kernelName,
                   aiter_tensor_t* bias, float alpha, float beta, int bpreshuffle,
@@ -105,7 +108,11 @@ int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
 
 /* ---- opus a16w16: csrc/opus_gemm/opus_gemm.cu:133-209 (heuristic) and
  * :294-350 (explicit kernel id).  XQ [b,M,K], WQ [b,N,K] bf16, Y [b,M,N]
- * bf16 or f32, bias f32 [N] or [b,N] or NULL. */
+ * bf16 or f32, bias f32 [N] or [b,N] or NULL.  kernelId is a reference opus
+ * kid (csrc/opus_gemm/opus_gemm_common.py:238-513: 4-9, 200-223, 300-315,
+ * 1400-1404 and their +1000 / +2000..+4000 / +5000 variants): the kernel of
+ * the same tile here when there is one and M > 32, else the heuristic
+ * choice; ids outside the gfx950 table are an error; < 0 = heuristic. */
 int opus_gemm(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
               aiter_tensor_t* bias, aiter_stream_t stream);
 int opus_gemm_a16w16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
@@ -253,6 +260,18 @@ int moe_sum(aiter_tensor_t* input, aiter_tensor_t* output, aiter_stream_t stream
  * "id,name,family,skinny,bm,bn,split,a_pre,b_pre,out_f32" (0 or -1). */
 int aiter_amd_num_kernels(void);
 int aiter_amd_kernel_info(int id, char* buf, int buflen);
+
+/* Tuned-CSV name resolution, the lookup gemm_a4w4_asm / gemm_a16w16_asm /
+ * mxfp8_mxfp4_gemm_asm apply to kernelName (the reference resolves names in
+ * its dispatch maps, csrc/py_itfs_cu/asm_gemm_a4w4.cu:221-263 and
+ * csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale.cu:28-62), for an
+ * M-row GEMM of family 0 (a4w4), 1 (a8w4) or 2 (a16w16) with the given
+ * layout flags: returns the kernel id, -1 for the heuristic choice, -2 for a
+ * name that is neither this library's nor a reference kernel name.
+ * aiter_amd_resolve_opus_kid does the same for a reference opus kernel id
+ * (row-major B).  No GPU call. */
+int aiter_amd_resolve_kernel_name(const char* name, int family, int a_pre, int b_pre, int out_f32, int64_t M);
+int aiter_amd_resolve_opus_kid(int kid, int out_f32, int64_t M);
 
 /* Pre-sizes the split-K fp32 workspace owned by (device, stream) to at least
  * `bytes`, so that a later HIP-graph capture never needs to allocate.  The

@@ -143,3 +143,105 @@ def test_tuner_candidates_respect_shape():
     big = tuner.candidates("a4w4", 4096)
     assert all("skinny" not in n for _, n, _ in big)
     assert any(n == "a4w4_tile_256x256" for _, n, _ in big)
+
+
+# ---------------------------------------------------------------- reference kernel names
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _lines(name):
+    with open(os.path.join(GOLDEN, name)) as f:
+        return [l.strip() for l in f if l.strip()]
+
+
+def _resolve(name, fam=0, m=4096, b_pre=1, out_f32=0):
+    from aiter_amd._lib import lib
+
+    return lib().aiter_amd_resolve_kernel_name(name.encode(), fam, 0, b_pre, out_f32, m)
+
+
+def test_every_reference_a4w4_kernel_name_resolves():
+    """All 43 kernel names of the reference's a4w4_blockscale_tuned_gemm.csv
+    (ASM tiles and CK instances; list in tests/golden) resolve without error:
+    to the tile of the same shape here, else to the heuristic (-1)."""
+    from aiter_amd._lib import kernel_table
+
+    table = {r[0]: r for r in kernel_table()}
+    names = _lines("reference_a4w4_kernel_names.txt")
+    assert len(names) == 43
+    for nm in names:
+        for m in (1, 32, 33, 4096):
+            kid = _resolve(nm, m=m)
+            assert kid >= -1, (nm, m)
+            if m <= 32:
+                assert kid == -1, (nm, m)   # small M: this library's skinny kernels via the heuristic
+            if kid >= 0:
+                row = table[kid]
+                assert row[2] == "a4w4" and not row[3] and row[8], (nm, row)
+    # tiles this library has map to them exactly, others to the heuristic
+    assert table[_resolve("_ZN5aiter42f4gemm_bf16_per1x32Fp4_BpreShuffle_256x256E")][1] == "a4w4_tile_256x256"
+    assert table[_resolve("_ZN5aiter41f4gemm_bf16_per1x32Fp4_BpreShuffle_64x128E")][1] == "a4w4_tile_64x128"
+    assert _resolve("_ZN5aiter42f4gemm_bf16_per1x32Fp4_BpreShuffle_160x256E") == -1
+    ck = "a4w4_blockscale_256x128x256x128_16x16_16x16_8x32x1_8x32x1_1x32x1x8_8_2x2_intrawave_v3"
+    assert table[_resolve(ck)][1] == "a4w4_tile_128x256"
+    assert _resolve("a4w4_blockscale_256x96x384x128_16x16_16x16_8x32x1_8x32x1_1x32x1x8_8_2x2_intrawave_v3") == -1
+    # row-major B: the no-preshuffle reference kernel
+    nm = "_ZN5aiter44f4gemm_bf16_per1x32Fp4_noBpreShuffle_256x256E"
+    assert table[_resolve(nm, b_pre=0)][1] == "a4w4_tile_256x256_bplain"
+
+
+def test_library_and_unknown_names():
+    from aiter_amd._lib import kernel_table
+
+    for row in kernel_table()[:20]:
+        assert _resolve(row[1]) == row[0]
+    for bad in ("not_a_kernel", "_ZN5aiter3fooE", "a4w4_blockscale_garbage", "_ZN5aiter_12x34"):
+        assert _resolve(bad) == -2, bad
+
+
+def test_reference_bf16_asm_names_resolve():
+    from aiter_amd._lib import kernel_table
+
+    table = {r[0]: r for r in kernel_table()}
+    for nm in _lines("reference_bf16_asm_names.txt"):
+        for m in (1, 64, 8192):
+            kid = _resolve(nm, fam=2, m=m, b_pre=0)
+            assert kid >= -1, (nm, m)
+            if kid >= 0:
+                assert table[kid][2] == "a16w16" and not table[kid][8]
+    big = _resolve("_ZN5aiter24bf16gemm_bf16_tn_256x256E", fam=2, m=8192, b_pre=0)
+    assert table[big][1] == "a16w16_tile_256x256_bplain"
+    sk = _resolve("_ZN5aiter39bf16gemm_fp32bf16_tn_64x64_splitk_cleanE", fam=2, m=64, b_pre=0)
+    assert table[sk][1] == "a16w16_tile_64x64_splitk_bplain"
+
+
+def test_reference_opus_kids_resolve():
+    """Every gfx950 opus kid in the reference's bf16 tuned CSVs decodes; 6401
+    (mono tile 128x256, >4 GiB-safe) and 300 (persistent 256x256) land on the
+    same tiles here; gfx942 ids (>= 10000) and removed ids are errors."""
+    from aiter_amd._lib import kernel_table, lib
+
+    table = {r[0]: r for r in kernel_table()}
+    kids = [int(x) for x in _lines("reference_opus_kids.txt")]
+    assert 6401 in kids and len(kids) == 35
+    for kid in kids:
+        for m in (1, 2048):
+            r = lib().aiter_amd_resolve_opus_kid(kid, 0, m)
+            assert r >= -1, kid
+            if m == 1:
+                assert r == -1
+    assert table[lib().aiter_amd_resolve_opus_kid(6401, 0, 2048)][1] == "a16w16_tile_128x256_bplain"
+    assert table[lib().aiter_amd_resolve_opus_kid(300, 0, 8192)][1] == "a16w16_tile_256x256_bplain"
+    assert table[lib().aiter_amd_resolve_opus_kid(200, 1, 256)][1] == "a16w16_tile_64x64_splitk_bplain_f32"
+    for bad in (3, 100, 1100, 10000, 10300, -5):
+        assert lib().aiter_amd_resolve_opus_kid(bad, 0, 1024) == -2, bad
+
+
+def test_reference_row_fixture_routes(gfx950, monkeypatch):
+    """The reference-CSV fixture merges and its rows look up like any other."""
+    p = os.path.join(GOLDEN, "reference_a4w4_rows.csv")
+    monkeypatch.setenv("AITER_CONFIG_GEMM_A4W4", p)
+    _clear()
+    assert "_ZN" in aiter_amd.get_GEMM_config(1, 4096, 4096)["kernelName"]
+    assert aiter_amd.get_GEMM_config(2048, 7168, 2048)["kernelName"].startswith("a4w4_blockscale_")
+    assert aiter_amd.get_GEMM_config(96, 1024, 512)["kernelName"] == "not_a_kernel_of_anyone"
