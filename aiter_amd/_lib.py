@@ -92,6 +92,9 @@ SIGNATURES = {
     "gemm_a4w4_asm": ([_T, _T, _T, _T, _T, ctypes.c_char_p, _T, ctypes.c_float, ctypes.c_float,
                        ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
     "gemm_a4w4_blockscale": ([_T, _T, _T, _T, _T, ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
+    "gemm_a4w4_asm_noalloc": ([_T, _T, _T, _T, _T, ctypes.c_char_p, _T, ctypes.c_float, ctypes.c_float,
+                               ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
+    "gemm_a4w4_noalloc_scratch_bytes": ([], ctypes.c_size_t),
     "mxfp8_mxfp4_gemm_asm": ([_T, _T, _T, _T, _T, ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
     "gemm_a16w16_asm": ([_T, _T, _T, _T, _T, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
     "opus_gemm": ([_T, _T, _T, _T, _S], ctypes.c_int),

@@ -528,7 +528,22 @@ struct GemmCall {
     bool out_fp4 = false;
     // an opus kernel id of the reference, decoded to its tile (tm > 0)
     RefTile ref_tile;
+    // caller-free scratch (gemm_a4w4_asm_noalloc): used instead of the
+    // library workspace for split-K partials; nothing is allocated
+    void* scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
+
+// split-K partial buffer of a call: the call's scratch when it brings one
+// (never grown: too small is an error), else the (device, stream) workspace
+float* split_buffer(const GemmCall& c, int dev, hipStream_t st, size_t need) {
+    if (c.scratch) {
+        AA_CHECK(need <= c.scratch_bytes, "split-K partials need ", need, " bytes, more than the ", c.scratch_bytes,
+                 "-byte scratch of the no-allocation entry point");
+        return static_cast<float*>(c.scratch);
+    }
+    return workspace(dev, st, need);
+}
 
 void run_gemm(const GemmCall& c, hipStream_t stream) {
     check_tensor(c.A, "A", 2);
@@ -660,7 +675,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             sp = (nst + p.k_steps_per_split - 1) / p.k_steps_per_split;
             if (sp > 1) {
                 const size_t need = (size_t)sp * M * N * sizeof(float);
-                p.ws = workspace(dev, stream, need);
+                p.ws = split_buffer(c, dev, stream, need);
                 inst->fn(p, dim3(tiles, sp), stream);
                 const unsigned blocks = (unsigned)(((int64_t)M * N / 4 + 255) / 256);
                 if (c.var.out_f32)
@@ -708,7 +723,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         const dim3 grid((unsigned)((N + inst->bn - 1) / inst->bn), (unsigned)splits);
         if (inst->split && splits > 1) {
             const size_t need = (size_t)M * N * sizeof(float);
-            p.ws = workspace(dev, stream, need);
+            p.ws = split_buffer(c, dev, stream, need);
             const int64_t n4 = (int64_t)M * N;
             fill_zero_kernel<><<<dim3((unsigned)((n4 / 4 + 255) / 256 + 1)), 256, 0, stream>>>(p.ws, n4);
             inst->fn(p, grid, stream);
@@ -731,6 +746,27 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         }
     }
     AA_HIP(hipGetLastError());
+}
+
+// ---- fixed scratch of the no-allocation entry point ----------------------
+// One array per GPU, allocated with the code object when the library loads
+// on that device; host code reaches it only through the device address
+// hipGetSymbolAddress returns (the array's name is a host-side stand-in).
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// device address of `scratch` on `dev` (current device), looked up once
+void* scratch_address(int dev) {
+    static std::mutex mu;
+    static std::map<int, void*> addr;
+    std::lock_guard<std::mutex> lk(mu);
+    auto it = addr.find(dev);
+    if (it != addr.end()) return it->second;
+    void* ptr = nullptr;
+    AA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    AA_CHECK(ptr, "no device address for the scratch array");
+    addr[dev] = ptr;
+    return ptr;
 }
 
 }  // namespace
@@ -783,6 +819,30 @@ int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
         run_gemm(c, reinterpret_cast<hipStream_t>(stream));
     });
 }
+
+// gemm_a4w4_asm without any allocation: split-K partials go to the fixed
+// per-GPU `scratch` array (kNoAllocScratchBytes), never to the library
+// workspace; a call whose partials need more raises.  The array is shared by
+// every call on the GPU and keeps the previous call's contents: the split
+// kernels clear what they accumulate into with a fill kernel first, and
+// calls that overlap on one GPU (two streams, two threads) race.
+int gemm_a4w4_asm_noalloc(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale, aiter_tensor_t* B_scale,
+                          aiter_tensor_t* out, const char* kernelName, aiter_tensor_t* bias, float alpha, float beta,
+                          int bpreshuffle, int log2_k_split, aiter_stream_t stream) {
+    return safe_call([&] {
+        AA_CHECK(A, "A is NULL");
+        DeviceGuard g(A->device_id);
+        int dev = A->device_id;
+        if (dev < 0) AA_HIP(hipGetDevice(&dev));
+        GemmCall c{kA4W4, {false, bpreshuffle != 0, false}, A, B, A_scale, B_scale, out, bias,
+                   alpha, beta, kernelName, -1, log2_k_split > 0 ? log2_k_split : -1};
+        c.scratch = scratch_address(dev);
+        c.scratch_bytes = kNoAllocScratchBytes;
+        run_gemm(c, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+size_t gemm_a4w4_noalloc_scratch_bytes(void) { return kNoAllocScratchBytes; }
 
 // gfx1250 f4gemm entry (aiter/ops/gemm_op_a4w4.py:290-304, dispatch :80-124):
 // the output dtype picks the form: bf16 [M, N] (gemm_a4w4), fp4x2 [M, N/2]

@@ -80,6 +80,21 @@ int gemm_a4w4_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
                   aiter_tensor_t* bias, float alpha, float beta, int bpreshuffle,
                   int log2_k_split, aiter_stream_t stream);
 
+/* ---- A4W4 without allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments and
+ * result as gemm_a4w4_asm; split-K partials go to a fixed per-GPU scratch
+ * array of gemm_a4w4_noalloc_scratch_bytes() bytes (32 MiB) that the
+ * library holds until the process ends, instead of the library workspace.
+ * A call whose partials need more is an error; nothing is ever allocated.
+ * Every call on a GPU shares that GPU's array, so calls that overlap on one
+ * GPU (two streams or threads at once) race. */
+int gemm_a4w4_asm_noalloc(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* A_scale,
+                          aiter_tensor_t* B_scale, aiter_tensor_t* out, const char* kernelName,
+                          aiter_tensor_t* bias, float alpha, float beta, int bpreshuffle,
+                          int log2_k_split, aiter_stream_t stream);
+size_t gemm_a4w4_noalloc_scratch_bytes(void);
+
 /* ---- A4W4 blockscale (the CK-instance entry):
  * csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale.cu:69-93 and the tune
  * entry csrc/ck_gemm_a4w4_blockscale/gemm_a4w4_blockscale_tune.cu:58-90.
