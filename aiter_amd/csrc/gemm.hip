@@ -78,7 +78,10 @@ void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
 
 template <int KA, int BM, bool OF = false, bool BP = true>
 void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
+    if (p.alpha == 1.0f)
+        gemm_flat_persist_kernel<KA, BM, OF, BP, false, false><<<grid, 256, 0, s>>>(p);
+    else
+        gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
@@ -708,7 +711,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             AA_CHECK(inst->persistent && inst->fam == kA4W4 && inst->bm == 256 && inst->bn == 256 && c.var.b_pre &&
                          !c.var.out_f32 && !p.bias && !batched,
                      "packed-fp4 epilogue: only the 256x256 persistent A4W4 tile, no bias or batch");
-            gemm_flat_persist_kernel<kFp4, 256, false, true, true>
+            gemm_flat_persist_kernel<kFp4, 256, false, true, true, false>
                 <<<dim3(std::min(tiles, cus), 1, 1), 256, 0, stream>>>(p);
             AA_HIP(hipGetLastError());
             return;

@@ -40,7 +40,8 @@ struct FlatPersistCfg {
 };
 
 // BPRE = false: row-major B, loaded straight into VGPRs as in gemm_flat_kernel.
-template <int KA, int BM, bool OUT_F32, bool BPRE = true, bool OUT_FP4 = false>
+// SCALED = false: alpha == 1 (the epilogue skips the multiply).
+template <int KA, int BM, bool OUT_F32, bool BPRE = true, bool OUT_FP4 = false, bool SCALED = true>
 __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p) {
     using Cfg = FlatPersistCfg<KA, BM>;
     constexpr int NS = 4;
@@ -342,7 +343,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         // epilogue through ring slot 3: every wave finished reading it before
         // the last stage's barrier, and its next copy is issued in the next
         // tile's first stage, after the barrier below
-        store_block<MA, NB, EP_MP, false, true, OUT_F32, true, OUT_FP4>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
+        store_block<MA, NB, EP_MP, false, SCALED, OUT_F32, true, OUT_FP4>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
                                                               lane, cm0, cn0 + wave * 64);
         wait_vmcnt_lgkm0<63>();
         asm volatile("" ::: "memory");

@@ -15,13 +15,19 @@ Also reported on the same JSON line:
 * ``decode``: the bandwidth-bound configs[1] (M in {1,8,16,32,64}, N=7168,
   K=2048), cold-cache (B/scales rotated over >512 MiB) and warm, GB/s incl.
   scales and % of 8 TB/s;
-* ``extra``: bf16 A16W16 8192x8192x8192, MXFP8xMXFP4 4096x7168x16384 and the
-  dynamic quantiser;
+* ``decode_sweep`` / ``prefill_sweep``: the dispatch sweep, M in
+  {1, 32} cold and M in {256, 2048, 8192} warm, A4W4 (also with the
+  activation quantised on the fly) and bf16, through the tuned dispatch;
+* ``a8w4_mxfp8``: configs[3], MXFP8 x MXFP4 at M in {256, 4096}, N=7168,
+  K=16384, the GEMM alone and with the dynamic MXFP8 quant of a bf16 input;
+* ``extra``: bf16 A16W16 8192x8192x8192 (row-major and preshuffled B), the
+  K=16384 prefill variant, the quantisers and the "next" rows;
 * ``roofline`` of the dominant kernel (A4W4 tile kernel) from HIP events on the
   launch stream; ``traffic`` is the HBM bytes/launch measured with rocprofv3
   PMC counters (profiles/), or null when no such measurement is committed;
-* ``cpu_baseline``: the CPU oracle (dequantise -> f32 matmul, the reference's
-  ``run_torch`` of op_tests/test_gemm_a4w4.py:23-39) on a bounded row sample.
+* ``cpu_baseline``: the reference's CPU torch path on the full headline
+  problem (dequantise to f32 + ``torch.mm``, op_tests/test_gemm_a4w4.py:23-39,
+  restated in oracle/torch_ref.py), dequantisation and matmul timed apart.
 """
 from __future__ import annotations
 
@@ -269,6 +275,87 @@ def bench_decode_sweep(dev, ms=(1, 32)):
     return rows
 
 
+def bench_prefill_sweep(dev, ms=(256, 2048, 8192)):
+    """Compute-bound rows of the dispatch sweep: M in
+    {256, 2048, 8192} over its five (N, K), through the tuned dispatch.
+    A4W4: ``gemm_a4w4`` on MXFP4 operands (``us``), and with the bf16
+    activation quantised on the fly first (``us_with_quant``:
+    dynamic_mxfp4_quant + gemm_a4w4); bf16: ``gemm_a16w16`` with row-major B
+    (the layout of the reference's bf16 rows).  Warm L2; roofline fraction
+    against the dense MXFP4 / bf16 peak."""
+    import aiter_amd
+
+    rows = []
+    g = torch.Generator(device=dev).manual_seed(5)
+    for n, k in SWEEP_NK:
+        w16 = torch.randn((n, k), generator=g, device=dev).to(torch.bfloat16)
+        wq, ws = aiter_amd.dynamic_mxfp4_quant(w16, shuffle=True)
+        wq = aiter_amd.shuffle_weight(wq)
+        for m in ms:
+            x16 = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+            xq, xs = aiter_amd.dynamic_mxfp4_quant(x16, shuffle=True)
+            flop = 2.0 * m * n * k
+            steps = max(3, min(20, int(2e13 / flop)))
+            cfg = aiter_amd.get_GEMM_config(m, n, k)
+            t = time_graph(lambda: aiter_amd.gemm_a4w4(xq, wq, xs, ws), steps, 2)
+            tq = time_graph(lambda: _quant_then_gemm(aiter_amd, x16, wq, ws), steps, 2)
+            rows.append({"fam": "a4w4", "M": m, "N": n, "K": k,
+                         "kernel": str(cfg["kernelName"]) if cfg else "heuristic",
+                         "us": round(t * 1e6, 2), "TFLOPs": round(flop / t / 1e12, 1),
+                         "frac_mxfp4_peak": round(flop / t / 1e12 / PEAK_MXFP4, 4),
+                         "us_with_quant": round(tq * 1e6, 2)})
+            log(f"prefill sweep a4w4 M={m} N={n} K={k}: {t*1e6:.1f} us ({flop/t/1e12:.0f} TF), "
+                f"with quant {tq*1e6:.1f} us")
+            t16 = time_graph(lambda: aiter_amd.gemm_a16w16(x16, w16), steps, 2)
+            rows.append({"fam": "bf16", "M": m, "N": n, "K": k, "kernel": "tuned/heuristic",
+                         "us": round(t16 * 1e6, 2), "TFLOPs": round(flop / t16 / 1e12, 1),
+                         "frac_bf16_peak": round(flop / t16 / 1e12 / PEAK_BF16, 4)})
+            log(f"prefill sweep bf16 M={m} N={n} K={k}: {t16*1e6:.1f} us ({flop/t16/1e12:.0f} TF)")
+            del x16, xq, xs
+        del w16, wq, ws
+        torch.cuda.empty_cache()
+    return rows
+
+
+def _quant_then_gemm(aiter_amd, x16, wq, ws):
+    xq, xs = aiter_amd.dynamic_mxfp4_quant(x16, shuffle=True)
+    return aiter_amd.gemm_a4w4(xq, wq, xs, ws)
+
+
+def bench_a8w4(dev, ms=(256, 4096)):
+    """MXFP8 x MXFP4, M in {256, 4096}, N = 7168,
+    K = 16384, from a bf16 N(0,1) activation: the GEMM alone on quantised
+    operands and the whole call with the dynamic MXFP8 quant
+    (``gemm_a8w4_mxfp8_dynamic``: quant kernel + GEMM), against the dense
+    MXFP8 peak."""
+    import aiter_amd
+
+    rows = []
+    n, k = 7168, 16384
+    g = torch.Generator(device=dev).manual_seed(7)
+    w = torch.randn((n, k), generator=g, device=dev).to(torch.bfloat16)
+    wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+    wq = aiter_amd.shuffle_weight(wq)
+    del w
+    for m in ms:
+        x = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+        xq, xs = aiter_amd.dynamic_mxfp8_quant(x, shuffle=True)
+        flop = 2.0 * m * n * k
+        t = time_graph(lambda: aiter_amd.gemm_a8w4_mxfp8(xq, wq, xs, ws, a_preshuffle=False), 10, 2)
+        td = time_graph(lambda: aiter_amd.gemm_a8w4_mxfp8_dynamic(x, wq, ws), 10, 2)
+        tq = time_graph(lambda: aiter_amd.dynamic_mxfp8_quant(x, shuffle=True), 20, 2)
+        cfg = aiter_amd.gemm_op_a8w4.get_GEMM_A8W4_config(m, n, k)
+        rows.append({"M": m, "N": n, "K": k, "kernel": str(cfg["kernelName"]) if cfg else "heuristic",
+                     "gemm_us": round(t * 1e6, 1), "gemm_TFLOPs": round(flop / t / 1e12, 1),
+                     "frac_mxfp8_peak": round(flop / t / 1e12 / PEAK_MXFP8, 4),
+                     "with_dynamic_quant_us": round(td * 1e6, 1),
+                     "with_dynamic_quant_TFLOPs": round(flop / td / 1e12, 1),
+                     "quant_us": round(tq * 1e6, 1), "quant_GBps": round(m * k * (2 + 1 + 1 / 32) / tq / 1e9, 1)})
+        log(f"a8w4 M={m}: gemm {t*1e6:.1f} us ({flop/t/1e12:.0f} TF), with dynamic quant {td*1e6:.1f} us")
+        del x, xq, xs
+    return rows
+
+
 def bench_extra(dev):
     import aiter_amd
 
@@ -295,20 +382,6 @@ def bench_extra(dev):
                                    "frac_mxfp4_peak": round(2 * m * n * k / t / 1e12 / PEAK_MXFP4, 4),
                                    "kernel": str(cfg["kernelName"]) if cfg else "heuristic"}
     del aq, as_, bq, bs_
-    # MXFP8 x MXFP4 M=4096 N=7168 K=16384 (+ dynamic quant of the bf16 activation)
-    m, n, k = 4096, 7168, 16384
-    x = torch.randn((m, k), generator=g).to(torch.bfloat16).to(dev)
-    w = torch.randn((n, k), generator=g).to(dev)
-    wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
-    wq = aiter_amd.shuffle_weight(wq)
-    del w
-    xq, xs = aiter_amd.dynamic_mxfp8_quant(x, shuffle=True)
-    t = time_graph(lambda: aiter_amd.gemm_a8w4_mxfp8(xq, wq, xs, ws, a_preshuffle=False), 10, 2)
-    tq = time_graph(lambda: aiter_amd.dynamic_mxfp8_quant(x, shuffle=True), 20, 2)
-    out["a8w4_4096x7168x16384"] = {"us": round(t * 1e6, 1), "TFLOPs": round(2 * m * n * k / t / 1e12, 1),
-                                   "frac_mxfp8_peak": round(2 * m * n * k / t / 1e12 / PEAK_MXFP8, 4),
-                                   "quant_us": round(tq * 1e6, 1),
-                                   "quant_GBps": round(m * k * (2 + 1 + 1 / 32) / tq / 1e9, 1)}
     # MXFP4 activation quant 8192 x 8192 bf16
     xa = torch.randn((8192, 8192), generator=g).to(torch.bfloat16).to(dev)
     tq = time_graph(lambda: aiter_amd.per_1x32_mx_quant_hip(xa, shuffle=True), 20, 2)
@@ -434,39 +507,54 @@ def bf16_plumbing(dev):
                                             <= 1e-2 + 1e-2 * ref.bfloat16().float().abs()).float().mean()), 6)}
 
 
-def cpu_baseline(budget_s=10.0):
-    """Oracle (numpy) dequantise + f32 matmul on a row sample of the 8192^3
-    A4W4 problem, scaled to TFLOP/s."""
-    from oracle import mx_oracle as O
+def cpu_threads():
+    """Host threads the CPU baseline uses: the box's CPU share
+    (OMP_NUM_THREADS when set, as on the GPU boxes), else every CPU."""
+    env = os.environ.get("OMP_NUM_THREADS")
+    return max(1, int(env)) if env and env.isdigit() else (os.cpu_count() or 1)
 
+
+def cpu_baseline():
+    """The reference's CPU torch path on the headline problem itself
+    ``run_torch`` of op_tests/test_gemm_a4w4.py:23-39
+    restated in oracle/torch_ref.py -- dequantise the MXFP4 A and B of
+    M = N = K = 8192 to f32, one f32 ``torch.mm``, cast to bf16 -- on the
+    host threads, 2 warm-ups then 1 timed run (the problem is above 100
+    GFLOP).  ``value`` is the whole path's TFLOP/s; the dequantisation and
+    the matmul are also timed separately."""
+    import platform
+
+    from oracle import torch_ref as T
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    m = n = k = 8192
+    g = torch.Generator().manual_seed(0)
+    # quantised operands of the headline shape (random e2m1 bytes, e8m0 near 2^0)
+    aq = torch.randint(0, 256, (m, k // 2), dtype=torch.uint8, generator=g)
+    bq = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, generator=g)
+    asc = torch.randint(120, 134, (m, k // 32), dtype=torch.uint8, generator=g)
+    bsc = torch.randint(120, 134, (n, k // 32), dtype=torch.uint8, generator=g)
+    for _ in range(2):
+        T.run_torch_a4w4(aq, bq, asc, bsc)
+    tm = {}
+    t0 = time.perf_counter()
+    T.run_torch_a4w4(aq, bq, asc, bsc, timings=tm)
+    total = time.perf_counter() - t0
+    flop = 2.0 * m * n * k
+    cpu_model = platform.processor() or "unknown"
     try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [os.cpu_count()])
-    except Exception:
-        threads = os.cpu_count()
-    n = k = 8192
-    rs = np.random.default_rng(0)
-    # already-quantised operands (random e2m1 bytes, e8m0 scales around 2^0):
-    # the timed CPU path is the reference's dequantise + f32 matmul
-    bq = rs.integers(0, 256, (n, k // 2), dtype=np.uint8)
-    bsc = rs.integers(120, 134, (n, k // 32), dtype=np.uint8)
-    rows = 512
-    total_flop = 0.0
-    total_t = 0.0
-    runs = 0
-    while total_t < budget_s and runs < 64:
-        aq = rs.integers(0, 256, (rows, k // 2), dtype=np.uint8)
-        asc = rs.integers(120, 134, (rows, k // 32), dtype=np.uint8)
-        t0 = time.perf_counter()
-        O.gemm_a4w4_ref(aq, bq, asc, bsc)
-        dt = time.perf_counter() - t0
-        total_t += dt
-        total_flop += 2.0 * rows * n * k
-        runs += 1
-    return {"value": round(total_flop / total_t / 1e12, 5), "unit": "TFLOP/s", "cores": int(threads),
+        with open("/proc/cpuinfo") as f:
+            cpu_model = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except (OSError, StopIteration):
+        pass
+    return {"value": round(flop / total / 1e12, 5), "unit": "TFLOP/s", "cores": int(torch.get_num_threads()),
             "kind": "port",
-            "sample": f"{runs} run(s) of M={rows} rows x N=K=8192 (dequantise A and B + f32 matmul + bf16), "
-                      f"{total_t:.1f} s"}
+            "sample": f"the full M=N=K=8192 A4W4 problem: dequantise A and B to f32 ({tm['dequant_s']:.2f} s) + "
+                      f"torch.mm f32 ({tm['mm_s']:.2f} s) + bf16 cast, {total:.2f} s, 1 timed run after 2 warm-ups",
+            "dequant_s": round(tm["dequant_s"], 3), "mm_s": round(tm["mm_s"], 3),
+            "mm_TFLOPs": round(flop / tm["mm_s"] / 1e12, 4), "cpu_model": cpu_model,
+            "torch": torch.__version__}
 
 
 def pmc_workload(dev):
@@ -508,6 +596,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--moe", action="store_true", help="only the fused-MoE workloads (for profiling)")
     ap.add_argument("--decode", action="store_true", help="only the decode workloads (configs[1] and configs[4])")
+    ap.add_argument("--sweep", action="store_true", help="only the prefill sweep (configs[4]) and configs[3]")
+    ap.add_argument("--cpu", action="store_true", help="only the CPU baseline")
     ap.add_argument("--pmc", action="store_true",
                     help="only the launches of the HBM-traffic counter runs (copy calibration + A4W4 8192^3)")
     args = ap.parse_args()
@@ -529,12 +619,20 @@ def main():
     if args.decode:
         print(json.dumps({"decode": bench_decode(dev), "decode_sweep": bench_decode_sweep(dev)}), flush=True)
         return
+    if args.sweep:
+        print(json.dumps({"prefill_sweep": bench_prefill_sweep(dev), "a8w4_mxfp8": bench_a8w4(dev)}), flush=True)
+        return
+    if args.cpu:
+        print(json.dumps({"cpu_baseline": cpu_baseline()}), flush=True)
+        return
 
     log("prefill A4W4 8192^3")
     sec, tflops, kname = bench_prefill(args.steps, args.warmup, dev)
     log(f"prefill: {sec*1e6:.1f} us/step, {tflops:.0f} TFLOP/s ({kname or 'heuristic'})")
     decode = [] if args.quick else bench_decode(dev)
     sweep = [] if args.quick else bench_decode_sweep(dev)
+    prefill_sweep = [] if args.quick else bench_prefill_sweep(dev)
+    a8w4 = [] if args.quick else bench_a8w4(dev)
     extra = {} if args.quick else bench_extra(dev)
     cpu = None if (args.no_cpu or args.quick) else cpu_baseline()
     m = n = k = 8192
@@ -558,6 +656,8 @@ def main():
         "cpu_baseline": cpu,
         "decode": decode,
         "decode_sweep": sweep,
+        "prefill_sweep": prefill_sweep,
+        "a8w4_mxfp8": a8w4,
         "extra": extra,
     }
     print(json.dumps(line), flush=True)

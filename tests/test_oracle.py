@@ -377,3 +377,45 @@ def test_gemm_a4w4o4_ref_integer_brute_force():
     # saturation: |c| > 6 maps to code 7 / 15
     big = np.abs(exact) > 6
     assert np.all((got[big] & 7) == 7)
+
+
+# ---------------------------------------------------------------- torch restatement (CPU baseline)
+def test_torch_ref_codecs_match_numpy_oracle():
+    """oracle/torch_ref.py decodes every e2m1 byte and every e8m0 byte exactly
+    as the pinned numpy oracle (bit patterns, -0.0 and NaN included)."""
+    import torch
+
+    from oracle import torch_ref as T
+
+    allb = np.arange(256, dtype=np.uint8)
+    got = T.mxfp4_to_f32(torch.from_numpy(allb[None, :])).numpy()
+    ref = O.mxfp4_to_f32(allb[None, :])
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    gs = T.e8m0_to_f32(torch.from_numpy(allb)).numpy()
+    rs = O.e8m0_to_f32(allb)
+    assert np.array_equal(gs[:255].view(np.uint32), rs[:255].view(np.uint32))
+    assert np.isnan(gs[255]) and np.isnan(rs[255])
+
+
+def test_torch_ref_gemm_matches_numpy_oracle():
+    import torch
+
+    from oracle import torch_ref as T
+
+    rs = np.random.default_rng(5)
+    m, n, k = 24, 40, 256
+    aq = rs.integers(0, 256, (m, k // 2), dtype=np.uint8)
+    bq = rs.integers(0, 256, (n, k // 2), dtype=np.uint8)
+    asc = rs.integers(118, 136, (m, k // 32), dtype=np.uint8)
+    bsc = rs.integers(118, 136, (n, k // 32), dtype=np.uint8)
+    da = T.dequant_mxfp4(torch.from_numpy(aq), torch.from_numpy(asc)).numpy()
+    assert np.array_equal(da.view(np.uint32), O.dequant_mxfp4(aq, asc).view(np.uint32))
+    tm = {}
+    got = T.run_torch_a4w4(torch.from_numpy(aq), torch.from_numpy(bq), torch.from_numpy(asc), torch.from_numpy(bsc),
+                           timings=tm).view(torch.int16).numpy().view(np.uint16)
+    ref = O.gemm_a4w4_ref(aq, bq, asc, bsc)
+    assert set(tm) == {"dequant_s", "mm_s"}
+    # same dequantised operands; the f32 matmul may sum in another order: bf16
+    # results equal or one bf16 step apart
+    diff = np.abs(got.astype(np.int32) - ref.astype(np.int32))
+    assert diff.max() <= 1 and np.mean(diff == 0) > 0.99
