@@ -22,6 +22,12 @@ over enough copies of the weight operand (> 512 MiB in total, capped at 64
 copies) that every call streams its weights from HBM as in serving, and the
 graph replay is timed with HIP events on the launch stream.
 
+Each shape is tuned in a worker process of its own under a watchdog, and its
+row is merged into the output as soon as it is done; a rerun skips the
+shapes already there (``--all`` retunes them); a worker that fails costs only
+its shape.  ``--compare --update_improved`` keeps a tuned row only when it
+beats the current dispatch by ``--min_improvement_pct``.
+
     python -m aiter_amd.tuner --family a4w4 -i untuned.csv -o tuned.csv
     python -m aiter_amd.tuner --family a16w16 --sweep -o bf16_tuned_gemm.csv
 """
@@ -270,6 +276,18 @@ def tune_bf16(M: int, N: int, K: int, bias: bool, otype: torch.dtype, bpreshuffl
 
 
 # ---------------------------------------------------------------- driver
+#
+# Fault isolation (the role of aiter/utility/mp_tuner.py:483-705): the driver
+# process never touches the GPU.  Each shape is tuned by a fresh worker
+# process (`python -m aiter_amd.tuner --worker ...`) under a watchdog; a
+# worker that crashes, faults the GPU or hangs costs that one shape, which is
+# logged and left untuned, and the sweep goes on.  Each worker writes its row
+# into the output CSV as soon as the shape is done (merged under a file lock,
+# replaced atomically), so an interrupted sweep keeps every finished shape,
+# and a rerun skips the shapes the output already holds (the resume of
+# aiter/utility/base_tuner.py:1573-1595; --all retunes them).
+
+
 def _read_untuned(path: str, family: str):
     df = pd.read_csv(path, skipinitialspace=True)
     rows = []
@@ -282,6 +300,179 @@ def _read_untuned(path: str, family: str):
     return rows
 
 
+def _keys(family: str):
+    return BF16_COLUMNS[:10] if family == "a16w16" else A4W4_COLUMNS[:5]
+
+
+def _columns(family: str):
+    return BF16_COLUMNS if family == "a16w16" else A4W4_COLUMNS
+
+
+def _shape_key(family: str, gfx: str, cu: int, s) -> tuple:
+    if family == "a16w16":
+        m, n, k, bias, otype, bpre = s
+        return (gfx, cu, m, n, k, bool(bias), str(dtypes.bf16), otype, False, bool(bpre))
+    return (gfx, cu) + tuple(int(v) for v in s)
+
+
+def _row_key(family: str, row) -> tuple:
+    def b(v):
+        return v if isinstance(v, bool) else str(v) == "True"
+
+    if family == "a16w16":
+        return (str(row["gfx"]), int(row["cu_num"]), int(row["M"]), int(row["N"]), int(row["K"]), b(row["bias"]),
+                str(row["dtype"]), str(row["outdtype"]), b(row["scaleAB"]), b(row["bpreshuffle"]))
+    return (str(row["gfx"]), int(row["cu_num"]), int(row["M"]), int(row["N"]), int(row["K"]))
+
+
+def tuned_keys(path: str, family: str) -> set:
+    if not os.path.exists(path):
+        return set()
+    df = pd.read_csv(path)
+    return {_row_key(family, r) for _, r in df.iterrows()}
+
+
+def write_row(path: str, family: str, row: dict) -> None:
+    """Merge one tuned row into the CSV at `path` (a row with the same key is
+    replaced), under an exclusive lock, through an atomic rename."""
+    import fcntl
+
+    os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+    cols = _columns(family)
+    with open(path + ".lock", "w") as lk:
+        fcntl.flock(lk, fcntl.LOCK_EX)
+        new = pd.DataFrame([row], columns=cols)
+        if os.path.exists(path) and os.path.getsize(path) > 0:
+            old = pd.read_csv(path)
+            key = _row_key(family, row)
+            old = old[[_row_key(family, r) != key for _, r in old.iterrows()]]
+            df = pd.concat([old, new], ignore_index=True) if len(old) else new
+        else:
+            df = new
+        tmp = f"{path}.tmp{os.getpid()}"
+        df.to_csv(tmp, index=False)
+        os.replace(tmp, path)
+
+
+def _shape_arg(family: str, s) -> str:
+    return ",".join(str(v) for v in s)
+
+
+def _parse_shape(family: str, text: str):
+    f = text.split(",")
+    if family == "a16w16":
+        return (int(f[0]), int(f[1]), int(f[2]), f[3] == "True", f[4], f[5] == "True")
+    return (int(f[0]), int(f[1]), int(f[2]))
+
+
+def _time_production(family: str, s, iters: int):
+    """Seconds per call of the shape through the library's current dispatch
+    (the tuned tables in effect, else the heuristic) -- the --compare
+    baseline; None when the call fails."""
+    import aiter_amd
+
+    dev = torch.device("cuda", torch.cuda.current_device())
+    g = torch.Generator(device="cpu").manual_seed(1)
+    try:
+        if family == "a16w16":
+            m, n, k = s[:3]
+            a = torch.randn((m, k), generator=g).to(dtypes.bf16).to(dev)
+            b = torch.randn((n, k), generator=g).to(dtypes.bf16).to(dev)
+            if s[5]:
+                b = shuffle_weight(b)
+            fn = lambda i: aiter_amd.gemm_a16w16(a, b)
+        else:
+            m, n, k = s
+            a = torch.randn((m, k), generator=g).to(dev)
+            b = torch.randn((n, k), generator=g).to(dev)
+            bq, bs = dynamic_mxfp4_quant(b, shuffle=True)
+            bq = shuffle_weight(bq)
+            if family == "a4w4":
+                aq, as_ = dynamic_mxfp4_quant(a, shuffle=True)
+                fn = lambda i: aiter_amd.gemm_a4w4(aq, bq, as_, bs)
+            else:
+                aq, as_ = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=True)
+                fn = lambda i: aiter_amd.gemm_a8w4_mxfp8(aq, bq, as_, bs, a_preshuffle=False)
+        return time_rotated(fn, 1, iters)
+    except RuntimeError as e:
+        _log(f"  production run failed: {e}")
+        return None
+
+
+def worker(family: str, shape, tune_file: str, iters: int, max_err_ratio: float, compare: bool,
+           min_improvement_pct: float) -> int:
+    """Tune one shape in this process and merge its row into `tune_file`."""
+    if family == "a16w16":
+        m, n, k, bias, otype, bpre = shape
+        row = tune_bf16(m, n, k, bias, torch.float32 if "float32" in otype else dtypes.bf16, bpre, iters,
+                        max_err_ratio)
+    else:
+        row = tune_mx(family, *shape, iters=iters, max_err_ratio=max_err_ratio)
+    _log(f"  -> {row['kernelName']} split {row['splitK']} {row['us']} us {row['tflops']} TFLOP/s")
+    if compare:
+        base = _time_production(family, shape, iters)
+        gain = None if base is None else (base / (row["us"] * 1e-6) - 1.0) * 100.0
+        _log(f"  compare: production {'failed' if base is None else f'{base * 1e6:.2f} us'}, tuned "
+             f"{row['us']} us" + ("" if gain is None else f" ({gain:+.1f} %)"))
+        if gain is not None and gain < min_improvement_pct:
+            _log(f"  keep the existing dispatch (improvement {gain:.1f} % < {min_improvement_pct} %)")
+            return 0
+    write_row(tune_file, family, row)
+    return 0
+
+
+def _probe_arch(timeout: float):
+    """(gfx, cu_num) from a short child process, so that this process never
+    initialises the GPU; GPU_ARCHS / CU_NUM override."""
+    import subprocess
+
+    if os.environ.get("GPU_ARCHS") and os.environ.get("CU_NUM"):
+        return os.environ["GPU_ARCHS"].split(";")[0], int(os.environ["CU_NUM"])
+    code = "from aiter_amd.config import get_gfx, get_cu_num; print(get_gfx(), get_cu_num())"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=timeout,
+                       cwd=os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    gfx, cu = r.stdout.split()[-2:]
+    return gfx, int(cu)
+
+
+def drive(family: str, shapes, tune_file: str, iters: int, max_err_ratio: float, retune_all: bool,
+          timeout: float, compare: bool = False, min_improvement_pct: float = 3.0, worker_cmd=None) -> dict:
+    """Tune `shapes` one worker process each.  Returns {"tuned": [...],
+    "skipped": [...], "failed": [(shape, reason)]}.  `worker_cmd` (tests)
+    replaces the worker's command line prefix."""
+    import subprocess
+
+    gfx, cu = _probe_arch(max(60.0, timeout))
+    done = set() if retune_all else tuned_keys(tune_file, family)
+    res = {"tuned": [], "skipped": [], "failed": []}
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    for s in shapes:
+        if _shape_key(family, gfx, cu, s) in done:
+            _log(f"{family} {s}: already in {tune_file}, skipped")
+            res["skipped"].append(s)
+            continue
+        _log(f"{family} {s}")
+        cmd = list(worker_cmd) if worker_cmd else [sys.executable, "-m", "aiter_amd.tuner"]
+        cmd += ["--family", family, "--worker", _shape_arg(family, s), "-o", tune_file, "--iters", str(iters),
+                "--errRatio", str(max_err_ratio), "--min_improvement_pct", str(min_improvement_pct)]
+        if compare:
+            cmd.append("--compare")
+        try:
+            r = subprocess.run(cmd, cwd=root, timeout=timeout, capture_output=True, text=True)
+            sys.stdout.write(r.stdout)
+            if r.returncode != 0:
+                reason = f"worker exit {r.returncode}: {(r.stderr or '').strip().splitlines()[-1:]}"
+                _log(f"  FAILED {s}: {reason}")
+                res["failed"].append((s, reason))
+                continue
+        except subprocess.TimeoutExpired:
+            _log(f"  FAILED {s}: no result within {timeout:.0f} s")
+            res["failed"].append((s, "timeout"))
+            continue
+        res["tuned"].append(s)
+    return res
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--family", choices=["a4w4", "a8w4", "a16w16"], required=True)
@@ -290,11 +481,24 @@ def main(argv=None):
     ap.add_argument("-o", "--tune_file", required=True)
     ap.add_argument("--iters", type=int, default=20)
     ap.add_argument("--errRatio", type=float, default=0.05, help="max fraction of elements off tolerance")
-    ap.add_argument("--append", action="store_true", help="keep rows of an existing output for other keys")
+    ap.add_argument("--all", action="store_true", help="retune shapes the output already holds")
+    ap.add_argument("--timeout", type=float, default=600.0, help="per-shape watchdog (s) of a worker")
+    ap.add_argument("--compare", action="store_true",
+                    help="time the shape through the current dispatch first; with --update_improved keep a "
+                         "tuned row only if it is faster by --min_improvement_pct")
+    ap.add_argument("--update_improved", action="store_true")
+    ap.add_argument("--min_improvement_pct", type=float, default=3.0)
+    ap.add_argument("--no_isolate", action="store_true",
+                    help="tune every shape in this process (no worker processes, no watchdog)")
+    ap.add_argument("--worker", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
-    if not torch.cuda.is_available():
-        print("the tuner needs a GPU", file=sys.stderr)
-        return 2
+    min_pct = args.min_improvement_pct if (args.compare and args.update_improved) else -1e30
+    if args.worker is not None:
+        if not torch.cuda.is_available():
+            print("the tuner needs a GPU", file=sys.stderr)
+            return 2
+        return worker(args.family, _parse_shape(args.family, args.worker), args.tune_file, args.iters,
+                      args.errRatio, args.compare, min_pct)
     if args.untune_file:
         shapes = _read_untuned(args.untune_file, args.family)
     elif args.sweep:
@@ -303,29 +507,25 @@ def main(argv=None):
             shapes = [(m, n, k, False, "torch.bfloat16", False) for (m, n, k) in shapes]
     else:
         ap.error("give -i untuned.csv or --sweep")
-    rows = []
     t0 = time.time()
-    for s in shapes:
-        _log(f"{args.family} {s}")
-        if args.family == "a16w16":
-            m, n, k, bias, otype, bpre = s
-            row = tune_bf16(m, n, k, bias, torch.float32 if "float32" in otype else dtypes.bf16, bpre,
-                            args.iters, args.errRatio)
-        else:
-            row = tune_mx(args.family, *s, iters=args.iters, max_err_ratio=args.errRatio)
-        _log(f"  -> {row['kernelName']} split {row['splitK']} {row['us']} us {row['tflops']} TFLOP/s")
-        rows.append(row)
-        torch.cuda.empty_cache()
-    cols = BF16_COLUMNS if args.family == "a16w16" else A4W4_COLUMNS
-    df = pd.DataFrame(rows, columns=cols)
-    if args.append and os.path.exists(args.tune_file):
-        old = pd.read_csv(args.tune_file)
-        keys = cols[:10] if args.family == "a16w16" else cols[:5]
-        df = pd.concat([old, df], ignore_index=True).drop_duplicates(subset=keys, keep="last")
-    os.makedirs(os.path.dirname(os.path.abspath(args.tune_file)), exist_ok=True)
-    df.to_csv(args.tune_file, index=False)
-    _log(f"wrote {len(df)} rows to {args.tune_file} in {time.time() - t0:.0f} s")
-    return 0
+    if args.no_isolate:
+        if not torch.cuda.is_available():
+            print("the tuner needs a GPU", file=sys.stderr)
+            return 2
+        done = set() if args.all else tuned_keys(args.tune_file, args.family)
+        for s in shapes:
+            if _shape_key(args.family, get_gfx(), get_cu_num(), s) in done:
+                continue
+            _log(f"{args.family} {s}")
+            worker(args.family, s, args.tune_file, args.iters, args.errRatio, args.compare, min_pct)
+            torch.cuda.empty_cache()
+        _log(f"done in {time.time() - t0:.0f} s")
+        return 0
+    res = drive(args.family, shapes, args.tune_file, args.iters, args.errRatio, args.all, args.timeout,
+                args.compare, min_pct)
+    _log(f"tuned {len(res['tuned'])}, skipped {len(res['skipped'])}, failed {len(res['failed'])} "
+         f"in {time.time() - t0:.0f} s")
+    return 1 if res["failed"] else 0
 
 
 if __name__ == "__main__":

@@ -557,26 +557,54 @@ def cpu_baseline():
             "torch": torch.__version__}
 
 
-def pmc_workload(dev):
-    """Launches for the HBM-traffic counter runs (rocprofv3 --pmc FETCH_SIZE /
-    WRITE_SIZE): three plain device copies of COPY_BYTES (the calibration
-    kernel: it must read and write exactly COPY_BYTES each), then three
-    launches of the headline A4W4 8192^3 GEMM, each on a cold L2 (the copy
-    in between evicts it)."""
+def profile_workload(dev, name):
+    """Launches for the rocprofv3 runs behind profiles/ (kernel trace, FETCH_SIZE,
+    WRITE_SIZE, MFMA busy): three plain device copies of COPY_BYTES (the
+    traffic counters' calibration), then three launches of workload ``name``,
+    each after another copy (L2 and MALL start cold).  Every workload goes
+    through the library's public entry point and its tuned dispatch."""
     import aiter_amd
 
     src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
-    aq, as_, bq, bs = quantised_operands(8192, 8192, 8192, 0, dev)
-    out = torch.empty((8192, 8192), dtype=torch.bfloat16, device=dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+
+    def bf16(r, c):
+        return torch.randn((r, c), generator=g, device=dev).to(torch.bfloat16)
+
+    if name == "a4w4_8192":
+        aq, as_, bq, bs = quantised_operands(8192, 8192, 8192, 0, dev)
+        fn = lambda: aiter_amd.gemm_a4w4(aq, bq, as_, bs)
+    elif name in ("bf16_8192_bplain", "bf16_8192_bpre"):
+        a, b = bf16(8192, 8192), bf16(8192, 8192)
+        if name == "bf16_8192_bpre":
+            b = aiter_amd.shuffle_weight(b)
+        fn = lambda: aiter_amd.gemm_a16w16(a, b)
+    elif name == "a8w4_4096x7168x16384":
+        x, w = bf16(4096, 16384), bf16(7168, 16384)
+        wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+        wq = aiter_amd.shuffle_weight(wq)
+        xq, xs = aiter_amd.dynamic_mxfp8_quant(x, shuffle=True)
+        fn = lambda: aiter_amd.gemm_a8w4_mxfp8(xq, wq, xs, ws, a_preshuffle=False)
+    elif name == "quant_mxfp4_8192":
+        x = bf16(8192, 8192)
+        fn = lambda: aiter_amd.dynamic_mxfp4_quant(x, shuffle=True)
+    elif name == "a4w4_splitk_256x14336x4096":
+        aq, as_, bq, bs = quantised_operands(256, 14336, 4096, 0, dev)
+        fn = lambda: aiter_amd.gemm_a4w4(aq, bq, as_, bs)
+    elif name == "bf16_8192x8192x28672":
+        a, b = bf16(8192, 28672), bf16(8192, 28672)
+        fn = lambda: aiter_amd.gemm_a16w16(a, b)
+    else:
+        raise SystemExit(f"unknown workload {name}")
+    fn()
     for _ in range(3):
         dst.copy_(src)
-    kname = headline_kernel()
     for _ in range(3):
         dst.copy_(src)
-        aiter_amd.gemm_a4w4_asm(aq, bq, as_, bs, out, kernelName=kname)
+        fn()
     torch.cuda.synchronize()
-    log(f"pmc workload done: copy {COPY_BYTES} B x6, a4w4 8192^3 x3 ({kname or 'heuristic'})")
+    log(f"profile workload done: copy {COPY_BYTES} B x6, {name} x3 (+1 warm-up call)")
 
 
 def traffic_from_profiles():
@@ -598,8 +626,8 @@ def main():
     ap.add_argument("--decode", action="store_true", help="only the decode workloads (configs[1] and configs[4])")
     ap.add_argument("--sweep", action="store_true", help="only the prefill sweep (configs[4]) and configs[3]")
     ap.add_argument("--cpu", action="store_true", help="only the CPU baseline")
-    ap.add_argument("--pmc", action="store_true",
-                    help="only the launches of the HBM-traffic counter runs (copy calibration + A4W4 8192^3)")
+    ap.add_argument("--workload", default=None,
+                    help="only the launches of one profiled workload (see profile_workload)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path.",
@@ -610,8 +638,8 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda", 0)
     import aiter_amd  # noqa: F401  (fails loudly if the HIP library is missing)
-    if args.pmc:
-        pmc_workload(dev)
+    if args.workload:
+        profile_workload(dev, args.workload)
         return
     if args.moe:
         print(json.dumps({"fused_moe_a4w4_deepseek": bench_moe(dev)}), flush=True)
