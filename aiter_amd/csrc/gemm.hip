@@ -19,6 +19,7 @@
 #include "mfma32.h"
 #include "gemm_flat.h"
 #include "gemm_flat_persist.h"
+#include "gemm_lds_persist.h"
 #include "gemm_t32.h"
 #include "out_quant.h"
 
@@ -82,6 +83,14 @@ void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
         gemm_flat_persist_kernel<KA, BM, OF, BP, false, false><<<grid, 256, 0, s>>>(p);
     else
         gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
+}
+
+template <bool BP>
+void launch_lds_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
+    if (p.alpha == 1.0f)
+        gemm_lds_persist_kernel<BP, false><<<grid, 256, 0, s>>>(p);
+    else
+        gemm_lds_persist_kernel<BP, true><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
@@ -254,6 +263,11 @@ std::vector<Instance>& registry() {
         skinny(kA16W16, 2, false, b16p, launch_skinny<kBf16, 2, true, false, false, 2>, "a16w16", 32);
         skinny(kA16W16, 1, false, b16r, launch_skinny<kBf16, 1, false, false, false, 2>, "a16w16", 32);
         skinny(kA16W16, 2, false, b16r, launch_skinny<kBf16, 2, false, false, false, 2>, "a16w16", 32);
+        // ---- bf16 256x256 persistent tiles with A and B both through LDS in
+        // half-width ring slots (gemm_lds_persist.h) ----
+        persist(kA16W16, 256, b16r, launch_lds_persist<false>, "a16w16");
+        persist(kA16W16, 256, b16p, launch_lds_persist<true>, "a16w16");
+        reg.back().name = "a16w16_tile_256x256_lds_persist";
     });
     return reg;
 }
@@ -697,7 +711,10 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             AA_CHECK(twin, "no non-split twin of ", inst->name);
             inst = twin;
         }
-        if (inst->persistent && (p.bias || batched)) {
+        // the persistent kernels address A and B through whole-tensor 32-bit
+        // buffer offsets
+        const bool big = M * p.lda >= (1LL << 31) || N * p.ldb >= (1LL << 31);
+        if (inst->persistent && (p.bias || batched || big)) {
             // the persistent epilogue has no bias term: its one-tile-per-workgroup twin
             const Instance* twin = nullptr;
             for (auto& in : registry())

@@ -264,6 +264,37 @@ def test_gemm_a16w16_every_instance(cuda, name):
     assert ok, msg
 
 
+def _persistent_a16w16():
+    try:
+        from aiter_amd._lib import kernel_table
+
+        return [(r[1], bool(r[8])) for r in kernel_table() if r[2] == "a16w16" and r[1].endswith("_persist")]
+    except RuntimeError:
+        return []
+
+
+@pytest.mark.parametrize("m,n,k", [(600, 528, 64), (600, 528, 1088), (4352, 4096, 256)])
+@pytest.mark.parametrize("name,b_pre", _persistent_a16w16())
+def test_gemm_a16w16_persistent_instances(cuda, name, b_pre, m, n, k):
+    """The persistent bf16 tiles without bias (with a bias the host takes
+    their one-tile-per-workgroup twins): ragged M and N, K of one stage and of
+    an odd stage count, and more tiles than CUs (several tiles per workgroup)."""
+    import aiter_amd
+
+    announce(f"a16w16 persistent {name} {m}x{n}x{k}")
+    a = bf16_operand(m, k, 11)
+    b = bf16_operand(n, k, 12)
+    ref = O.bf16_bits_to_f32(O.gemm_a16w16_ref(a, b))
+    bt_np = O.shuffle_weight(b) if b_pre else b
+    at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+    bt = _dev(bt_np.view(np.int16), cuda).view(torch.bfloat16)
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.gemm_a16w16_asm(at, bt, out, kernelName=name, bpreshuffle=b_pre)
+    torch.cuda.synchronize()
+    ok, msg = allclose_report(_bf16_np(out), ref)
+    assert ok, msg
+
+
 def test_gemm_a16w16_opus_batched(cuda):
     import aiter_amd
 
