@@ -435,6 +435,17 @@ def _probe_arch(timeout: float):
     return gfx, int(cu)
 
 
+def worker_args(family: str, shape, tune_file: str, iters: int, max_err_ratio: float, compare: bool,
+                min_improvement_pct: float) -> list:
+    """Command-line arguments of the worker that tunes `shape`: the effective
+    improvement threshold is passed as is (``=`` form: it may be negative)."""
+    args = ["--family", family, "--worker", _shape_arg(family, shape), "-o", tune_file, "--iters", str(iters),
+            f"--errRatio={max_err_ratio}"]
+    if compare:
+        args += ["--compare", f"--min_improvement_pct={min_improvement_pct}"]
+    return args
+
+
 def drive(family: str, shapes, tune_file: str, iters: int, max_err_ratio: float, retune_all: bool,
           timeout: float, compare: bool = False, min_improvement_pct: float = 3.0, worker_cmd=None) -> dict:
     """Tune `shapes` one worker process each.  Returns {"tuned": [...],
@@ -453,10 +464,7 @@ def drive(family: str, shapes, tune_file: str, iters: int, max_err_ratio: float,
             continue
         _log(f"{family} {s}")
         cmd = list(worker_cmd) if worker_cmd else [sys.executable, "-m", "aiter_amd.tuner"]
-        cmd += ["--family", family, "--worker", _shape_arg(family, s), "-o", tune_file, "--iters", str(iters),
-                "--errRatio", str(max_err_ratio), "--min_improvement_pct", str(min_improvement_pct)]
-        if compare:
-            cmd.append("--compare")
+        cmd += worker_args(family, s, tune_file, iters, max_err_ratio, compare, min_improvement_pct)
         try:
             r = subprocess.run(cmd, cwd=root, timeout=timeout, capture_output=True, text=True)
             sys.stdout.write(r.stdout)
@@ -492,13 +500,14 @@ def main(argv=None):
                     help="tune every shape in this process (no worker processes, no watchdog)")
     ap.add_argument("--worker", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
-    min_pct = args.min_improvement_pct if (args.compare and args.update_improved) else -1e30
     if args.worker is not None:
+        # the driver passes the effective threshold itself
         if not torch.cuda.is_available():
             print("the tuner needs a GPU", file=sys.stderr)
             return 2
         return worker(args.family, _parse_shape(args.family, args.worker), args.tune_file, args.iters,
-                      args.errRatio, args.compare, min_pct)
+                      args.errRatio, args.compare, args.min_improvement_pct)
+    min_pct = args.min_improvement_pct if (args.compare and args.update_improved) else -1e30
     if args.untune_file:
         shapes = _read_untuned(args.untune_file, args.family)
     elif args.sweep:

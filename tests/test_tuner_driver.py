@@ -4,6 +4,7 @@ resume (shapes already tuned are skipped, --all retunes), and a crashing or
 hanging worker costing only its own shape.  A stand-in worker script plays
 the GPU worker's part (writes a row, crashes or hangs by shape)."""
 import os
+import subprocess
 import sys
 import textwrap
 
@@ -11,6 +12,8 @@ import pandas as pd
 import pytest
 
 from aiter_amd import tuner
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 FAKE = textwrap.dedent('''
     import sys, time
@@ -79,3 +82,20 @@ def test_bf16_keys_round_trip(tmp_path):
     tuner.write_row(out, "a16w16", row)
     assert tuner._shape_key("a16w16", "gfx950", 256, s) in tuner.tuned_keys(out, "a16w16")
     assert tuner._parse_shape("a16w16", tuner._shape_arg("a16w16", s)) == s
+
+
+@pytest.mark.parametrize("compare,pct", [(False, 3.0), (True, -1e30), (True, 5.0)])
+def test_worker_command_line_parses(tmp_path, compare, pct):
+    """The worker command that the driver builds is accepted by the tuner's
+    own argument parser (a negative threshold included); without a GPU the
+    worker then stops with its own message, not a usage error."""
+    from aiter_amd import tuner
+
+    shape = (64, 512, 256, False, "torch.bfloat16", True)
+    args = tuner.worker_args("a16w16", shape, str(tmp_path / "t.csv"), 5, 0.05, compare, pct)
+    env = dict(os.environ, HIP_VISIBLE_DEVICES="-1", CUDA_VISIBLE_DEVICES="-1")
+    r = subprocess.run([sys.executable, "-m", "aiter_amd.tuner"] + args, cwd=ROOT, env=env, capture_output=True,
+                       text=True, timeout=300)
+    assert "error: argument" not in r.stderr, r.stderr
+    assert r.returncode == 2 and "the tuner needs a GPU" in r.stderr, (r.returncode, r.stderr)
+    assert tuner._parse_shape("a16w16", args[args.index("--worker") + 1]) == shape
