@@ -18,6 +18,9 @@ from .gemm_op_a4w4 import (MXFP8_OUT_SCALE_BLOCK, gemm_a4w4o4, gemm_a4w4o8, gemm
                            gemm_a4w4_blockscale_tune, get_GEMM_config)
 from .batched_gemm_op_bf16 import batched_gemm_bf16, batched_gemm_bf16_CK, batched_gemm_bf16_tune
 from .fused_quant import fused_rms_mxfp4_quant, fused_rms_mxfp8_quant
+from .fused_gemm import (fused_gemm_afp4wfp4_a16w16, fused_gemm_afp4wfp4_mul_add,
+                         fused_gemm_afp4wfp4_preshuffle_add_mul, fused_gemm_afp4wfp4_preshuffle_split_cat,
+                         fused_gemm_afp4wfp4_split_cat)
 from .fused_moe import (ActivationType, ck_moe_stage1, ck_moe_stage2, fused_dynamic_mx_quant_moe_sort,
                         fused_dynamic_mxfp4_quant_moe_sort, fused_dynamic_mxfp8_quant_moe_sort, fused_moe,
                         fused_moe_2stages, get_block_size_M, moe_sorting, moe_sorting_fwd, moe_sum,

@@ -549,6 +549,9 @@ struct GemmCall {
     // library workspace for split-K partials; nothing is allocated
     void* scratch = nullptr;
     size_t scratch_bytes = 0;
+    // output operation fused into the epilogue (fused_gemm_afp4wfp4_*); the
+    // persistent kernels do not carry it, their one-tile twins do
+    EpiOp epi{};
 };
 
 // split-K partial buffer of a call: the call's scratch when it brings one
@@ -617,6 +620,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     p.K = (int)K;
     p.alpha = c.alpha;
     p.beta = c.beta;
+    p.epi = c.epi;
     if (c.bias) {
         check_tensor(c.bias, "bias");
         AA_CHECK(c.bias->dtype == AITER_DTYPE_fp32, "bias must be f32");
@@ -714,7 +718,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         // the persistent kernels address A and B through whole-tensor 32-bit
         // buffer offsets
         const bool big = M * p.lda >= (1LL << 31) || N * p.ldb >= (1LL << 31);
-        if (inst->persistent && (p.bias || batched || big)) {
+        if (inst->persistent && (p.bias || batched || big || c.epi.kind)) {
             // the persistent epilogue has no bias term: its one-tile-per-workgroup twin
             const Instance* twin = nullptr;
             for (auto& in : registry())
@@ -787,6 +791,141 @@ void* scratch_address(int dev) {
     AA_CHECK(ptr, "no device address for the scratch array");
     addr[dev] = ptr;
     return ptr;
+}
+
+// ---- fused_gemm_afp4wfp4_* (aiter/ops/triton/gemm/fused/) ----
+
+// plain e8m0 scales [rows, groups] (row stride in bytes) -> the shuffled
+// layout of shuffle_scale (aiter/ops/shuffle.py:339-365), pad32(rows) rows,
+// padding zero: output byte o of 32-row block i0 holds the scale of row
+// i0*32 + 16*a + b, group 8*c + 4*d + e, o = i0*32*groups + 256c + 64e + 4b + 2d + a
+__global__ __launch_bounds__(256) void plain_scale_shuffle_kernel(const uint8_t* src, int64_t src_stride, int rows,
+                                                                  int groups, uint8_t* dst, int64_t total) {
+    const int64_t o = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (o >= total) return;
+    const int64_t blk = 32 * (int64_t)groups;
+    const int i0 = (int)(o / blk);
+    const int w0 = (int)(o - i0 * blk);
+    const int c = w0 / 256, w = w0 % 256;
+    const int e = w / 64, b = (w % 64) / 4, d = (w % 4) / 2, a = w % 2;
+    const int r = i0 * 32 + a * 16 + b, g = c * 8 + d * 4 + e;
+    dst[o] = r < rows ? src[(int64_t)r * src_stride + g] : 0;
+}
+
+// c1[m, d, S1 + j] = y[m, d, j] (bf16, y of any strides, c1 contiguous)
+__global__ __launch_bounds__(256) void split_cat_copy_kernel(const uint16_t* y, int64_t ys0, int64_t ys1, int64_t ys2,
+                                                             uint16_t* c1, int M, int D, int S1, int S3) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)M * D * S3) return;
+    const int j = (int)(i % S3);
+    const int64_t md = i / S3;
+    const int d = (int)(md % D), m = (int)(md / D);
+    c1[((int64_t)m * D + d) * (S1 + S3) + S1 + j] = y[m * ys0 + d * ys1 + j * ys2];
+}
+
+// contiguous [rows, cols] view of a tensor's bytes
+aiter_tensor_t flat_view(const aiter_tensor_t* t, int64_t rows, int64_t cols, const char* what) {
+    check_tensor(t, what);
+    int64_t expect = 1;
+    for (int d = t->ndim - 1; d >= 0; --d) {
+        AA_CHECK(t->shape[d] == 1 || t->strides[d] == expect, what, " must be contiguous");
+        expect *= t->shape[d];
+    }
+    AA_CHECK((int64_t)t->numel == rows * cols, what, " has ", t->numel, " elements, expected ", rows, " x ", cols);
+    aiter_tensor_t v = *t;
+    v.ndim = 2;
+    v.shape[0] = rows;
+    v.shape[1] = cols;
+    v.strides[0] = cols;
+    v.strides[1] = 1;
+    return v;
+}
+
+// e8m0 scales of a fused call as the GEMM takes them: shuffled tensors (any
+// shape over the shuffled bytes, e.g. the Triton [R/32, K] view) are viewed
+// as [bytes / (K/32), K/32]; plain [R, K/32] tensors are shuffled into
+// workspace slot `slot` first
+aiter_tensor_t fused_scales(const aiter_tensor_t* sc, bool shuffled, int64_t R, int64_t K, int dev, hipStream_t st,
+                            int slot, const char* what) {
+    const int64_t kb = K / 32;
+    check_tensor(sc, what);
+    AA_CHECK(is_byte_type(sc->dtype), what, " must be e8m0 bytes");
+    if (shuffled) {
+        AA_CHECK((int64_t)sc->numel % kb == 0, what, " (shuffled) has ", sc->numel, " bytes, not a multiple of K/32");
+        return flat_view(sc, (int64_t)sc->numel / kb, kb, what);
+    }
+    AA_CHECK(sc->ndim == 2 && rows_2d(sc) >= R && cols_2d(sc) == kb, what, " must be [", R, ", ", kb, "] (plain e8m0)");
+    const int64_t stride = row_stride_2d(sc, what);
+    const int64_t rows = (R + 31) / 32 * 32;
+    uint8_t* dst = reinterpret_cast<uint8_t*>(workspace(dev, st, (size_t)(rows * kb), slot));
+    const int64_t total = rows * kb;
+    if (total > 0) {
+        plain_scale_shuffle_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, st>>>(
+            static_cast<const uint8_t*>(sc->ptr), stride, (int)R, (int)kb, dst, total);
+        AA_HIP(hipGetLastError());
+    }
+    aiter_tensor_t v{};
+    v.ptr = dst;
+    v.numel = (size_t)total;
+    v.ndim = 2;
+    v.shape[0] = rows;
+    v.shape[1] = kb;
+    v.strides[0] = kb;
+    v.strides[1] = 1;
+    v.dtype = AITER_DTYPE_fp8_e8m0;
+    v.device_id = sc->device_id;
+    return v;
+}
+
+// A4W4 GEMM of a fused op: x [M, K/2], w [N, K/2] row-major or its
+// shuffle_weight bytes (any shape, e.g. the Triton [N/16, K*8] view); with
+// preshuffled w the w scales are shuffled and the x scales too when M >= 32
+// (the Triton preshuffled ops' convention), otherwise both are plain
+void fused_a4w4(const aiter_tensor_t* x, const aiter_tensor_t* w, const aiter_tensor_t* xs, const aiter_tensor_t* ws,
+                bool preshuffled, const aiter_tensor_t* out, const aiter_tensor_t* bias, const EpiOp& epi,
+                const char* kernel_name, hipStream_t st) {
+    check_tensor(x, "x", 2);
+    check_tensor(w, "w", 2);
+    const int64_t M = rows_2d(x), K = cols_2d(x) * 2;
+    AA_CHECK(K % 256 == 0, "K = ", K, " must be a multiple of 256");
+    int64_t N;
+    aiter_tensor_t wv;
+    if (preshuffled) {
+        AA_CHECK((int64_t)w->numel % (K / 2) == 0, "w (preshuffled) has ", w->numel, " bytes, not a multiple of K/2");
+        N = (int64_t)w->numel / (K / 2);
+        wv = flat_view(w, N, K / 2, "w");
+    } else {
+        N = rows_2d(w);
+        AA_CHECK(cols_2d(w) * 2 == K, "w K dim ", cols_2d(w) * 2, " != x K dim ", K);
+        wv = *w;
+    }
+    int dev = x->device_id;
+    if (dev < 0) AA_HIP(hipGetDevice(&dev));
+    const aiter_tensor_t xsv = fused_scales(xs, preshuffled && M >= 32, M, K, dev, st, 3, "x_scale");
+    const aiter_tensor_t wsv = fused_scales(ws, preshuffled, N, K, dev, st, 4, "w_scale");
+    GemmCall c{kA4W4, {false, preshuffled, false}, x, &wv, &xsv, &wsv, out, bias, 1.0f, 1.0f, kernel_name, -1, -1};
+    c.epi = epi;
+    run_gemm(c, st);
+}
+
+// one operand of mul_add: tensor broadcastable to [M, N] (f32 or bf16) or NULL
+void mul_add_operand(const aiter_tensor_t* t, int64_t M, int64_t N, const void** ptr, int* bf16, int64_t* sm,
+                     int64_t* sn, const char* what) {
+    *ptr = nullptr;
+    if (!t) return;
+    check_tensor(t, what);
+    AA_CHECK(t->dtype == AITER_DTYPE_fp32 || t->dtype == AITER_DTYPE_bf16, what, " must be f32 or bf16");
+    *ptr = t->ptr;
+    *bf16 = t->dtype == AITER_DTYPE_bf16;
+    if (t->numel == 1) {
+        *sm = *sn = 0;
+        return;
+    }
+    AA_CHECK(t->ndim == 2, what, " must be a scalar or 2-D (broadcastable to [M, N])");
+    AA_CHECK(t->shape[0] == M || t->shape[0] == 1, what, " has ", t->shape[0], " rows, expected ", M, " or 1");
+    AA_CHECK(t->shape[1] == N || t->shape[1] == 1, what, " has ", t->shape[1], " columns, expected ", N, " or 1");
+    *sm = t->shape[0] == 1 ? 0 : t->strides[0];
+    *sn = t->shape[1] == 1 ? 0 : t->strides[1];
 }
 
 }  // namespace
@@ -1150,6 +1289,105 @@ int aiter_amd_resolve_opus_kid(int kid, int out_f32, int64_t M) {
     if (!decode_opus_kid(kid, &t)) return -2;
     const Instance* in = reference_tile_instance(t, kA16W16, Variant{false, false, out_f32 != 0}, M);
     return in ? in->id : -1;
+}
+
+// fused_gemm_afp4wfp4_mul_add / fused_gemm_afp4wfp4_preshuffle_add_mul
+// (aiter/ops/triton/gemm/fused/fused_gemm_afp4wfp4_mul_add.py:63-236, 239-...):
+// out = a * (x w^T) + b (fuse_type 0) or a * b + x w^T (fuse_type 1), in f32,
+// one rounding to bf16; a / b: tensors ([M, N], [1, N], [M, 1] or one element;
+// f32 or bf16) or NULL for the scalar argument.
+int fused_gemm_afp4wfp4_mul_add(aiter_tensor_t* x, aiter_tensor_t* w, aiter_tensor_t* x_scale, aiter_tensor_t* w_scale,
+                                aiter_tensor_t* a, float a_scalar, aiter_tensor_t* b, float b_scalar, int fuse_type,
+                                aiter_tensor_t* out, int preshuffled, const char* kernelName, aiter_stream_t stream) {
+    return safe_call([&] {
+        AA_CHECK(x && w && out, "x, w and out must be given");
+        DeviceGuard g(x->device_id);
+        AA_CHECK(fuse_type == 0 || fuse_type == 1, "fuse_type must be 0 or 1");
+        AA_CHECK(out->dtype == AITER_DTYPE_bf16, "out must be bf16");
+        const int64_t M = rows_2d(x), N = cols_2d(out);
+        EpiOp e{};
+        e.kind = 1;
+        e.fuse = fuse_type;
+        e.sa = a_scalar;
+        e.sb = b_scalar;
+        mul_add_operand(a, M, N, &e.ta, &e.ta_bf16, &e.ta_sm, &e.ta_sn, "a");
+        mul_add_operand(b, M, N, &e.tb, &e.tb_bf16, &e.tb_sm, &e.tb_sn, "b");
+        fused_a4w4(x, w, x_scale, w_scale, preshuffled != 0, out, nullptr, e, kernelName,
+                   reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+// fused_gemm_afp4wfp4_split_cat / fused_gemm_afp4wfp4_preshuffle_split_cat
+// (aiter/ops/triton/gemm/fused/fused_gemm_afp4wfp4_split_cat.py:19-196, 199-...):
+// C = x w^T viewed [M, D, S1+S2]; c1 = cat(C[..., :S1], y) [M, D, S1+S3],
+// c2 = C[..., S1:] [M, D, S2]; bf16, c1 and c2 contiguous; S1, S2, S3
+// multiples of 8 (whole 16-byte pieces per segment).
+int fused_gemm_afp4wfp4_split_cat(aiter_tensor_t* x, aiter_tensor_t* w, aiter_tensor_t* x_scale,
+                                  aiter_tensor_t* w_scale, aiter_tensor_t* y, aiter_tensor_t* c1, aiter_tensor_t* c2,
+                                  int S1, int S2, int preshuffled, const char* kernelName, aiter_stream_t stream) {
+    return safe_call([&] {
+        AA_CHECK(x && w && y && c1 && c2, "x, w, y, c1 and c2 must be given");
+        DeviceGuard g(x->device_id);
+        check_tensor(y, "y", 3);
+        AA_CHECK(y->ndim == 3 && y->dtype == AITER_DTYPE_bf16, "y must be [M, D, S3] bf16");
+        const int64_t M = y->shape[0], D = y->shape[1], S3 = y->shape[2];
+        AA_CHECK(rows_2d(x) == M, "x has ", rows_2d(x), " rows, y ", M);
+        AA_CHECK(S1 > 0 && S2 > 0 && S1 % 8 == 0 && S2 % 8 == 0 && S3 % 8 == 0,
+                 "S1, S2 and S3 must be positive multiples of 8 (got ", S1, ", ", S2, ", ", S3, ")");
+        AA_CHECK(c1->dtype == AITER_DTYPE_bf16 && c2->dtype == AITER_DTYPE_bf16, "c1 and c2 must be bf16");
+        const aiter_tensor_t c1v = flat_view(c1, M * D, S1 + S3, "c1");
+        (void)flat_view(c2, M * D, S2, "c2");
+        AA_CHECK(((uintptr_t)c1->ptr & 15) == 0 && ((uintptr_t)c2->ptr & 15) == 0, "c1 and c2 must be 16-byte aligned");
+        const int64_t N = D * (S1 + S2);
+        EpiOp e{};
+        e.kind = 2;
+        e.c2 = c2->ptr;
+        e.s1 = S1;
+        e.s2 = S2;
+        e.s3 = (int)S3;
+        e.ld1 = D * (S1 + S3);
+        e.ld2 = D * S2;
+        // the GEMM's own output descriptor: [M, N] at c1 (only its pointer is used)
+        aiter_tensor_t outv = c1v;
+        outv.ndim = 2;
+        outv.shape[0] = M;
+        outv.shape[1] = N;
+        outv.strides[0] = N;
+        outv.strides[1] = 1;
+        outv.numel = (size_t)(M * N);
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        fused_a4w4(x, w, x_scale, w_scale, preshuffled != 0, &outv, nullptr, e, kernelName, st);
+        const int64_t total = M * D * S3;
+        if (total > 0) {
+            split_cat_copy_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, st>>>(
+                static_cast<const uint16_t*>(y->ptr), y->strides[0], y->strides[1], y->strides[2],
+                static_cast<uint16_t*>(c1->ptr), (int)M, (int)D, S1, (int)S3);
+            AA_HIP(hipGetLastError());
+        }
+    });
+}
+
+// fused_gemm_afp4wfp4_a16w16 (aiter/ops/triton/gemm/fused/fused_gemm_afp4wfp4_a16w16.py:23-254):
+// y_fp4 = x_fp4 w_fp4^T (+ bias_fp4) and y_bf16 = x_bf16 w_bf16^T (+ bias_bf16)
+// over the same M and K, bf16 out; biases f32 [N]; two launches on `stream`.
+int fused_gemm_afp4wfp4_a16w16(aiter_tensor_t* x_fp4, aiter_tensor_t* w_fp4, aiter_tensor_t* x_fp4_scale,
+                               aiter_tensor_t* w_fp4_scale, aiter_tensor_t* bias_fp4, aiter_tensor_t* y_fp4,
+                               const char* kernel_fp4, aiter_tensor_t* x_bf16, aiter_tensor_t* w_bf16,
+                               aiter_tensor_t* bias_bf16, aiter_tensor_t* y_bf16, const char* kernel_bf16,
+                               int preshuffled, aiter_stream_t stream) {
+    return safe_call([&] {
+        AA_CHECK(x_fp4 && x_bf16, "x_fp4 and x_bf16 must be given");
+        DeviceGuard g(x_fp4->device_id);
+        check_tensor(x_fp4, "x_fp4", 2);
+        check_tensor(x_bf16, "x_bf16", 2);
+        AA_CHECK(rows_2d(x_fp4) == rows_2d(x_bf16), "x_fp4 and x_bf16 must have the same M");
+        AA_CHECK(cols_2d(x_fp4) * 2 == cols_2d(x_bf16), "x_fp4 and x_bf16 must have the same K");
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        fused_a4w4(x_fp4, w_fp4, x_fp4_scale, w_fp4_scale, preshuffled != 0, y_fp4, bias_fp4, EpiOp{}, kernel_fp4, st);
+        GemmCall c{kA16W16, {false, false, false}, x_bf16, w_bf16, nullptr, nullptr, y_bf16, bias_bf16,
+                   1.0f, 1.0f, kernel_bf16, -1, -1};
+        run_gemm(c, st);
+    });
 }
 
 // Pre-size the split-K workspace of (device, stream) before graph capture.

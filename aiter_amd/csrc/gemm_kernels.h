@@ -44,6 +44,27 @@ template <> struct OpTraits<kBf16> {
     static constexpr bool scaled = false;
 };
 
+// Output operation fused into the epilogue (fused_gemm_afp4wfp4_mul_add /
+// _split_cat of aiter/ops/triton/gemm/fused/), applied to the f32 result
+// after alpha and bias:
+//   kind 1 (mul_add): out = a * acc + b (fuse 0) or a * b + acc (fuse 1),
+//     a and b each a scalar or an [M, N] tensor (f32 or bf16, element strides);
+//   kind 2 (split_cat): column n of the [M, D*(S1+S2)] product goes to
+//     c1[m, d, s] (s < S1) or c2[m, d, s-S1] (d = n / (S1+S2), s = n % (S1+S2));
+//     p.D is c1 ([M, D, S1+S3] rows of ld1 elements), c2 has rows of ld2.
+struct EpiOp {
+    int kind;
+    int fuse;
+    const void* ta;   // mul_add tensors (null: the scalar sa / sb)
+    const void* tb;
+    int ta_bf16, tb_bf16;
+    int64_t ta_sm, ta_sn, tb_sm, tb_sn;
+    float sa, sb;
+    void* c2;
+    int s1, s2, s3;
+    int64_t ld1, ld2;
+};
+
 struct GemmParams {
     const uint8_t* A;
     const uint8_t* B;
@@ -64,7 +85,35 @@ struct GemmParams {
     // batched launches (gridDim.z = batch): per-batch offsets of A, B, D in
     // bytes and of the bias in elements (0: shared by every batch)
     int64_t bs_a, bs_b, bs_d, bs_bias;
+    EpiOp epi;
 };
+
+// element (m, n) of a mul_add operand
+AA_DEV float epi_operand(const void* t, int bf16, int64_t sm, int64_t sn, float scalar, int m, int n) {
+    if (!t) return scalar;
+    const int64_t off = (int64_t)m * sm + (int64_t)n * sn;
+    return bf16 ? bf16_bits_to_f32(static_cast<const uint16_t*>(t)[off]) : static_cast<const float*>(t)[off];
+}
+
+// mul_add on the four f32 values of row m, columns n..n+3 (all inside the output)
+AA_DEV void epi_mul_add(const GemmParams& p, float (&v)[4], int m, int n) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float a = epi_operand(p.epi.ta, p.epi.ta_bf16, p.epi.ta_sm, p.epi.ta_sn, p.epi.sa, m, n + r);
+        const float b = epi_operand(p.epi.tb, p.epi.tb_bf16, p.epi.tb_sm, p.epi.tb_sn, p.epi.sb, m, n + r);
+        v[r] = p.epi.fuse == 0 ? a * v[r] + b : a * b + v[r];
+    }
+}
+
+// split_cat destination of output element (m, n), in elements of `elem` bytes:
+// a run of columns that stays inside one S1 or S2 segment is contiguous there
+AA_DEV uint8_t* epi_split_dst(const GemmParams& p, int m, int n, int elem) {
+    const int seg = p.epi.s1 + p.epi.s2;
+    const int d = n / seg, s = n - d * seg;
+    if (s < p.epi.s1)
+        return static_cast<uint8_t*>(p.D) + ((int64_t)m * p.epi.ld1 + (int64_t)d * (p.epi.s1 + p.epi.s3) + s) * elem;
+    return static_cast<uint8_t*>(p.epi.c2) + ((int64_t)m * p.epi.ld2 + (int64_t)d * p.epi.s2 + (s - p.epi.s1)) * elem;
+}
 
 // moves the operand pointers to batch blockIdx.z (no-op for unbatched grids)
 AA_DEV void apply_batch(GemmParams& p) {
@@ -156,11 +205,14 @@ AA_DEV void store_frag(const GemmParams& p, f32x4_t acc, int m, int n) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) v[r] += p.beta * bp[r];
     }
+    if (p.epi.kind == 1) epi_mul_add(p, v, m, n);
     if constexpr (OUT_F32) {
-        float* d = static_cast<float*>(p.D) + (int64_t)m * p.ldd + n;
+        float* d = p.epi.kind == 2 ? reinterpret_cast<float*>(epi_split_dst(p, m, n, 4))
+                                   : static_cast<float*>(p.D) + (int64_t)m * p.ldd + n;
         *reinterpret_cast<f32x4_t*>(d) = f32x4_t{v[0], v[1], v[2], v[3]};
     } else {
-        uint16_t* d = static_cast<uint16_t*>(p.D) + (int64_t)m * p.ldd + n;
+        uint16_t* d = p.epi.kind == 2 ? reinterpret_cast<uint16_t*>(epi_split_dst(p, m, n, 2))
+                                      : static_cast<uint16_t*>(p.D) + (int64_t)m * p.ldd + n;
         typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
         *reinterpret_cast<u32x2_t*>(d) = u32x2_t{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
     }

@@ -86,8 +86,11 @@ AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f
 // live registers leave no room for all accumulator reads at once.  OUT_FP4
 // = true writes packed e2m1 (conversion scale 1, RNE, saturating: two values
 // per byte, the lower column in the low nibble; p.ldd still counts elements).
+// EPI = true adds, at run time, the bias and the fused output operation of
+// p.epi (mul_add on the f32 values; split_cat sends each 16-byte piece to
+// c1 or c2, which needs S1 and S2 to be multiples of a piece).
 template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false, bool FENCED = false,
-          bool OUT_FP4 = false>
+          bool OUT_FP4 = false, bool EPI = false>
 AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     static_assert(MA % MP == 0, "whole passes");
     static_assert(!(OUT_FP4 && OUT_F32), "one output format");
@@ -129,6 +132,17 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
                     }
+                    if constexpr (EPI) {
+                        // values of rows >= M / columns >= N are computed at a
+                        // clamped position and dropped by the store
+                        const int m = min(mb + i0 * 32 + r, p.M - 1), n = min(nb + nl, p.N - 4);
+                        if (p.bias) {
+                            const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
+                        }
+                        if (p.epi.kind == 1) epi_mul_add(p, v, m, n);
+                    }
                     const int byte = nl * EB2 / 2;
                     const int piece = (byte >> 4) ^ ((r >> RSH) & SWM);
                     if constexpr (OUT_FP4) {
@@ -150,16 +164,25 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
             const int r = rr + lane / P;
             const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
             const int m = mb + i0 * 32 + r;
+            if constexpr (EPI) {
+                if (p.epi.kind == 2) {
+                    if (m < p.M && n_out < p.N)
+                        *reinterpret_cast<i32x4_t*>(epi_split_dst(p, m, n_out, EB2 / 2)) = v;
+                    continue;
+                }
+            }
             const int off = col_off == 0x7fffffff ? col_off : m * (int)p.ldd * EB2 / 2 + col_off;
             __builtin_amdgcn_raw_buffer_store_b128(v, d_rsrc, off, 0, 0);
         }
     }
 }
 
-// the three epilogue flavours picked at run time (uniform branch)
+// the epilogue flavours picked at run time (uniform branch)
 template <int MA, int NB, int MP, bool OUT_F32>
 AA_DEV void store_block_any(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
-    if (p.bias)
+    if (p.epi.kind)
+        store_block<MA, NB, MP, false, true, OUT_F32, false, false, true>(p, acc, cb, lane, mb, nb);
+    else if (p.bias)
         store_block<MA, NB, MP, true, true, OUT_F32>(p, acc, cb, lane, mb, nb);
     else if (p.alpha != 1.0f)
         store_block<MA, NB, MP, false, true, OUT_F32>(p, acc, cb, lane, mb, nb);

@@ -200,6 +200,41 @@ int mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* ScaleA,
                    aiter_tensor_t* out, aiter_tensor_t* out_scale, const char* kernelName, int a_preshuffle,
                    aiter_stream_t stream);
 
+/* ---- fused GEMM + output operation: the Triton ops of
+ * aiter/ops/triton/gemm/fused/fused_gemm_afp4wfp4_{mul_add,split_cat,a16w16}.py
+ * (no C entry in the reference; these are what their host code would bind).
+ * x [M, K/2] e2m1; w [N, K/2] row-major, or (preshuffled != 0) the
+ * shuffle_weight bytes in any shape (the Triton ops pass [N/16, K*8]).
+ * Scales: plain [R, K/32] e8m0 when not preshuffled; when preshuffled, w's
+ * are the shuffle_scale bytes in any shape (Triton: [N/32, K]) and x's too
+ * when M >= 32, plain below.  Plain scales are shuffled into a library
+ * workspace first (so a graph capture needs one eager call of the shape).
+ * kernelName: an A4W4 instance of this library or NULL for the heuristic. */
+/* fused_gemm_afp4wfp4_mul_add.py:63-236 and _preshuffle_add_mul :239-:
+ * out [M, N] bf16 = a * (x w^T) + b (fuse_type 0) or a * b + x w^T (1) in f32;
+ * a / b: f32 or bf16 tensors broadcastable to [M, N] (one element = scalar)
+ * or NULL for a_scalar / b_scalar. */
+int fused_gemm_afp4wfp4_mul_add(aiter_tensor_t* x, aiter_tensor_t* w, aiter_tensor_t* x_scale,
+                                aiter_tensor_t* w_scale, aiter_tensor_t* a, float a_scalar, aiter_tensor_t* b,
+                                float b_scalar, int fuse_type, aiter_tensor_t* out, int preshuffled,
+                                const char* kernelName, aiter_stream_t stream);
+/* fused_gemm_afp4wfp4_split_cat.py:19-196 and _preshuffle_split_cat :199-:
+ * C = x w^T viewed [M, D, S1+S2]; c1 [M, D, S1+S3] = cat(C[..., :S1], y),
+ * c2 [M, D, S2] = C[..., S1:]; y [M, D, S3]; bf16; c1, c2 contiguous;
+ * S1, S2, S3 multiples of 8. */
+int fused_gemm_afp4wfp4_split_cat(aiter_tensor_t* x, aiter_tensor_t* w, aiter_tensor_t* x_scale,
+                                  aiter_tensor_t* w_scale, aiter_tensor_t* y, aiter_tensor_t* c1,
+                                  aiter_tensor_t* c2, int S1, int S2, int preshuffled, const char* kernelName,
+                                  aiter_stream_t stream);
+/* fused_gemm_afp4wfp4_a16w16.py:23-254: y_fp4 = x_fp4 w_fp4^T (+ bias_fp4) and
+ * y_bf16 = x_bf16 w_bf16^T (+ bias_bf16), same M and K, bf16 out, biases f32
+ * [N] or NULL; w_bf16 row-major [N_bf16, K]; two launches on `stream`. */
+int fused_gemm_afp4wfp4_a16w16(aiter_tensor_t* x_fp4, aiter_tensor_t* w_fp4, aiter_tensor_t* x_fp4_scale,
+                               aiter_tensor_t* w_fp4_scale, aiter_tensor_t* bias_fp4, aiter_tensor_t* y_fp4,
+                               const char* kernel_fp4, aiter_tensor_t* x_bf16, aiter_tensor_t* w_bf16,
+                               aiter_tensor_t* bias_bf16, aiter_tensor_t* y_bf16, const char* kernel_bf16,
+                               int preshuffled, aiter_stream_t stream);
+
 /* ---- fused MoE (MXFP4 weights, per-1x32 e8m0 scales) ---------------------
  * Routing sort: replaces moe_sorting_fwd (aiter/ops/moe_sorting.py:12-27,
  * called from aiter/fused_moe.py:171-285).  topk_ids int32 [M, topk],

@@ -451,6 +451,36 @@ def gemm_a4w4_ref(a_packed, b_packed, a_scale, b_scale) -> np.ndarray:
     return f32_to_bf16_bits(a @ b.T)
 
 
+def gemm_a4w4_f32(a_packed, b_packed, a_scale, b_scale) -> np.ndarray:
+    """The f32 product of ``gemm_a4w4_ref`` before its bf16 rounding (plain scales)."""
+    return dequant_mxfp4(a_packed, a_scale) @ dequant_mxfp4(b_packed, b_scale).T
+
+
+def mul_add_ref(c, a, b, fuse_type: int) -> np.ndarray:
+    """Epilogue of fused_gemm_afp4wfp4_mul_add
+    (aiter/ops/triton/_triton_kernels/gemm/fused/fused_gemm_afp4wfp4_mul_add.py:190-219):
+    with the f32 product ``c``, ``a * c + b`` (fuse_type 0) or ``a * b + c``
+    (fuse_type 1) in f32, then bf16 bits.  ``a``/``b``: numbers or arrays that
+    broadcast to ``c``."""
+    c = np.asarray(c, dtype=np.float32)
+    a = np.asarray(a, dtype=np.float32)
+    b = np.asarray(b, dtype=np.float32)
+    out = a * c + b if fuse_type == 0 else a * b + c
+    return f32_to_bf16_bits(out.astype(np.float32))
+
+
+def split_cat_ref(c, y, s1: int, s2: int):
+    """fused_gemm_afp4wfp4_split_cat (aiter/ops/triton/gemm/fused/fused_gemm_afp4wfp4_split_cat.py:35-39):
+    ``c`` [M, D*(S1+S2)] viewed [M, D, S1+S2] is split into [..., :S1] and
+    [..., S1:], and ``y`` [M, D, S3] is concatenated to the first part.
+    Returns (c1 [M, D, S1+S3], c2 [M, D, S2]) of the dtype of ``c``."""
+    c = np.asarray(c)
+    y = np.asarray(y)
+    m, d = y.shape[0], y.shape[1]
+    v = c.reshape(m, d, s1 + s2)
+    return np.concatenate([v[:, :, :s1], y.astype(c.dtype)], axis=2), np.ascontiguousarray(v[:, :, s1:])
+
+
 def gemm_a8w4_ref(a_q, b_packed, a_scale, b_scale) -> np.ndarray:
     """MXFP8 x MXFP4: same structure with an e4m3 A (no gfx950 reference
     kernel exists; semantics from the MX spec and the gfx1250 API

@@ -75,7 +75,7 @@ def _run(fam, name, a, b, sa, sb, m, n, cuda, bias=None, alpha=1.0, b_pre=True):
         out = aiter_amd.gemm_a8w4_mxfp8(a.view(torch.float8_e4m3fn), b, sa, sb, a_preshuffle=False, kernelName=name)
     else:
         out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
-        aiter_amd.gemm_a16w16_asm(a, b, out, bias=bias, kernelName=name, bpreshuffle=True)
+        aiter_amd.gemm_a16w16_asm(a, b, out, bias=bias, kernelName=name, bpreshuffle=b_pre)
     torch.cuda.synchronize()
     return out
 
@@ -83,7 +83,9 @@ def _run(fam, name, a, b, sa, sb, m, n, cuda, bias=None, alpha=1.0, b_pre=True):
 @pytest.mark.parametrize("row", ROWS, ids=IDS)
 def test_persist_matches_twin(cuda, row):
     name, fam, b_pre = row[1], row[2], bool(row[8])
-    twin = name[: -len("_persist")]
+    # the one-tile-per-workgroup kernel of the same tile (the LDS-staged bf16
+    # tile's twin is the plain tile name of its B layout)
+    twin = name[: -len("_persist")].replace("_lds", "")
     for i, (m, n, k) in enumerate(_shapes(row)):
         announce(f"persist {name} vs {twin} {m}x{n}x{k}")
         a, b, sa, sb = _operands(fam, m, n, k, cuda, seed=40 + i)

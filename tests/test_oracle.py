@@ -419,3 +419,39 @@ def test_torch_ref_gemm_matches_numpy_oracle():
     # results equal or one bf16 step apart
     diff = np.abs(got.astype(np.int32) - ref.astype(np.int32))
     assert diff.max() <= 1 and np.mean(diff == 0) > 0.99
+
+
+def test_mul_add_ref_known_answers():
+    """fused mul_add epilogue: hand-computed values of both fuse types with
+    scalar and matrix operands (all exact in bf16)."""
+    c = np.array([[1.0, 2.0], [3.0, 4.0]], dtype=np.float32)
+    bm = np.array([[1.0, 1.0], [0.0, -1.0]], dtype=np.float32)
+    got0 = O.bf16_bits_to_f32(O.mul_add_ref(c, 2.0, bm, 0))
+    assert np.array_equal(got0, np.array([[3.0, 5.0], [6.0, 7.0]], dtype=np.float32))
+    got1 = O.bf16_bits_to_f32(O.mul_add_ref(c, 2.0, 3.0, 1))
+    assert np.array_equal(got1, np.array([[7.0, 8.0], [9.0, 10.0]], dtype=np.float32))
+    am = np.array([[0.5, -1.0], [2.0, 0.0]], dtype=np.float32)
+    got2 = O.bf16_bits_to_f32(O.mul_add_ref(c, am, bm, 0))
+    assert np.array_equal(got2, np.array([[1.5, -1.0], [6.0, -1.0]], dtype=np.float32))
+    # a = 1, b = 0 is the plain GEMM rounding
+    r = np.random.default_rng(0).standard_normal((3, 5)).astype(np.float32)
+    assert np.array_equal(O.mul_add_ref(r, 1.0, 0.0, 0), O.f32_to_bf16_bits(r))
+    assert np.array_equal(O.mul_add_ref(r, 0.0, 7.0, 1), O.f32_to_bf16_bits(r))
+
+
+def test_split_cat_ref_known_answer_and_inverse():
+    """fused split_cat: a hand-worked [1, 2*(2+1)] case, then on random data
+    the parts reassemble the product and carry y unchanged."""
+    c = np.arange(6, dtype=np.float32).reshape(1, 6)
+    y = np.array([[[10.0], [11.0]]], dtype=np.float32)
+    c1, c2 = O.split_cat_ref(c, y, 2, 1)
+    assert np.array_equal(c1, np.array([[[0, 1, 10], [3, 4, 11]]], dtype=np.float32))
+    assert np.array_equal(c2, np.array([[[2], [5]]], dtype=np.float32))
+    rs = np.random.default_rng(1)
+    m, d, s1, s2, s3 = 3, 4, 8, 16, 8
+    c = rs.standard_normal((m, d * (s1 + s2))).astype(np.float32)
+    y = rs.standard_normal((m, d, s3)).astype(np.float32)
+    c1, c2 = O.split_cat_ref(c, y, s1, s2)
+    assert c1.shape == (m, d, s1 + s3) and c2.shape == (m, d, s2)
+    assert np.array_equal(np.concatenate([c1[:, :, :s1], c2], axis=2).reshape(m, -1), c)
+    assert np.array_equal(c1[:, :, s1:], y)
