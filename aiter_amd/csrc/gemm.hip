@@ -268,6 +268,8 @@ std::vector<Instance>& registry() {
         persist(kA16W16, 256, b16r, launch_lds_persist<false>, "a16w16");
         persist(kA16W16, 256, b16p, launch_lds_persist<true>, "a16w16");
         reg.back().name = "a16w16_tile_256x256_lds_persist";
+        // ---- A4W4 64-row skinny with 32 columns per workgroup ----
+        skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false, 2>, "a4w4", 32);
     });
     return reg;
 }

@@ -536,7 +536,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
         for (int j = 0; j < NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     // software pipeline: the next pair's loads are in flight while the
-    // current pair is multiplied
+    // current pair is multiplied (a deeper register ring measured slower on
+    // the bf16 decode shapes)
     auto run = [&](auto bh) {
         constexpr int BH = decltype(bh)::value;
         int pr = p_begin + wave;

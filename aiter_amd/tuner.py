@@ -50,6 +50,7 @@ from .shuffle import shuffle_weight
 
 E2M1 = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0]
 ROTATE_BYTES = 600 << 20
+VERBOSE = os.environ.get("AITER_TUNE_VERBOSE", "0") not in ("", "0")   # log every candidate's time
 MAX_COPIES = 64
 
 # BASELINE dispatch sweep: (N, K) x M, plus the decode / prefill / mixed shapes
@@ -212,6 +213,8 @@ def tune_mx(family: str, M: int, N: int, K: int, iters: int, max_err_ratio: floa
             _log(f"  reject {name} split {l2}: errRatio {er:.4f}")
             continue
         t = time_rotated(run, n_copies, iters)
+        if VERBOSE:
+            _log(f"  {name} split {l2}: {t * 1e6:.2f} us")
         if best is None or t < best[0]:
             best = (t, kid, name, l2, er)
     del wq, ws
@@ -262,6 +265,8 @@ def tune_bf16(M: int, N: int, K: int, bias: bool, otype: torch.dtype, bpreshuffl
             _log(f"  reject {name} split {split}: errRatio {er:.4f}")
             continue
         t = time_rotated(run, n_copies, iters)
+        if VERBOSE:
+            _log(f"  {name} split {split}: {t * 1e6:.2f} us")
         if best is None or t < best[0]:
             best = (t, kid, name, split, er)
     del wb
