@@ -400,7 +400,20 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
 
     // prologue: B stages 0, 1 first, then A stages 0..NS-2 (so that at the loop
     // head at least as many loads follow each B load as in the steady state,
-    // and the compiler's B waits there stay as loose as in the loop); wait for A 0
+    // and the compiler's B waits there stay as loose as in the loop).
+    // The wait at the end of stage t (vmcnt WAIT_N) publishes the copies of
+    // stage t+1 only if at least WAIT_N loads were issued after them.  For a
+    // copy issued here (stage t+1 <= NS-2) that is (NS-3-t)*NDMA later
+    // prologue copies + t whole stages + the NDMA + 3*NB loads of stage t
+    // before its wait, fewer than WAIT_N for the first stages of a 4-slot ring
+    // (stage 1: 2*NDMA + 3*NB).  Those copies are waited for here, with
+    // stage 0's: they were issued right after it.
+    constexpr int PRO_WAITED = [] {
+        int d = 0;
+        for (int t = 0; t + 1 <= NS - 2; ++t)
+            if ((NS - 3 - t) * NDMA + t * LOADS_ITER + NDMA + 3 * NB < WAIT_N) d = t + 1;
+        return d;
+    }();
 #pragma unroll
     for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -412,7 +425,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t) dma_stage(t);
     __builtin_amdgcn_sched_barrier(0);
-    wait_vmcnt<(NS - 2) * NDMA>();
+    wait_vmcnt<(NS - 2 - PRO_WAITED) * NDMA>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");

@@ -1,0 +1,198 @@
+"""CPU model of the vector-memory issue order of the LDS-ring GEMM kernels.
+
+The tile kernels copy A (and the e8m0 scales, and in gemm_t32.h B too) into a
+ring of LDS slots with ``buffer_load ... lds`` and publish a slot with
+``s_waitcnt vmcnt(N)`` + ``s_barrier``: vmcnt(N) returns once at most the N
+most recently issued vector-memory operations of the wave are outstanding, so
+the copies of the stage being published are complete only if at least N
+operations were issued after them.  The counts N are compile-time constants
+sized for the steady state of the loop; the prologue and the tile
+transitions issue fewer operations between a copy and its wait.  This model
+replays each kernel's issue order per wave (register loads of B, ring copies,
+epilogue stores) with the kernels' own constants and checks that every wait
+that precedes reads of a slot covers that slot's copies.  Inside a k-step
+region the compiler may order the region's loads freely, so the model issues
+a region's copies last (the fewest followers).
+
+Kernels modelled: gemm_flat.h ``flat_body`` (prologue and main loop),
+gemm_t32.h ``gemm_t32_kernel``, gemm_flat_persist.h (prologue, tile
+transitions).  A wrong count here (the flat kernel's former prologue wait of
+(NS - 2) * NDMA) lets the first stage read a slot whose copies may still be
+in flight: a timing-dependent wrong tile.
+"""
+import pytest
+
+
+class Wave:
+    """Issued vector-memory operations of one wave and what the waits so far
+    guarantee complete."""
+
+    def __init__(self):
+        self.n = 0
+        self.done = 0          # operations [0, done) are complete
+        self.ops = {}
+
+    def issue(self, tag, k=1):
+        for _ in range(k):
+            self.ops.setdefault(tag, []).append(self.n)
+            self.n += 1
+
+    def wait(self, vmcnt):
+        self.done = max(self.done, self.n - vmcnt)
+
+    def complete(self, tag):
+        return all(i < self.done for i in self.ops.get(tag, []))
+
+
+def _parts(ndma):
+    """sizes of the three dma_part calls of a stage"""
+    dp = (ndma + 2) // 3
+    return [max(0, min(ndma, (p + 1) * dp) - p * dp) for p in range(3)]
+
+
+def flat_prologue_wait(ns, ndma, nb):
+    """gemm_flat.h: vmcnt of the prologue wait, (NS - 2 - PRO_WAITED) * NDMA"""
+    nbl = 4 * nb
+    loads_iter = ndma + nbl
+    wait_n = (ns - 3) * loads_iter + ndma + 3 * nb if ns >= 3 else 0
+    waited = 0
+    for t in range(ns - 2):
+        if (ns - 3 - t) * ndma + t * loads_iter + ndma + 3 * nb < wait_n:
+            waited = t + 1
+    return (ns - 2 - waited) * ndma
+
+
+def run_flat(ns, ndma, nb, nstages, prologue_wait=flat_prologue_wait):
+    """flat_body: B stages 0, 1 into registers, copies of stages 0..NS-2, the
+    prologue wait; stage t: three regions (B of stage t+2 k-step r, copies of
+    stage t+NS-1 part r), the publishing wait (WAIT_N) for stage t+1, then
+    B k-step 3.  Returns the stages whose publishing wait does not cover
+    their copies."""
+    nbl = 4 * nb
+    wait_n = (ns - 3) * (ndma + nbl) + ndma + 3 * nb if ns >= 3 else 0
+    w = Wave()
+    w.issue(("B", 0), nbl)
+    w.issue(("B", 1), nbl)
+    for t in range(ns - 1):
+        w.issue(("A", t), ndma)
+    w.wait(prologue_wait(ns, ndma, nb))
+    bad = [] if w.complete(("A", 0)) else [0]
+    for t in range(nstages + nstages % 2):
+        for r, k in enumerate(_parts(ndma)):
+            w.issue(("B", t + 2), nb)
+            w.issue(("A", t + ns - 1), k)
+        w.wait(wait_n)
+        if not w.complete(("A", t + 1)):
+            bad.append(t + 1)
+        w.issue(("B", t + 2), nb)
+    return bad
+
+
+def run_t32(ns, ndma, nstages):
+    """gemm_t32_kernel: only ring copies (A, B and scales) per stage"""
+    wait_n = (ns - 2) * ndma if ns >= 3 else 0
+    w = Wave()
+    for t in range(ns - 1):
+        w.issue(("A", t), ndma)
+    w.wait((ns - 2) * ndma)
+    bad = [] if w.complete(("A", 0)) else [0]
+    for t in range(nstages):
+        for k in _parts(ndma):
+            w.issue(("A", t + ns - 1), k)
+        w.wait(wait_n)
+        if not w.complete(("A", t + 1)):
+            bad.append(t + 1)
+    return bad
+
+
+def run_persist(ndma, nb, nst, nstages, tiles):
+    """gemm_flat_persist.h: 4-slot ring; prologue copies of stages 0, 1, B of
+    stages 0, 1, copies of stage 2, NST stand-in stores; per tile nst4 stages
+    whose look-ahead moves to the next tile in the last stages (copies from
+    stage nst4-3, B from stage nst4-2); epilogue NST stores.  Waits: WAIT_T
+    for the first two stages of a tile, WAIT_N after."""
+    nbl = 4 * nb
+    loads_iter = ndma + nbl
+    wait_n = loads_iter + ndma + 3 * nb
+    wait_t = min(63, wait_n + nst)
+    wait_p = min(63, 2 * ndma + 2 * nbl + nst)
+    nst4 = 8 if nstages <= 8 else (nstages + 3) & ~3
+    w = Wave()
+    for t in range(2):
+        w.issue(("A", 0, t), ndma)
+    w.issue(("B", 0, 0), nbl)
+    w.issue(("B", 0, 1), nbl)
+    w.issue(("A", 0, 2), ndma)
+    w.issue("st", nst)
+    w.wait(wait_p)
+    bad = [] if w.complete(("A", 0, 0)) else [(0, 0)]
+    for it in range(tiles):
+        for t in range(nst4):
+            dt = (it, t + 3) if t + 3 < nst4 else (it + 1, t + 3 - nst4)
+            bt = (it, t + 2) if t + 2 < nst4 else (it + 1, t + 2 - nst4)
+            for k in _parts(ndma):
+                w.issue(("B",) + bt, nb)
+                w.issue(("A",) + dt, k)
+            w.wait(wait_t if t < 2 else wait_n)
+            pub = (it, t + 1) if t + 1 < nst4 else (it + 1, 0)
+            if not w.complete(("A",) + pub):
+                bad.append(pub)
+            w.issue(("B",) + bt, nb)
+        w.issue("st", nst)
+        w.wait(63)
+    return bad
+
+
+def _flat_cfg(ka, bm):
+    """FlatCfg<KA, BM>: (NS, NDMA) with NB = 2 B tiles per wave"""
+    mx = ka != "bf16"
+    fa = 2 if ka == "fp8" else 1
+    a_ch = bm // 8 * fa
+    stage_kb = a_ch + (4 if mx else 0)
+    ns = min(4, 160 // stage_kb)
+    return ns, a_ch // 4 + (1 if mx else 0)
+
+
+FLAT_CFGS = [("fp4", 32), ("fp4", 64), ("fp4", 128), ("fp4", 256), ("fp8", 32), ("fp8", 64), ("fp8", 128),
+             ("bf16", 128), ("bf16", 256)]
+
+
+@pytest.mark.parametrize("ka,bm", FLAT_CFGS)
+@pytest.mark.parametrize("nstages", [1, 2, 3, 4, 7, 28])
+def test_flat_kernel_waits_cover_every_stage(ka, bm, nstages):
+    ns, ndma = _flat_cfg(ka, bm)
+    assert run_flat(ns, ndma, 2, nstages) == []
+
+
+@pytest.mark.parametrize("ns", [2, 3, 4])
+@pytest.mark.parametrize("ndma", list(range(1, 10)))
+def test_flat_kernel_waits_any_ring(ns, ndma):
+    assert run_flat(ns, ndma, 2, 12) == []
+
+
+def test_flat_model_catches_a_short_prologue_wait():
+    """The former prologue wait, (NS - 2) * NDMA, covers stage 0 only; with a
+    4-slot ring the first stage's wait then does not cover stage 1."""
+    def old(ns, ndma, nb):
+        return (ns - 2) * ndma
+
+    ns, ndma = _flat_cfg("fp4", 32)
+    assert ns == 4
+    assert run_flat(ns, ndma, 2, 8, prologue_wait=old) == [1]
+    assert run_flat(*_flat_cfg("fp8", 128), 2, 8, prologue_wait=old) == [1]
+
+
+@pytest.mark.parametrize("ns", [2, 3, 4])
+@pytest.mark.parametrize("ndma", list(range(1, 17)))
+def test_t32_kernel_waits(ns, ndma):
+    assert run_t32(ns, ndma, 10) == []
+
+
+@pytest.mark.parametrize("ka,bm", [("fp4", 256), ("fp4", 128), ("fp8", 256), ("bf16", 256)])
+@pytest.mark.parametrize("eb2", [1, 4, 8])
+@pytest.mark.parametrize("nstages", [2, 8, 9, 32])
+def test_persistent_kernel_waits(ka, bm, eb2, nstages):
+    fa = 2 if ka == "fp8" else 1
+    ndma = bm // 8 * fa // 4 + (0 if ka == "bf16" else 1)
+    nst = bm * 64 * eb2 // 2048
+    assert run_persist(ndma, 2, nst, nstages, tiles=3) == []
