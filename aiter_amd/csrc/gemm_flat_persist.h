@@ -61,6 +61,13 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     constexpr int STAGE_BYTES = Cfg::STAGE_KB * 1024;
     constexpr int A_ROW_BYTES = 128 * FA;
     constexpr int EB2 = OUT_FP4 ? 1 : (OUT_F32 ? 8 : 4);   // output bytes per two elements
+    // MX: the paired tile layout (swap45 in mfma32.h): MFMA tile 2p+b of a
+    // wave takes rows 16b..16b+15 of the 32-row groups 2p and 2p+1 (B: columns
+    // 16j..16j+15 of the wave's two 32-column groups), so every lane of a tile
+    // uses byte b (+2) of the same two shuffled-scale dwords and a tile pair
+    // shares them: two dword reads per pair and stage, no byte shuffle
+    constexpr bool PAIRED = MX;
+    static_assert(!PAIRED || MA % 2 == 0, "tile pairs");
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES];
 
@@ -86,11 +93,12 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     int b_off[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        const int b16 = 4 * wave + 2 * j + ((lane >> 4) & 1);
+        const int b16 = 4 * wave + (PAIRED ? 2 * ((lane >> 4) & 1) + j : 2 * j + ((lane >> 4) & 1));
+        const int col = 64 * wave + (PAIRED ? swap45(32 * j + (lane & 31)) : 32 * j + (lane & 31));
         if constexpr (BPRE)
             b_off[j] = b16 * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
         else
-            b_off[j] = (64 * wave + 32 * j + (lane & 31)) * (int)p.ldb + (lane >> 5) * 16;
+            b_off[j] = col * (int)p.ldb + (lane >> 5) * 16;
     }
     // whole-tensor descriptors: rows past M / N and groups past the scale
     // tensors read zeros
@@ -101,7 +109,19 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     const bool sc_is_b = wave >= SCA && wave < SCA + 2;
     const int sc_chunk = sc_is_a ? wave : (sc_is_b ? wave - SCA : 0);
     const int sc_stride = sc_is_b ? (int)p.sb_stride : (int)p.sa_stride;
-    const int sc_off = (4 * sc_chunk + (lane >> 4)) * 32 * sc_stride + (lane & 15) * 16;
+    // chunk = 4 groups x 256 B.  Paired: the two groups of a pair interleave
+    // by 128-byte halves (even group's first half, odd group's first half,
+    // even's second, odd's second), the odd group's 64-byte quarters swapped:
+    // a lane's two dwords are then 256 B apart for every lane, and the 64
+    // lanes of a read spread over the banks (32 or 64 of them)
+    int sc_off;
+    if constexpr (PAIRED) {
+        const int pos = lane & 31, o = (pos >> 3) & 1;
+        const int k = (pos >> 4) * 8 + ((pos & 7) ^ (o * 4));
+        sc_off = (4 * sc_chunk + 2 * (lane >> 5) + o) * 32 * sc_stride + k * 16;
+    } else {
+        sc_off = (4 * sc_chunk + (lane >> 4)) * 32 * sc_stride + (lane & 15) * 16;
+    }
     const __amdgpu_buffer_rsrc_t sc_rsrc =
         sc_is_a ? make_rsrc(p.As, (int64_t)p.sa_groups * 32 * p.sa_stride)
                 : (sc_is_b ? make_rsrc(p.Bs, (int64_t)p.sb_groups * 32 * p.sb_stride) : null_rsrc);
@@ -119,7 +139,8 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         nst = it < my_tiles ? nstages : 0;
     };
 
-    const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;
+    const int pos0 = PAIRED ? ((lane >> 4) & 1) * 128 + ((((lane >> 5) * 64) + (lane & 15) * 4) ^ (((lane >> 4) & 1) * 64))
+                            : ((lane & 15) + 16 * (lane >> 5)) * 4;
     const unsigned sc_perm = 0x06040200u + ((lane >> 4) & 1) * 0x01010101u;
 
     i32x4_t af[2][MA][FA];
@@ -135,7 +156,10 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         return v;
     };
     const int ar = lane & 31;
-    const int a_lane_off = (ar >> 3) * 1024 + (ar & 7) * 128;
+    // paired: MFMA row ar of tile 2p+b is row swap45(32(2p+b) + ar), in 8-row
+    // chunk 8p + 2b + 4(ar>>4) + ((ar>>3)&1); the swizzle (row>>1)&7 is the same
+    const int a_lane_off = PAIRED ? (4 * ((ar >> 4) & 1) + ((ar >> 3) & 1)) * 1024 + (ar & 7) * 128
+                                  : (ar >> 3) * 1024 + (ar & 7) * 128;
     const int a_swz = (ar >> 1) & 7;
     auto read_a = [&](auto slot_c, int s, int reg) {
         const uint8_t* base = smem + slot_off(slot_c);
@@ -146,12 +170,24 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
                 const int piece = (FA == 1) ? (2 * s + (lane >> 5)) : ((4 * s + 2 * h + (lane >> 5)) & 7);
                 const int hh = (FA == 1) ? 0 : ((4 * s + 2 * h) >> 3);
                 af[reg][i][h] = *reinterpret_cast<const i32x4_t*>(
-                    base + (hh * (BM / 8) + i * 4) * 1024 + a_lane_off + ((piece ^ a_swz) * 16));
+                    base + (hh * (BM / 8) + (PAIRED ? (i >> 1) * 8 + (i & 1) * 2 : i * 4)) * 1024 + a_lane_off +
+                    ((piece ^ a_swz) * 16));
             }
     };
     auto read_scales = [&](auto slot_c, int (&pa)[MA], int (&pb)[NB]) {
         if constexpr (!MX) return;
         const uint8_t* base = smem + slot_off(slot_c) + A_CH * 1024 + pos0;
+        if constexpr (PAIRED) {
+            // pair p: dwords d0 (k-steps 0, 2) and d1 (1, 3) -> pa[2p], pa[2p+1]
+#pragma unroll
+            for (int q = 0; q < MA / 2; ++q) {
+                pa[2 * q] = *reinterpret_cast<const int*>(base + q * 512);
+                pa[2 * q + 1] = *reinterpret_cast<const int*>(base + q * 512 + 256);
+            }
+            pb[0] = *reinterpret_cast<const int*>(base + SCA * 1024 + wave * 512);
+            pb[1] = *reinterpret_cast<const int*>(base + SCA * 1024 + wave * 512 + 256);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < MA; ++i) {
             const unsigned d0 = *reinterpret_cast<const unsigned*>(base + i * 256);
@@ -253,12 +289,29 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         auto mma = [&](int areg, int bpar, auto sel) {
             constexpr int s = decltype(sel)::value;
             constexpr int osel = (s == 0) ? 0 : (s == 1) ? 2 : (s == 2) ? 1 : 3;
+            if constexpr (PAIRED) {
+                // tile 2q+b: byte b + 2(s/2) of dword d(s%2) of pair q (B: tile j, byte j + 2(s/2))
+                constexpr int o = 2 * (s >> 1);
 #pragma unroll
-            for (int i = 0; i < MA; ++i)
+                for (int i = 0; i < MA; ++i) {
+                    const int sa = sa_pk[2 * (i >> 1) + (s & 1)], sb = sb_pk[s & 1];
+                    const i32x4_t &a0 = af[areg][i][0], &a1 = af[areg][i][FA - 1];
+                    if (i & 1) {
+                        acc[i][0] = mma32x<KA, 1 + o, 0 + o>(bq[bpar][0][s], a0, a1, acc[i][0], sa, sb);
+                        acc[i][1] = mma32x<KA, 1 + o, 1 + o>(bq[bpar][1][s], a0, a1, acc[i][1], sa, sb);
+                    } else {
+                        acc[i][0] = mma32x<KA, 0 + o, 0 + o>(bq[bpar][0][s], a0, a1, acc[i][0], sa, sb);
+                        acc[i][1] = mma32x<KA, 0 + o, 1 + o>(bq[bpar][1][s], a0, a1, acc[i][1], sa, sb);
+                    }
+                }
+            } else {
 #pragma unroll
-                for (int j = 0; j < NB; ++j)
-                    acc[i][j] = mma32<KA, osel>(bq[bpar][j][s], af[areg][i][0], af[areg][i][FA - 1], acc[i][j], sa_pk[i],
-                                                sb_pk[j]);
+                for (int i = 0; i < MA; ++i)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+                        acc[i][j] = mma32<KA, osel>(bq[bpar][j][s], af[areg][i][0], af[areg][i][FA - 1], acc[i][j],
+                                                    sa_pk[i], sb_pk[j]);
+            }
         };
         // stage t (ring slot SLOT = t % 4) of the current tile; look-ahead: copies
         // of stage dt of tile (da, dsc, dnst) into slot SLOT+3, B of stage bt of
@@ -343,7 +396,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         // epilogue through ring slot 3: every wave finished reading it before
         // the last stage's barrier, and its next copy is issued in the next
         // tile's first stage, after the barrier below
-        store_block<MA, NB, EP_MP, false, SCALED, OUT_F32, true, OUT_FP4>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
+        store_block<MA, NB, EP_MP, false, SCALED, OUT_F32, true, OUT_FP4, false, PAIRED>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
                                                               lane, cm0, cn0 + wave * 64);
         wait_vmcnt_lgkm0<63>();
         asm volatile("" ::: "memory");

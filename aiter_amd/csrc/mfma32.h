@@ -13,6 +13,8 @@
 // l supplies the e8m0 byte of (row l%32, block 2s + l/32) for k-step s of a
 // 256-element window, selected from a 32-bit register by op_sel (byte 0..3).
 #pragma once
+#include <type_traits>
+
 #include "gemm_kernels.h"
 #include "mx_quant.h"
 
@@ -51,8 +53,34 @@ AA_DEV void wait_vmcnt_lgkm0() {
 // One k-step of a 32x32 MFMA tile: src0 = B fragment (16 bytes per lane),
 // src1 = A fragment(s) (two 16-byte halves for e4m3), packed scale bytes with
 // op_sel OSEL for the MX kinds.  Result lane l holds C[m = l%32][n = 8q + 4(l/32) + r].
+template <int KA, int OSEL_A, int OSEL_B>
+AA_DEV f32x16v_t mma32x(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f32x16v_t c, int sa, int sb);
+
 template <int KA, int OSEL>
 AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f32x16v_t c, int sa, int sb) {
+    return mma32x<KA, OSEL, OSEL>(b, a0, a1, c, sa, sb);
+}
+
+// f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time indices)
+template <int N, typename F, int I = 0>
+AA_DEV void static_for(F&& f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<N, F, I + 1>(static_cast<F&&>(f));
+    }
+}
+
+// Row / column order of the "paired" tile layout: MFMA row (column) x of a
+// 64-row (64-column) block holds row (column) swap45(x), i.e. bits 4 and 5 of
+// the index exchanged.  Tile 2p+b then takes rows 16b..16b+15 of the 32-row
+// groups 2p and 2p+1, so all its lanes read e8m0 byte b (+2) of the same
+// shuffled-scale dwords (the scale of row r sits in byte (r%32)/16), and a
+// pair of tiles shares one dword pair: no per-lane byte shuffle.
+AA_DEV constexpr int swap45(int x) { return (x & ~48) | ((x & 16) << 1) | ((x & 32) >> 1); }
+
+// As mma32, with separate op_sel byte selections for the A and B scales.
+template <int KA, int OSEL_A, int OSEL_B>
+AA_DEV f32x16v_t mma32x(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f32x16v_t c, int sa, int sb) {
     if constexpr (KA == kBf16) {
         typedef __bf16 bf16x8v_t __attribute__((ext_vector_type(8)));
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8v_t, b), __builtin_bit_cast(bf16x8v_t, a0),
@@ -67,7 +95,7 @@ AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f
         } else {
             av[4] = 0; av[5] = 0; av[6] = 0; av[7] = 0;
         }
-        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, c, 4, OpTraits<KA>::fmt, OSEL, sb, OSEL, sa);
+        return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(bv, av, c, 4, OpTraits<KA>::fmt, OSEL_B, sb, OSEL_A, sa);
     }
 }
 
@@ -88,12 +116,15 @@ AA_DEV f32x16v_t mma32(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f
 // per byte, the lower column in the low nibble; p.ldd still counts elements).
 // EPI = true adds, at run time, the bias and the fused output operation of
 // p.epi (mul_add on the f32 values; split_cat sends each 16-byte piece to
-// c1 or c2, which needs S1 and S2 to be multiples of a piece).
+// c1 or c2, which needs S1 and S2 to be multiples of a piece).  REMAP = true:
+// the accumulators are in the paired layout (swap45 of the row within each
+// 64-row block and of the column within the 64 columns; MA even, NB == 2).
 template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false, bool FENCED = false,
-          bool OUT_FP4 = false, bool EPI = false>
+          bool OUT_FP4 = false, bool EPI = false, bool REMAP = false>
 AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     static_assert(MA % MP == 0, "whole passes");
     static_assert(!(OUT_FP4 && OUT_F32), "one output format");
+    static_assert(!REMAP || (MA % 2 == 0 && NB == 2), "paired layout: 64-row and 64-column blocks");
     constexpr int EB2 = OUT_FP4 ? 1 : (OUT_F32 ? 8 : 4);   // output bytes per two elements
     constexpr int RB = 16 * NB * EB2;           // bytes per block row
     constexpr int P = RB / 16;                  // 16-byte pieces per row
@@ -109,6 +140,10 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
     const int pc = lane % P;
     const int n_out = nb + pc * (32 / EB2);
     const int col_off = n_out < p.N ? n_out * EB2 / 2 : 0x7fffffff;   // outside D when past N
+    // lane parts of the paired row maps (swap45 permutes bits, and the
+    // compile-time parts below hold the other bits)
+    const int lrow1 = REMAP ? swap45(lane & 31) : (lane & 31);
+    const int lrow2 = REMAP ? swap45(lane / P) : lane / P;
 #pragma unroll
     for (int i0 = 0; i0 < MA; i0 += MP) {
 #pragma unroll
@@ -119,7 +154,9 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
                     const int r = i * 32 + (lane & 31);
-                    const int nl = j * 32 + 8 * q + 4 * (lane >> 5);
+                    // column: 4 adjacent ones; row within the block
+                    const int nl = (REMAP ? swap45(j * 32 + 8 * q) : j * 32 + 8 * q) + 4 * (lane >> 5);
+                    const int mr = (REMAP ? swap45((i0 + i) * 32) : (i0 + i) * 32) + lrow1;
                     const f32x16v_t& a = acc[i0 + i][j];
                     float v[4] = {a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
                     if constexpr (SCALED) {
@@ -127,7 +164,7 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
                         for (int e = 0; e < 4; ++e) v[e] *= p.alpha;
                     }
                     if constexpr (HAS_BIAS) {
-                        const int m = min(mb + i0 * 32 + r, p.M - 1), n = min(nb + nl, p.N - 4);
+                        const int m = min(mb + mr, p.M - 1), n = min(nb + nl, p.N - 4);
                         const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[e] += p.beta * b[e];
@@ -135,7 +172,7 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
                     if constexpr (EPI) {
                         // values of rows >= M / columns >= N are computed at a
                         // clamped position and dropped by the store
-                        const int m = min(mb + i0 * 32 + r, p.M - 1), n = min(nb + nl, p.N - 4);
+                        const int m = min(mb + mr, p.M - 1), n = min(nb + nl, p.N - 4);
                         if (p.bias) {
                             const f32x4_t b = *reinterpret_cast<const f32x4_t*>(p.bias + (int64_t)m * p.ld_bias + n);
 #pragma unroll
@@ -163,7 +200,7 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
         for (int rr = 0; rr < 32 * MP; rr += ROWS_PER) {
             const int r = rr + lane / P;
             const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
-            const int m = mb + i0 * 32 + r;
+            const int m = mb + (REMAP ? swap45(i0 * 32 + rr) : i0 * 32 + rr) + lrow2;
             if constexpr (EPI) {
                 if (p.epi.kind == 2) {
                     if (m < p.M && n_out < p.N)

@@ -21,14 +21,6 @@
 
 namespace aiter_amd {
 
-template <int N, typename F, int I = 0>
-AA_DEV void static_for(F&& f) {
-    if constexpr (I < N) {
-        f(std::integral_constant<int, I>{});
-        static_for<N, F, I + 1>(static_cast<F&&>(f));
-    }
-}
-
 struct MoeS2Params {
     int tiles_per_group;   // N tiles per workgroup
     int groups;            // N-tile groups per row block
