@@ -112,6 +112,12 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     constexpr int NBL = NB * 4;           // B loads per wave per stage
     constexpr int STAGE_BYTES = Cfg::STAGE_KB * 1024;
     constexpr int A_ROW_BYTES = 128 * FA;
+    // MX GEMM (not MoE): the paired tile layout of mfma32.h (swap45): MFMA
+    // tile 2p+b takes rows 16b..16b+15 of the 32-row groups 2p and 2p+1, the
+    // wave's B tile j columns 16j..16j+15 of its two 32-column groups, so each
+    // tile's lanes share one scale byte (op_sel) and a tile pair one dword pair
+    constexpr bool PAIRED = MX && MOE == kMoeNone;
+    static_assert(!PAIRED || MA % 2 == 0, "tile pairs");
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES];
 
@@ -203,13 +209,14 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     int b_off[NB];
 #pragma unroll
     for (int j = 0; j < NB; ++j) {
-        int blk = 4 * wave + 2 * j + ((lane >> 4) & 1);
+        int blk = 4 * wave + (PAIRED ? 2 * ((lane >> 4) & 1) + j : 2 * j + ((lane >> 4) & 1));
         if constexpr (MOE == kMoeStage1) blk = ((j ? mq.inter : 0) + n0 + 32 * wave) / 16 + ((lane >> 4) & 1);
         if constexpr (MOE == kMoeStage2) blk += n0 / 16;
         if constexpr (BPRE)
             b_off[j] = blk * 16 * (int)p.ldb + (lane >> 5) * 256 + (lane & 15) * 16;
         else
-            b_off[j] = (64 * wave + 32 * j + (lane & 31)) * (int)p.ldb + (lane >> 5) * 16;
+            b_off[j] = (64 * wave + (PAIRED ? swap45(32 * j + (lane & 31)) : 32 * j + (lane & 31))) * (int)p.ldb +
+                       (lane >> 5) * 16;
     }
     // ---- scales: wave w copies chunk w (A chunks first, then the 2 B chunks)
     const int ga0 = m0 / 32, gb0 = n0 / 32;
@@ -230,7 +237,16 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     if constexpr (MOE == kMoeStage2) {
         if (sc_is_b) sc_group += gb0;
     }
-    const int sc_off = sc_group * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + (lane & 15) * 16;
+    // paired: the two groups of a pair interleave by 128-byte halves, the odd
+    // group's 64-byte quarters swapped (bank-conflict-free reads, a lane's two
+    // dwords 256 B apart)
+    int sc_gran = lane & 15;
+    if constexpr (PAIRED) {
+        const int pos = lane & 31, o = (pos >> 3) & 1;
+        sc_group = 4 * sc_chunk + 2 * (lane >> 5) + o;
+        sc_gran = (pos >> 4) * 8 + ((pos & 7) ^ (o * 4));
+    }
+    const int sc_off = sc_group * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + sc_gran * 16;
     const __amdgpu_buffer_rsrc_t sc_rsrc = sc_is_a ? sa_rsrc : (sc_is_b ? sb_rsrc : null_rsrc);
 
     auto dma_stage = [&](int t) {
@@ -248,7 +264,8 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
                                                      (kt0 + t) * (BPRE ? 2048 : 128), 0);
     };
 
-    const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;
+    const int pos0 = PAIRED ? ((lane >> 4) & 1) * 128 + ((((lane >> 5) * 64) + (lane & 15) * 4) ^ (((lane >> 4) & 1) * 64))
+                            : ((lane & 15) + 16 * (lane >> 5)) * 4;
     // per group, lane l needs bytes h and 2+h (h = (l>>4)&1) of the window's
     // two scale dwords d0 (k-steps 0, 2) and d1 (k-steps 1, 3); v_perm packs
     // them as [d0.h, d0.(2+h), d1.h, d1.(2+h)] so that k-step s takes byte
@@ -266,7 +283,9 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     int sa_pk[MA] = {}, sb_pk[NB] = {};   // packed scale bytes of the stage being multiplied
 
     const int ar = lane & 31;
-    const int a_lane_off = (ar >> 3) * 1024 + (ar & 7) * 128;
+    // paired: MFMA row ar of tile 2p+b is in 8-row chunk 8p + 2b + 4(ar>>4) + ((ar>>3)&1)
+    const int a_lane_off = PAIRED ? (4 * ((ar >> 4) & 1) + ((ar >> 3) & 1)) * 1024 + (ar & 7) * 128
+                                  : (ar >> 3) * 1024 + (ar & 7) * 128;
     const int a_swz = (ar >> 1) & 7;
     auto read_a = [&](int t, int s, int slot) {
         const uint8_t* base = smem + (t % NS) * STAGE_BYTES;
@@ -277,12 +296,24 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
                 const int piece = (FA == 1) ? (2 * s + (lane >> 5)) : ((4 * s + 2 * h + (lane >> 5)) & 7);
                 const int hh = (FA == 1) ? 0 : ((4 * s + 2 * h) >> 3);
                 af[slot][i][h] = *reinterpret_cast<const i32x4_t*>(
-                    base + (hh * (BM / 8) + i * 4) * 1024 + a_lane_off + ((piece ^ a_swz) * 16));
+                    base + (hh * (BM / 8) + (PAIRED ? (i >> 1) * 8 + (i & 1) * 2 : i * 4)) * 1024 + a_lane_off +
+                    ((piece ^ a_swz) * 16));
             }
     };
     auto read_scales = [&](int t, int (&pa)[MA], int (&pb)[NB]) {
         if constexpr (!MX) return;
         const uint8_t* base = smem + (t % NS) * STAGE_BYTES + A_CH * 1024 + pos0;
+        if constexpr (PAIRED) {
+            // pair q: d0 (k-steps 0, 2) and d1 (1, 3) -> pa[2q], pa[2q+1]; B: the wave's pair
+#pragma unroll
+            for (int q = 0; q < MA / 2; ++q) {
+                pa[2 * q] = *reinterpret_cast<const int*>(base + q * 512);
+                pa[2 * q + 1] = *reinterpret_cast<const int*>(base + q * 512 + 256);
+            }
+            pb[0] = *reinterpret_cast<const int*>(base + SCA * 1024 + wave * 512);
+            pb[1] = *reinterpret_cast<const int*>(base + SCA * 1024 + wave * 512 + 256);
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < MA; ++i) {
             const unsigned d0 = *reinterpret_cast<const unsigned*>(base + i * 256);
@@ -302,12 +333,29 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     auto mma = [&](int aslot, int bpar, auto sel, const int (&pa)[MA], const int (&pb)[NB]) {
         constexpr int s = decltype(sel)::value;
         constexpr int osel = (s == 0) ? 0 : (s == 1) ? 2 : (s == 2) ? 1 : 3;
+        if constexpr (PAIRED) {
+            // tile 2q+b: byte b + 2(s/2) of dword d(s%2) of pair q (B: tile j, byte j + 2(s/2))
+            constexpr int o = 2 * (s >> 1);
 #pragma unroll
-        for (int i = 0; i < MA; ++i)
+            for (int i = 0; i < MA; ++i) {
+                const int sa = pa[2 * (i >> 1) + (s & 1)], sb = pb[s & 1];
+                const i32x4_t &a0 = af[aslot][i][0], &a1 = af[aslot][i][FA - 1];
+                if (i & 1) {
+                    acc[i][0] = mma32x<KA, 1 + o, 0 + o>(bq[bpar][0][s], a0, a1, acc[i][0], sa, sb);
+                    acc[i][1] = mma32x<KA, 1 + o, 1 + o>(bq[bpar][1][s], a0, a1, acc[i][1], sa, sb);
+                } else {
+                    acc[i][0] = mma32x<KA, 0 + o, 0 + o>(bq[bpar][0][s], a0, a1, acc[i][0], sa, sb);
+                    acc[i][1] = mma32x<KA, 0 + o, 1 + o>(bq[bpar][1][s], a0, a1, acc[i][1], sa, sb);
+                }
+            }
+        } else {
 #pragma unroll
-            for (int j = 0; j < NB; ++j)
-                acc[i][j] = mma32<KA, osel>(bq[bpar][j][s], af[aslot][i][0], af[aslot][i][FA - 1], acc[i][j], pa[i],
-                                            pb[j]);
+            for (int i = 0; i < MA; ++i)
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+                    acc[i][j] = mma32<KA, osel>(bq[bpar][j][s], af[aslot][i][0], af[aslot][i][FA - 1], acc[i][j],
+                                                pa[i], pb[j]);
+        }
     };
     // B of stage t+2, k-step s, into the registers k-step s of stage t just used
     auto prefetch_b = [&](int t, int bpar, int s) {
@@ -537,7 +585,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         return;
     }
     __syncthreads();
-    store_block_any<MA, NB, EP_MP, OUT_F32>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0, n0 + wave * 64);
+    store_block_any<MA, NB, EP_MP, OUT_F32, PAIRED>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0, n0 + wave * 64);
 }
 
 template <int KA, int BM, bool OUT_F32, bool BPRE = true>

@@ -215,16 +215,16 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
 }
 
 // the epilogue flavours picked at run time (uniform branch)
-template <int MA, int NB, int MP, bool OUT_F32>
+template <int MA, int NB, int MP, bool OUT_F32, bool REMAP = false>
 AA_DEV void store_block_any(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     if (p.epi.kind)
-        store_block<MA, NB, MP, false, true, OUT_F32, false, false, true>(p, acc, cb, lane, mb, nb);
+        store_block<MA, NB, MP, false, true, OUT_F32, false, false, true, REMAP>(p, acc, cb, lane, mb, nb);
     else if (p.bias)
-        store_block<MA, NB, MP, true, true, OUT_F32>(p, acc, cb, lane, mb, nb);
+        store_block<MA, NB, MP, true, true, OUT_F32, false, false, false, REMAP>(p, acc, cb, lane, mb, nb);
     else if (p.alpha != 1.0f)
-        store_block<MA, NB, MP, false, true, OUT_F32>(p, acc, cb, lane, mb, nb);
+        store_block<MA, NB, MP, false, true, OUT_F32, false, false, false, REMAP>(p, acc, cb, lane, mb, nb);
     else
-        store_block<MA, NB, MP, false, false, OUT_F32>(p, acc, cb, lane, mb, nb);
+        store_block<MA, NB, MP, false, false, OUT_F32, false, false, false, REMAP>(p, acc, cb, lane, mb, nb);
 }
 
 }  // namespace aiter_amd
