@@ -237,14 +237,11 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     if constexpr (MOE == kMoeStage2) {
         if (sc_is_b) sc_group += gb0;
     }
-    // paired: the two groups of a pair interleave by 128-byte halves, the odd
-    // group's 64-byte quarters swapped (bank-conflict-free reads, a lane's two
-    // dwords 256 B apart)
+    // paired: the chunk image of sc_pair_group / sc_pair_granule
     int sc_gran = lane & 15;
     if constexpr (PAIRED) {
-        const int pos = lane & 31, o = (pos >> 3) & 1;
-        sc_group = 4 * sc_chunk + 2 * (lane >> 5) + o;
-        sc_gran = (pos >> 4) * 8 + ((pos & 7) ^ (o * 4));
+        sc_group = 4 * sc_chunk + sc_pair_group(lane);
+        sc_gran = sc_pair_granule(lane);
     }
     const int sc_off = sc_group * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + sc_gran * 16;
     const __amdgpu_buffer_rsrc_t sc_rsrc = sc_is_a ? sa_rsrc : (sc_is_b ? sb_rsrc : null_rsrc);
@@ -264,8 +261,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
                                                      (kt0 + t) * (BPRE ? 2048 : 128), 0);
     };
 
-    const int pos0 = PAIRED ? ((lane >> 4) & 1) * 128 + ((((lane >> 5) * 64) + (lane & 15) * 4) ^ (((lane >> 4) & 1) * 64))
-                            : ((lane & 15) + 16 * (lane >> 5)) * 4;
+    const int pos0 = PAIRED ? sc_pair_read_off(lane) : ((lane & 15) + 16 * (lane >> 5)) * 4;
     // per group, lane l needs bytes h and 2+h (h = (l>>4)&1) of the window's
     // two scale dwords d0 (k-steps 0, 2) and d1 (k-steps 1, 3); v_perm packs
     // them as [d0.h, d0.(2+h), d1.h, d1.(2+h)] so that k-step s takes byte
@@ -585,7 +581,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         return;
     }
     __syncthreads();
-    store_block_any<MA, NB, EP_MP, OUT_F32, PAIRED>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0, n0 + wave * 64);
+    store_block_any<MA, NB, EP_MP, OUT_F32, PAIRED ? 3 : 0>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0, n0 + wave * 64);
 }
 
 template <int KA, int BM, bool OUT_F32, bool BPRE = true>

@@ -109,19 +109,9 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     const bool sc_is_b = wave >= SCA && wave < SCA + 2;
     const int sc_chunk = sc_is_a ? wave : (sc_is_b ? wave - SCA : 0);
     const int sc_stride = sc_is_b ? (int)p.sb_stride : (int)p.sa_stride;
-    // chunk = 4 groups x 256 B.  Paired: the two groups of a pair interleave
-    // by 128-byte halves (even group's first half, odd group's first half,
-    // even's second, odd's second), the odd group's 64-byte quarters swapped:
-    // a lane's two dwords are then 256 B apart for every lane, and the 64
-    // lanes of a read spread over the banks (32 or 64 of them)
-    int sc_off;
-    if constexpr (PAIRED) {
-        const int pos = lane & 31, o = (pos >> 3) & 1;
-        const int k = (pos >> 4) * 8 + ((pos & 7) ^ (o * 4));
-        sc_off = (4 * sc_chunk + 2 * (lane >> 5) + o) * 32 * sc_stride + k * 16;
-    } else {
-        sc_off = (4 * sc_chunk + (lane >> 4)) * 32 * sc_stride + (lane & 15) * 16;
-    }
+    // chunk = 4 groups x 256 B (paired: the image of sc_pair_group / _granule)
+    const int sc_off = PAIRED ? (4 * sc_chunk + sc_pair_group(lane)) * 32 * sc_stride + sc_pair_granule(lane) * 16
+                              : (4 * sc_chunk + (lane >> 4)) * 32 * sc_stride + (lane & 15) * 16;
     const __amdgpu_buffer_rsrc_t sc_rsrc =
         sc_is_a ? make_rsrc(p.As, (int64_t)p.sa_groups * 32 * p.sa_stride)
                 : (sc_is_b ? make_rsrc(p.Bs, (int64_t)p.sb_groups * 32 * p.sb_stride) : null_rsrc);
@@ -139,8 +129,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         nst = it < my_tiles ? nstages : 0;
     };
 
-    const int pos0 = PAIRED ? ((lane >> 4) & 1) * 128 + ((((lane >> 5) * 64) + (lane & 15) * 4) ^ (((lane >> 4) & 1) * 64))
-                            : ((lane & 15) + 16 * (lane >> 5)) * 4;
+    const int pos0 = PAIRED ? sc_pair_read_off(lane) : ((lane & 15) + 16 * (lane >> 5)) * 4;
     const unsigned sc_perm = 0x06040200u + ((lane >> 4) & 1) * 0x01010101u;
 
     i32x4_t af[2][MA][FA];
@@ -396,7 +385,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
         // epilogue through ring slot 3: every wave finished reading it before
         // the last stage's barrier, and its next copy is issued in the next
         // tile's first stage, after the barrier below
-        store_block<MA, NB, EP_MP, false, SCALED, OUT_F32, true, OUT_FP4, false, PAIRED>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
+        store_block<MA, NB, EP_MP, false, SCALED, OUT_F32, true, OUT_FP4, false, PAIRED ? 3 : 0>(p, acc, smem + 3 * STAGE_BYTES + wave * (STAGE_BYTES / 4),
                                                               lane, cm0, cn0 + wave * 64);
         wait_vmcnt_lgkm0<63>();
         asm volatile("" ::: "memory");

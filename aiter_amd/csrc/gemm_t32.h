@@ -68,6 +68,10 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
     static_assert(WAIT_N < 64, "vmcnt range");
     constexpr int STAGE_BYTES = Cfg::STAGE_KB * 1024;
     constexpr int A_ROW_BYTES = 128 * FA;
+    // MX: the paired layout of mfma32.h (swap45) for the rows when a wave holds
+    // an even number of 32-row tiles, for the columns when it holds an even
+    // number of 32-column tiles; a paired tile's lanes share one scale byte
+    constexpr bool PM = MX && MA % 2 == 0, PN = MX && NB % 2 == 0;
 
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES];
 
@@ -103,7 +107,8 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
         const int c = wave + 4 * q;
         if constexpr (BPRE) {
             const int s = c % 4, g = c / 4;
-            const int b16 = 2 * g + ((lane >> 4) & 1);
+            // paired: tile g takes 16-row block g&1 of the groups 2(g>>1) + lane half
+            const int b16 = PN ? 2 * (2 * (g >> 1) + ((lane >> 4) & 1)) + (g & 1) : 2 * g + ((lane >> 4) & 1);
             b_off[q] = b16 * 16 * (int)p.ldb + s * 512 + (lane >> 5) * 256 + (lane & 15) * 16;
         } else {
             const int r = c * 8 + (lane >> 3);
@@ -123,7 +128,10 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
         const bool sc_is_a = wave < SCA;
         const bool sc_is_b = wave >= SCA && wave < SCA + SCB;
         const int sc_chunk = sc_is_a ? wave : (sc_is_b ? wave - SCA : 0);
-        sc_off = (4 * sc_chunk + (lane >> 4)) * 32 * (int)(sc_is_b ? p.sb_stride : p.sa_stride) + (lane & 15) * 16;
+        const bool pair = sc_is_b ? PN : PM;   // chunk image of sc_pair_group / sc_pair_granule
+        sc_off = (4 * sc_chunk + (pair ? sc_pair_group(lane) : (lane >> 4))) * 32 *
+                     (int)(sc_is_b ? p.sb_stride : p.sa_stride) +
+                 (pair ? sc_pair_granule(lane) : (lane & 15)) * 16;
         sc_rsrc = sc_is_a ? sa_rsrc : (sc_is_b ? sb_rsrc : null_rsrc);
     }
 
@@ -159,7 +167,11 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
     // 2s + l/32 (+ 64 B for the second e4m3 half) stored at piece ^ swz(r)
     const int ar = lane & 31;
     const int row_off = (ar >> 3) * 1024 + (ar & 7) * 128;
+    // paired: MFMA row ar of tile 2p+b is in 8-row chunk 8p + 2b + 4(ar>>4) + ((ar>>3)&1)
+    const int prow_off = (4 * ((ar >> 4) & 1) + ((ar >> 3) & 1)) * 1024 + (ar & 7) * 128;
     const int swz = (ar >> 1) & 7;
+    // 8-row chunk offset of 32-row tile I (paired: with the lane part prow_off)
+    auto tile_chunks = [](int I, bool paired) { return paired ? (I >> 1) * 8 + (I & 1) * 2 : I * 4; };
     auto read_ops = [&](int t, int s, int slot) {
         const uint8_t* base = smem + (t % NS) * STAGE_BYTES;
 #pragma unroll
@@ -169,7 +181,8 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
                 const int piece = (FA == 1) ? (2 * s + (lane >> 5)) : ((4 * s + 2 * h + (lane >> 5)) & 7);
                 const int hh = (FA == 1) ? 0 : ((4 * s + 2 * h) >> 3);
                 af[slot][i][h] = *reinterpret_cast<const i32x4_t*>(
-                    base + (hh * (BM / 8) + (wm * MA + i) * 4) * 1024 + row_off + ((piece ^ swz) * 16));
+                    base + (hh * (BM / 8) + tile_chunks(wm * MA + i, PM)) * 1024 + (PM ? prow_off : row_off) +
+                    ((piece ^ swz) * 16));
             }
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
@@ -177,39 +190,72 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
                 bf[slot][j] = *reinterpret_cast<const i32x4_t*>(base + (A_CH + (wn * NB + j) * 4 + s) * 1024 + lane * 16);
             else
                 bf[slot][j] = *reinterpret_cast<const i32x4_t*>(
-                    base + (A_CH + (wn * NB + j) * 4) * 1024 + row_off + (((2 * s + (lane >> 5)) ^ swz) * 16));
+                    base + (A_CH + tile_chunks(wn * NB + j, PN)) * 1024 + (PN ? prow_off : row_off) +
+                    (((2 * s + (lane >> 5)) ^ swz) * 16));
         }
     };
     // MX: lane l needs bytes h and 2+h (h = (l>>4)&1) of its group's two scale
     // dwords d0 (k-steps 0, 2) and d1 (k-steps 1, 3); packed [d0.h, d0.(2+h), d1.h, d1.(2+h)]
+    // (paired: pair q's dwords d0 (k-steps 0, 2) and d1 (1, 3) as pa[2q], pa[2q+1])
     const int pos0 = ((lane & 15) + 16 * (lane >> 5)) * 4;
+    const int ppos = sc_pair_read_off(lane);
     const unsigned sc_perm = 0x06040200u + ((lane >> 4) & 1) * 0x01010101u;
     auto read_scales = [&](int t, int (&pa)[MA], int (&pb)[NB]) {
         if constexpr (MX) {
-            const uint8_t* base = smem + (t % NS) * STAGE_BYTES + (A_CH + B_CH) * 1024 + pos0;
+            const uint8_t* base = smem + (t % NS) * STAGE_BYTES + (A_CH + B_CH) * 1024;
+            if constexpr (PM) {
 #pragma unroll
-            for (int i = 0; i < MA; ++i) {
-                const uint8_t* g = base + (wm * MA + i) * 256;
-                pa[i] = (int)__builtin_amdgcn_perm(*reinterpret_cast<const unsigned*>(g + 128),
-                                                   *reinterpret_cast<const unsigned*>(g), sc_perm);
+                for (int q = 0; q < MA / 2; ++q) {
+                    const uint8_t* g = base + ppos + (wm * MA / 2 + q) * 512;
+                    pa[2 * q] = *reinterpret_cast<const int*>(g);
+                    pa[2 * q + 1] = *reinterpret_cast<const int*>(g + 256);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < MA; ++i) {
+                    const uint8_t* g = base + pos0 + (wm * MA + i) * 256;
+                    pa[i] = (int)__builtin_amdgcn_perm(*reinterpret_cast<const unsigned*>(g + 128),
+                                                       *reinterpret_cast<const unsigned*>(g), sc_perm);
+                }
             }
+            if constexpr (PN) {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) {
-                const uint8_t* g = base + SCA * 1024 + (wn * NB + j) * 256;
-                pb[j] = (int)__builtin_amdgcn_perm(*reinterpret_cast<const unsigned*>(g + 128),
-                                                   *reinterpret_cast<const unsigned*>(g), sc_perm);
+                for (int q = 0; q < NB / 2; ++q) {
+                    const uint8_t* g = base + SCA * 1024 + ppos + (wn * NB / 2 + q) * 512;
+                    pb[2 * q] = *reinterpret_cast<const int*>(g);
+                    pb[2 * q + 1] = *reinterpret_cast<const int*>(g + 256);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < NB; ++j) {
+                    const uint8_t* g = base + SCA * 1024 + pos0 + (wn * NB + j) * 256;
+                    pb[j] = (int)__builtin_amdgcn_perm(*reinterpret_cast<const unsigned*>(g + 128),
+                                                       *reinterpret_cast<const unsigned*>(g), sc_perm);
+                }
             }
         }
     };
     auto mma = [&](int slot, auto sel) {
         constexpr int s = decltype(sel)::value;
         constexpr int osel = (s == 0) ? 0 : (s == 1) ? 2 : (s == 2) ? 1 : 3;
+        // paired: tile 2q+b uses byte b + 2(s/2) of dword d(s%2) of pair q
+        constexpr int o0 = PM ? 2 * (s >> 1) : osel, o1 = PM ? 1 + 2 * (s >> 1) : osel;
+        constexpr int p0 = PN ? 2 * (s >> 1) : osel, p1 = PN ? 1 + 2 * (s >> 1) : osel;
 #pragma unroll
         for (int i = 0; i < MA; ++i)
 #pragma unroll
-            for (int j = 0; j < NB; ++j)
-                acc[i][j] = mma32<KA, osel>(bf[slot][j], af[slot][i][0], af[slot][i][FA - 1], acc[i][j], sa_pk[i],
-                                            sb_pk[j]);
+            for (int j = 0; j < NB; ++j) {
+                const int sa = PM ? sa_pk[2 * (i >> 1) + (s & 1)] : sa_pk[i];
+                const int sb = PN ? sb_pk[2 * (j >> 1) + (s & 1)] : sb_pk[j];
+                const i32x4_t &b = bf[slot][j], &a0 = af[slot][i][0], &a1 = af[slot][i][FA - 1];
+                if (i & 1) {
+                    if (j & 1) acc[i][j] = mma32x<KA, o1, p1>(b, a0, a1, acc[i][j], sa, sb);
+                    else acc[i][j] = mma32x<KA, o1, p0>(b, a0, a1, acc[i][j], sa, sb);
+                } else {
+                    if (j & 1) acc[i][j] = mma32x<KA, o0, p1>(b, a0, a1, acc[i][j], sa, sb);
+                    else acc[i][j] = mma32x<KA, o0, p0>(b, a0, a1, acc[i][j], sa, sb);
+                }
+            }
     };
 
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
@@ -294,10 +340,11 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
         GemmParams q = p;
         q.D = p.ws + (int64_t)blockIdx.y * p.M * p.N;
         q.ldd = p.N;
-        store_block<MA, NB, EP_MP32, false, false, true>(q, acc, smem + wave * WAVE_SCRATCH, lane, m0 + wm * WM,
-                                                         n0 + wn * WN);
+        store_block<MA, NB, EP_MP32, false, false, true, false, false, false, (PM ? 1 : 0) | (PN ? 2 : 0)>(
+            q, acc, smem + wave * WAVE_SCRATCH, lane, m0 + wm * WM, n0 + wn * WN);
     } else {
-        store_block_any<MA, NB, EP_MP, OUT_F32>(p, acc, smem + wave * WAVE_SCRATCH, lane, m0 + wm * WM, n0 + wn * WN);
+        store_block_any<MA, NB, EP_MP, OUT_F32, (PM ? 1 : 0) | (PN ? 2 : 0)>(p, acc, smem + wave * WAVE_SCRATCH, lane,
+                                                                          m0 + wm * WM, n0 + wn * WN);
     }
 }
 

@@ -78,6 +78,21 @@ AA_DEV void static_for(F&& f) {
 // pair of tiles shares one dword pair: no per-lane byte shuffle.
 AA_DEV constexpr int swap45(int x) { return (x & ~48) | ((x & 16) << 1) | ((x & 32) >> 1); }
 
+// e8m0 scales in the paired layout.  A ring slot's scale chunk holds 4 groups
+// x 256 B (one K stage of 32 rows each).  The two groups of a pair interleave
+// by 128-byte halves (even group's first half, odd group's first half, even's
+// second, odd's second), the odd group's 64-byte quarters swapped.  A lane's
+// two dwords (k-steps 0/2 and 1/3) are then 256 B apart for every lane, and
+// a wave's reads spread over 32 or 64 banks.  Copy: lane l fetches 16-byte
+// granule sc_pair_granule(l) of group sc_pair_group(l) of the chunk's four.
+// Read: pair q's dwords at q*512 + sc_pair_read_off(l) and +256.
+AA_DEV int sc_pair_group(int lane) { return 2 * (lane >> 5) + ((lane >> 3) & 1); }
+AA_DEV int sc_pair_granule(int lane) { return ((lane >> 4) & 1) * 8 + ((lane & 7) ^ (((lane >> 3) & 1) * 4)); }
+AA_DEV int sc_pair_read_off(int lane) {
+    const int o = (lane >> 4) & 1;
+    return o * 128 + ((((lane >> 5) * 64) + (lane & 15) * 4) ^ (o * 64));
+}
+
 // As mma32, with separate op_sel byte selections for the A and B scales.
 template <int KA, int OSEL_A, int OSEL_B>
 AA_DEV f32x16v_t mma32x(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, f32x16v_t c, int sa, int sb) {
@@ -116,15 +131,18 @@ AA_DEV f32x16v_t mma32x(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, 
 // per byte, the lower column in the low nibble; p.ldd still counts elements).
 // EPI = true adds, at run time, the bias and the fused output operation of
 // p.epi (mul_add on the f32 values; split_cat sends each 16-byte piece to
-// c1 or c2, which needs S1 and S2 to be multiples of a piece).  REMAP = true:
-// the accumulators are in the paired layout (swap45 of the row within each
-// 64-row block and of the column within the 64 columns; MA even, NB == 2).
+// c1 or c2, which needs S1 and S2 to be multiples of a piece).  REMAP: the
+// accumulators are in the paired layout, bit 0 for rows (swap45 of the row
+// within each 64-row block; MA even), bit 1 for columns (NB even); (mb, nb)
+// are then 64-aligned within the tile.
 template <int MA, int NB, int MP, bool HAS_BIAS, bool SCALED = true, bool OUT_F32 = false, bool FENCED = false,
-          bool OUT_FP4 = false, bool EPI = false, bool REMAP = false>
+          bool OUT_FP4 = false, bool EPI = false, int REMAP = 0>
 AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     static_assert(MA % MP == 0, "whole passes");
     static_assert(!(OUT_FP4 && OUT_F32), "one output format");
-    static_assert(!REMAP || (MA % 2 == 0 && NB == 2), "paired layout: 64-row and 64-column blocks");
+    static_assert(!(REMAP & 1) || MA % 2 == 0, "paired rows: 64-row blocks");
+    static_assert(!(REMAP & 2) || NB % 2 == 0, "paired columns: 64-column blocks");
+    constexpr bool RM = REMAP & 1, RN = REMAP & 2;
     constexpr int EB2 = OUT_FP4 ? 1 : (OUT_F32 ? 8 : 4);   // output bytes per two elements
     constexpr int RB = 16 * NB * EB2;           // bytes per block row
     constexpr int P = RB / 16;                  // 16-byte pieces per row
@@ -142,8 +160,8 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
     const int col_off = n_out < p.N ? n_out * EB2 / 2 : 0x7fffffff;   // outside D when past N
     // lane parts of the paired row maps (swap45 permutes bits, and the
     // compile-time parts below hold the other bits)
-    const int lrow1 = REMAP ? swap45(lane & 31) : (lane & 31);
-    const int lrow2 = REMAP ? swap45(lane / P) : lane / P;
+    const int lrow1 = RM ? swap45(lane & 31) : (lane & 31);
+    const int lrow2 = RM ? swap45(lane / P) : lane / P;
 #pragma unroll
     for (int i0 = 0; i0 < MA; i0 += MP) {
 #pragma unroll
@@ -155,8 +173,8 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
                 for (int q = 0; q < 4; ++q) {
                     const int r = i * 32 + (lane & 31);
                     // column: 4 adjacent ones; row within the block
-                    const int nl = (REMAP ? swap45(j * 32 + 8 * q) : j * 32 + 8 * q) + 4 * (lane >> 5);
-                    const int mr = (REMAP ? swap45((i0 + i) * 32) : (i0 + i) * 32) + lrow1;
+                    const int nl = (RN ? swap45(j * 32 + 8 * q) : j * 32 + 8 * q) + 4 * (lane >> 5);
+                    const int mr = (RM ? swap45((i0 + i) * 32) : (i0 + i) * 32) + lrow1;
                     const f32x16v_t& a = acc[i0 + i][j];
                     float v[4] = {a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
                     if constexpr (SCALED) {
@@ -200,7 +218,7 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
         for (int rr = 0; rr < 32 * MP; rr += ROWS_PER) {
             const int r = rr + lane / P;
             const i32x4_t v = *reinterpret_cast<const i32x4_t*>(cb + r * RB + ((pc ^ ((r >> RSH) & SWM)) * 16));
-            const int m = mb + (REMAP ? swap45(i0 * 32 + rr) : i0 * 32 + rr) + lrow2;
+            const int m = mb + (RM ? swap45(i0 * 32 + rr) : i0 * 32 + rr) + lrow2;
             if constexpr (EPI) {
                 if (p.epi.kind == 2) {
                     if (m < p.M && n_out < p.N)
@@ -215,7 +233,7 @@ AA_DEV void store_block(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* 
 }
 
 // the epilogue flavours picked at run time (uniform branch)
-template <int MA, int NB, int MP, bool OUT_F32, bool REMAP = false>
+template <int MA, int NB, int MP, bool OUT_F32, int REMAP = 0>
 AA_DEV void store_block_any(const GemmParams& p, f32x16v_t (&acc)[MA][NB], uint8_t* cb, int lane, int mb, int nb) {
     if (p.epi.kind)
         store_block<MA, NB, MP, false, true, OUT_F32, false, false, true, REMAP>(p, acc, cb, lane, mb, nb);
