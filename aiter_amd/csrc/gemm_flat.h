@@ -118,8 +118,17 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     // tile's lanes share one scale byte (op_sel) and a tile pair one dword pair
     constexpr bool PAIRED = MX && MOE == kMoeNone;
     static_assert(!PAIRED || MA % 2 == 0, "tile pairs");
+    // bf16 with row-major B: B is loaded whole 128-byte row lines at a time
+    // (8 rows per load, like the A copies) into registers two stages ahead,
+    // then transposed through a wave-private 8 KiB LDS region into the MFMA
+    // operand layout one stage before use.  A direct operand load of
+    // row-major B touches 32 rows x 32 bytes per instruction and runs at a
+    // quarter of the full-line rate in the memory pipeline.
+    constexpr bool BLDS = !MX && !BPRE && MOE == kMoeNone;
+    constexpr int BPRIV = 8192;   // 64 rows x 128 B per wave
+    static_assert(!BLDS || NS * Cfg::STAGE_KB + 4 * BPRIV / 1024 <= 160, "ring + private B fit the LDS");
 
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES + (BLDS ? 4 * BPRIV : 0)];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
@@ -218,6 +227,18 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
             b_off[j] = (64 * wave + (PAIRED ? swap45(32 * j + (lane & 31)) : 32 * j + (lane & 31))) * (int)p.ldb +
                        (lane >> 5) * 16;
     }
+    // BLDS: raw load q = the wave's B rows 8q..8q+7 (lane: row 8q + l/8), lane
+    // l fetching 16-byte piece (l%8) ^ swz(row) so that its store to the
+    // private region (granule 64q + l) leaves row r's piece p at r*128 +
+    // ((p ^ swz(r)) * 16), the layout of the A copies (swz(r) = (r>>1)&7)
+    int braw_off[BLDS ? 8 : 1];
+    if constexpr (BLDS) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            const int r = 8 * q + (lane >> 3);
+            braw_off[q] = (64 * wave + r) * (int)p.ldb + (((lane & 7) ^ ((r >> 1) & 7)) * 16);
+        }
+    }
     // ---- scales: wave w copies chunk w (A chunks first, then the 2 B chunks)
     const int ga0 = m0 / 32, gb0 = n0 / 32;
     const __amdgpu_buffer_rsrc_t sa_rsrc =
@@ -276,6 +297,8 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
 
     i32x4_t af[2][MA][FA];
     i32x4_t bq[2][NB][4];          // [stage parity][tile][k-step]
+    i32x4_t braw[BLDS ? 2 : 1][8];  // BLDS: raw row loads of stages t+1, t+2 (slot t % 2)
+    i32x4_t bfr[2][NB];            // BLDS: operands of the current / next k-step
     int sa_pk[MA] = {}, sb_pk[NB] = {};   // packed scale bytes of the stage being multiplied
 
     const int ar = lane & 31;
@@ -349,14 +372,35 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
             for (int i = 0; i < MA; ++i)
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
-                    acc[i][j] = mma32<KA, osel>(bq[bpar][j][s], af[aslot][i][0], af[aslot][i][FA - 1], acc[i][j],
-                                                pa[i], pb[j]);
+                    acc[i][j] = mma32<KA, osel>(BLDS ? bfr[s & 1][j] : bq[bpar][j][s], af[aslot][i][0],
+                                                af[aslot][i][FA - 1], acc[i][j], pa[i], pb[j]);
         }
     };
     // B of stage t+2, k-step s, into the registers k-step s of stage t just used
     auto prefetch_b = [&](int t, int bpar, int s) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) bq[bpar][j][s] = load_b(t + 2, j, s);
+    };
+    // BLDS: raw loads q0 .. q0+3 of stage t into braw[rb]; the raw stage in
+    // braw[rb] into the private region; the operand of k-step s (tile j: rows
+    // 32j + l%32, piece 2s + l/32) into bfr[slot]
+    uint8_t* const bpriv = smem + NS * STAGE_BYTES + wave * BPRIV;
+    auto load_raw = [&](int t, int rb, int q0) {
+        const __amdgpu_buffer_rsrc_t r = t < nstages ? b_rsrc : null_rsrc;
+#pragma unroll
+        for (int q = q0; q < q0 + 4; ++q)
+            braw[rb][q] = __builtin_amdgcn_raw_buffer_load_b128(r, braw_off[q], (kt0 + t) * 128, 0);
+    };
+    auto write_raw = [&](int rb) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) *reinterpret_cast<i32x4_t*>(bpriv + q * 1024 + lane * 16) = braw[rb][q];
+    };
+    auto read_bfr = [&](int s, int slot) {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            const int rr = 32 * j + (lane & 31);
+            bfr[slot][j] = *reinterpret_cast<const i32x4_t*>(bpriv + rr * 128 + (((2 * s + (lane >> 5)) ^ a_swz) * 16));
+        }
     };
 
     // Each k-step is its own scheduling region (sched_barrier fences): the LDS
@@ -376,24 +420,38 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
             else dma16(rs, base + (A_CH + wave) * 1024, sc_off, (kt0 + t) * 256);
         }
     };
+    // BLDS issue order per stage: raw loads in k-steps 0 and 1, the copies in
+    // k-steps 2 (D3 of them) and 3
+    constexpr int D3 = (NDMA + 1) / 2;
+    auto dma_half = [&](int t, int h) {
+        const bool live = t < nstages;
+        const __amdgpu_buffer_rsrc_t ra = live ? a_rsrc : null_rsrc;
+        uint8_t* base = smem + (t % NS) * STAGE_BYTES;
+#pragma unroll
+        for (int q = h * D3; q < (h ? NDMA : D3); ++q)
+            dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], (kt0 + t) * A_ROW_BYTES);
+    };
     // loads issued after the last A copy of stage t+1 and before the wait at
-    // the end of iteration t (all of them from later iterations)
+    // the end of iteration t (all of them from later iterations): the loads of
+    // NS-3 whole stages, then those of stage t before its wait
     constexpr int LOADS_ITER = NDMA + NBL;
-    constexpr int WAIT_N = NS >= 3 ? (NS - 3) * LOADS_ITER + NDMA + 3 * NB : 0;
+    constexpr int PRE_WAIT = BLDS ? NBL + D3 : NDMA + 3 * NB;
+    constexpr int WAIT_N = NS >= 3 ? (NS - 3) * LOADS_ITER + PRE_WAIT : 0;
     static_assert(WAIT_N < 64, "vmcnt range");
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
     // order inside a k-step region: one LDS read after each of the first RD
     // MFMAs, the region's global loads after the last MFMAs
     constexpr int RD = MA * FA;
     constexpr int MF = MA * NB;
-    auto pace = [&](int vmem) {
+    auto pace2 = [&](int ds, int vmem) {
 #pragma unroll
         for (int k = 0; k < MF; ++k) {
-            if (k < RD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // DS read
+            if (k < ds) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);           // DS read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                       // MFMA
             if (k >= MF - vmem) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM
         }
     };
+    auto pace = [&](int vmem) { pace2(RD, vmem); };
 
     // stage t of the main loop; bpar = t & 1 selects the B registers
     auto stage = [&](int t, int bpar) {
@@ -401,6 +459,44 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         using S1 = std::integral_constant<int, 1>;
         using S2 = std::integral_constant<int, 2>;
         using S3 = std::integral_constant<int, 3>;
+        if constexpr (BLDS) {
+            // k-steps 0, 1: raw loads of stage t+2 into the registers of stage
+            // t (in the private region since the end of stage t-1); k-steps 2,
+            // 3: the copies of stage t+NS-1; after the barrier the raw stage t+1
+            // goes to the private region (the operand reads of stage t from it
+            // are earlier in this wave's LDS order) and its k-step 0 comes back
+            read_a(t, 1, 1);
+            read_bfr(1, 1);
+            load_raw(t + 2, bpar, 0);
+            mma(0, bpar, S0{}, sa_pk, sb_pk);
+            pace2(RD + NB, 4);
+            fence();
+            read_a(t, 2, 0);
+            read_bfr(2, 0);
+            load_raw(t + 2, bpar, 4);
+            mma(1, bpar, S1{}, sa_pk, sb_pk);
+            pace2(RD + NB, 4);
+            fence();
+            read_a(t, 3, 1);
+            read_bfr(3, 1);
+            dma_half(t + NS - 1, 0);
+            mma(0, bpar, S2{}, sa_pk, sb_pk);
+            pace2(RD + NB, D3);
+            fence();
+            wait_vmcnt_lgkm0<WAIT_N>();
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            fence();
+            read_a(t + 1, 0, 0);
+            write_raw(bpar ^ 1);
+            read_bfr(0, 0);
+            dma_half(t + NS - 1, 1);
+            mma(1, bpar, S3{}, sa_pk, sb_pk);
+            pace2(RD + NB, NDMA - D3);
+            fence();
+            return;
+        }
         read_a(t, 1, 1);
         dma_part(t + NS - 1, 0);
         mma(0, bpar, S0{}, sa_pk, sb_pk);
@@ -442,30 +538,38 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         fence();
     };
 
-    // prologue: B stages 0, 1 first, then A stages 0..NS-2 (so that at the loop
+    // prologue: B stages 0, 1 first (BLDS: raw), then A stages 0..NS-2 (so that at the loop
     // head at least as many loads follow each B load as in the steady state,
     // and the compiler's B waits there stay as loose as in the loop).
     // The wait at the end of stage t (vmcnt WAIT_N) publishes the copies of
     // stage t+1 only if at least WAIT_N loads were issued after them.  For a
     // copy issued here (stage t+1 <= NS-2) that is (NS-3-t)*NDMA later
     // prologue copies + t whole stages + the NDMA + 3*NB loads of stage t
-    // before its wait, fewer than WAIT_N for the first stages of a 4-slot ring
-    // (stage 1: 2*NDMA + 3*NB).  Those copies are waited for here, with
-    // stage 0's: they were issued right after it.
+    // before its wait (PRE_WAIT), fewer than WAIT_N for the first stages of a
+    // 4-slot ring.  Those copies are waited for here, with stage 0's: they
+    // were issued right after it.
     constexpr int PRO_WAITED = [] {
         int d = 0;
         for (int t = 0; t + 1 <= NS - 2; ++t)
-            if ((NS - 3 - t) * NDMA + t * LOADS_ITER + NDMA + 3 * NB < WAIT_N) d = t + 1;
+            if ((NS - 3 - t) * NDMA + t * LOADS_ITER + PRE_WAIT < WAIT_N) d = t + 1;
         return d;
     }();
+    if constexpr (BLDS) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+        for (int t = 0; t < 2; ++t) {
+            load_raw(t, t, 0);
+            load_raw(t, t, 4);
+        }
+    } else {
 #pragma unroll
-        for (int j = 0; j < NB; ++j) bq[0][j][s] = load_b(0, j, s);
+        for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+            for (int j = 0; j < NB; ++j) bq[0][j][s] = load_b(0, j, s);
 #pragma unroll
-        for (int j = 0; j < NB; ++j) bq[1][j][s] = load_b(1, j, s);
+        for (int s = 0; s < 4; ++s)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) bq[1][j][s] = load_b(1, j, s);
+    }
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t) dma_stage(t);
     __builtin_amdgcn_sched_barrier(0);
@@ -476,6 +580,10 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     __builtin_amdgcn_sched_barrier(0);
     read_scales(0, sa_pk, sb_pk);
     read_a(0, 0, 0);
+    if constexpr (BLDS) {
+        write_raw(0);
+        read_bfr(0, 0);
+    }
 
     // the loop runs an even number of stages; an odd last stage is a zero stage
     for (int t = 0; t < nstages; t += 2) {

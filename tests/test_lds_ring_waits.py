@@ -14,7 +14,9 @@ that precedes reads of a slot covers that slot's copies.  Inside a k-step
 region the compiler may order the region's loads freely, so the model issues
 a region's copies last (the fewest followers).
 
-Kernels modelled: gemm_flat.h ``flat_body`` (prologue and main loop),
+Kernels modelled: gemm_flat.h ``flat_body`` (prologue and main loop; both
+its issue orders: B operand loads spread over the k-steps, and the BLDS order
+of row-major bf16 B, raw row loads first and the copies after),
 gemm_t32.h ``gemm_t32_kernel``, gemm_flat_persist.h (prologue, tile
 transitions).  A wrong count here (the flat kernel's former prologue wait of
 (NS - 2) * NDMA) lets the first stage read a slot whose copies may still be
@@ -85,6 +87,43 @@ def run_flat(ns, ndma, nb, nstages, prologue_wait=flat_prologue_wait):
         if not w.complete(("A", t + 1)):
             bad.append(t + 1)
         w.issue(("B", t + 2), nb)
+    return bad
+
+
+def flat_blds_waits(ns, ndma):
+    """gemm_flat.h with row-major bf16 B through the private LDS region
+    (BLDS): per stage 8 raw B loads (k-steps 0, 1), then the copies, D3 of
+    them before the wait; returns (WAIT_N, prologue vmcnt)"""
+    nbl, d3 = 8, (ndma + 1) // 2
+    loads_iter = ndma + nbl
+    pre_wait = nbl + d3
+    wait_n = (ns - 3) * loads_iter + pre_wait if ns >= 3 else 0
+    waited = 0
+    for t in range(ns - 2):
+        if (ns - 3 - t) * ndma + t * loads_iter + pre_wait < wait_n:
+            waited = t + 1
+    return wait_n, (ns - 2 - waited) * ndma
+
+
+def run_flat_blds(ns, ndma, nstages, waits=flat_blds_waits):
+    """issue order of the BLDS stage: raw loads of stage t+2 (4 + 4), copies
+    of stage t+NS-1 (D3, the wait publishing stage t+1, the rest)"""
+    wait_n, pro = waits(ns, ndma)
+    d3 = (ndma + 1) // 2
+    w = Wave()
+    w.issue(("B", 0), 8)
+    w.issue(("B", 1), 8)
+    for t in range(ns - 1):
+        w.issue(("A", t), ndma)
+    w.wait(pro)
+    bad = [] if w.complete(("A", 0)) else [0]
+    for t in range(nstages + nstages % 2):
+        w.issue(("B", t + 2), 8)
+        w.issue(("A", t + ns - 1), d3)
+        w.wait(wait_n)
+        if not w.complete(("A", t + 1)):
+            bad.append(t + 1)
+        w.issue(("A", t + ns - 1), ndma - d3)
     return bad
 
 
@@ -196,3 +235,20 @@ def test_persistent_kernel_waits(ka, bm, eb2, nstages):
     ndma = bm // 8 * fa // 4 + (0 if ka == "bf16" else 1)
     nst = bm * 64 * eb2 // 2048
     assert run_persist(ndma, 2, nst, nstages, tiles=3) == []
+
+
+@pytest.mark.parametrize("bm", [128, 256])
+@pytest.mark.parametrize("nstages", [1, 2, 3, 8, 64])
+def test_flat_blds_waits(bm, nstages):
+    ns, ndma = _flat_cfg("bf16", bm)
+    assert run_flat_blds(ns, ndma, nstages) == []
+
+
+def test_flat_blds_model_catches_the_plain_wait():
+    """The plain flat wait (NDMA + 3 NB before the wait) is too loose for the
+    BLDS order, whose last copies of a stage come after its raw loads."""
+    def plain(ns, ndma):
+        return (ns - 3) * (ndma + 8) + ndma + 6, (ns - 3) * ndma
+
+    ns, ndma = _flat_cfg("bf16", 256)
+    assert run_flat_blds(ns, ndma, 8, waits=plain) != []
