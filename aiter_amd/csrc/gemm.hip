@@ -20,6 +20,7 @@
 #include "gemm_flat.h"
 #include "gemm_flat_persist.h"
 #include "gemm_lds_persist.h"
+#include "gemm_skinny_lds.h"
 #include "gemm_t32.h"
 #include "out_quant.h"
 
@@ -62,6 +63,7 @@ struct Instance {
     Variant var;
     LaunchFn fn;
     bool persistent = false;   // grid of min(tiles, CUs) workgroups walking the tiles
+    int rank = 0;              // among skinny forms of one shape the heuristic takes the highest
 };
 
 template <int KA, int KB, int BM, int BN, bool AP, bool BP, bool OF>
@@ -101,6 +103,15 @@ void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
 template <int KA, int MF, bool BP, bool SPLIT, bool OF, int NB = 1>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
     gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
+}
+
+template <int KA, int MF, bool BP, int NB, int NW = kSkinnyWaves, int S = 2, bool BL = false>
+void launch_skinny_alds(const GemmParams& p, dim3 grid, hipStream_t s) {
+    // A (and a workgroup's B rows) are addressed through buffer descriptors
+    // with 32-bit offsets
+    AA_CHECK((int64_t)p.M * p.lda < (1LL << 31) && (int64_t)32 * p.ldb < (1LL << 31),
+             "skinny through-LDS kernel: A or a 32-row B panel larger than 2 GiB");
+    gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL><<<grid, 64 * NW, 0, s>>>(p);
 }
 
 std::vector<Instance>& registry() {
@@ -274,6 +285,27 @@ std::vector<Instance>& registry() {
         // through a wave-private LDS region (gemm_flat.h, BLDS) ----
         tile(kA16W16, 256, 256, b16r, launch_flat<kBf16, 256, false, false>, "a16w16");
         reg.back().name += "_flat";
+        // ---- skinny kernels with A (row-major bf16 B: A and B) copied
+        // through LDS in whole lines (gemm_skinny_lds.h); rank 1: the
+        // heuristic prefers them over the register-load forms above ----
+        auto staged = [&](Family f, int mf, Variant v, LaunchFn fn, const char* fam, int bn, const char* tag,
+                          int rank = 1) {
+            skinny(f, mf, false, v, fn, fam, bn);
+            reg.back().name += tag;
+            reg.back().rank = rank;
+        };
+        staged(kA16W16, 1, b16r, launch_skinny_alds<kBf16, 1, false, 2, 8, 2, true>, "a16w16", 32, "_lds");
+        staged(kA16W16, 2, b16r, launch_skinny_alds<kBf16, 2, false, 2, 8, 2, true>, "a16w16", 32, "_lds");
+        staged(kA16W16, 4, b16r, launch_skinny_alds<kBf16, 4, false, 2, 4, 2, true>, "a16w16", 32, "_lds");
+        staged(kA16W16, 1, b16r, launch_skinny_alds<kBf16, 1, false, 1, 8, 2, true>, "a16w16", 16, "_lds");
+        staged(kA16W16, 1, b16r, launch_skinny_alds<kBf16, 1, false, 1, 8, 3, true>, "a16w16", 16, "_lds_s3", 0);
+        staged(kA16W16, 2, b16r, launch_skinny_alds<kBf16, 2, false, 1, 8, 2, true>, "a16w16", 16, "_lds");
+        staged(kA16W16, 2, b16p, launch_skinny_alds<kBf16, 2, true, 2>, "a16w16", 32, "_alds");
+        staged(kA16W16, 4, b16p, launch_skinny_alds<kBf16, 4, true, 2>, "a16w16", 32, "_alds");
+        staged(kA4W4, 2, pre, launch_skinny_alds<kFp4, 2, true, 2>, "a4w4", 32, "_alds");
+        staged(kA4W4, 4, pre, launch_skinny_alds<kFp4, 4, true, 2>, "a4w4", 32, "_alds");
+        staged(kA4W4, 2, pre, launch_skinny_alds<kFp4, 2, true, 1>, "a4w4", 16, "_alds");
+        staged(kA8W4, 2, a8n, launch_skinny_alds<kFp8, 2, true, 2>, "a8w4", 32, "_alds");
     });
     return reg;
 }
@@ -323,14 +355,20 @@ const Instance* heuristic(Family f, const Variant& v, int M, int N, int K, int c
         // CUs: each A fragment then serves two B blocks (A's L2 traffic per
         // B byte halves); measured 4.3 -> 4.0 us at M=16 and 5.4 -> 4.4 us at
         // M=32 for N=7168, K=2048, and no gain at M=1
-        if (M > 8 && s == 1 && (N + 31) / 32 * 4 >= cus * 3)
+        auto pick = [&](int bn, bool split) {
+            const Instance* got = nullptr;
             for (auto& in : registry())
-                if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.bn == 32 && !in.split) return &in;
-        for (auto& in : registry())
-            if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.bn == 16 && in.split == (s > 1)) {
-                *splits = s;
-                return &in;
-            }
+                if (in.skinny && variant_ok(in, f, v) && in.bm == 16 * mf && in.bn == bn && in.split == split &&
+                    (!got || in.rank > got->rank))
+                    got = &in;
+            return got;
+        };
+        if (M > 8 && s == 1 && (N + 31) / 32 * 4 >= cus * 3)
+            if (const Instance* in = pick(32, false)) return in;
+        if (const Instance* in = pick(16, s > 1)) {
+            *splits = s;
+            return in;
+        }
     }
     // time ~ rounds of tiles x per-tile time, and a tile's time per K step
     // grows like BM + BN (operand bytes) while its work grows like BM * BN:
@@ -763,9 +801,11 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
                 splitk_finish_kernel<false><<<dim3((unsigned)((n4 / 4 + 255) / 256)), 256, 0, stream>>>(p);
         } else if (inst->split) {
             // a split instance asked for one split runs its non-split twin
+            // (the highest-ranked one, first registered among equals)
             const Instance* twin = nullptr;
             for (auto& in : registry())
-                if (in.skinny && !in.split && variant_ok(in, c.fam, c.var) && in.bm == inst->bm && in.bn == inst->bn)
+                if (in.skinny && !in.split && variant_ok(in, c.fam, c.var) && in.bm == inst->bm &&
+                    in.bn == inst->bn && (!twin || in.rank > twin->rank))
                     twin = &in;
             AA_CHECK(twin, "no non-split twin for ", inst->name);
             p.k_steps_per_split = kpairs;

@@ -373,7 +373,8 @@ def _parse_shape(family: str, text: str):
 def _time_production(family: str, s, iters: int):
     """Seconds per call of the shape through the library's current dispatch
     (the tuned tables in effect, else the heuristic) -- the --compare
-    baseline; None when the call fails."""
+    baseline; None when the call fails.  The weights rotate over as many
+    copies as the candidates' timing uses, so both read them from HBM."""
     import aiter_amd
 
     dev = torch.device("cuda", torch.cuda.current_device())
@@ -385,20 +386,25 @@ def _time_production(family: str, s, iters: int):
             b = torch.randn((n, k), generator=g).to(dtypes.bf16).to(dev)
             if s[5]:
                 b = shuffle_weight(b)
-            fn = lambda i: aiter_amd.gemm_a16w16(a, b)
+            n_copies = _copies(b.numel() * 2)
+            bl = [b] + [b.clone() for _ in range(n_copies - 1)]
+            fn = lambda i: aiter_amd.gemm_a16w16(a, bl[i])
         else:
             m, n, k = s
             a = torch.randn((m, k), generator=g).to(dev)
             b = torch.randn((n, k), generator=g).to(dev)
             bq, bs = dynamic_mxfp4_quant(b, shuffle=True)
             bq = shuffle_weight(bq)
+            n_copies = _copies(bq.numel() + bs.numel())
+            bql = [bq] + [bq.clone() for _ in range(n_copies - 1)]
+            bsl = [bs] + [bs.clone() for _ in range(n_copies - 1)]
             if family == "a4w4":
                 aq, as_ = dynamic_mxfp4_quant(a, shuffle=True)
-                fn = lambda i: aiter_amd.gemm_a4w4(aq, bq, as_, bs)
+                fn = lambda i: aiter_amd.gemm_a4w4(aq, bql[i], as_, bsl[i])
             else:
                 aq, as_ = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=True)
-                fn = lambda i: aiter_amd.gemm_a8w4_mxfp8(aq, bq, as_, bs, a_preshuffle=False)
-        return time_rotated(fn, 1, iters)
+                fn = lambda i: aiter_amd.gemm_a8w4_mxfp8(aq, bql[i], as_, bsl[i], a_preshuffle=False)
+        return time_rotated(fn, n_copies, iters)
     except RuntimeError as e:
         _log(f"  production run failed: {e}")
         return None
