@@ -306,6 +306,10 @@ std::vector<Instance>& registry() {
         staged(kA4W4, 4, pre, launch_skinny_alds<kFp4, 4, true, 2>, "a4w4", 32, "_alds");
         staged(kA4W4, 2, pre, launch_skinny_alds<kFp4, 2, true, 1>, "a4w4", 16, "_alds");
         staged(kA8W4, 2, a8n, launch_skinny_alds<kFp8, 2, true, 2>, "a8w4", 32, "_alds");
+        // ---- split-K forms of the 256-row and 256-column bf16 row-major tiles
+        // (M = 256 with long K: every B byte read once) ----
+        tsplit(kA16W16, 256, 128, b16r, launch_t32<kBf16, false, 256, 128, 2, false, true>, "a16w16");
+        tsplit(kA16W16, 128, 256, b16r, launch_t32<kBf16, false, 128, 256, 2, false, true>, "a16w16");
     });
     return reg;
 }
