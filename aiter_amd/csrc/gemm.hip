@@ -281,8 +281,8 @@ std::vector<Instance>& registry() {
         reg.back().name = "a16w16_tile_256x256_lds_persist";
         // ---- A4W4 64-row skinny with 32 columns per workgroup ----
         skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false, 2>, "a4w4", 32);
-        // ---- bf16 row-major B on the flat tiles: whole-line B loads, transposed
-        // through a wave-private LDS region (gemm_flat.h, BLDS) ----
+        // ---- bf16 row-major B on the flat tiles: whole-line B copies into
+        // wave-private LDS regions (gemm_flat.h, BLDS) ----
         tile(kA16W16, 256, 256, b16r, launch_flat<kBf16, 256, false, false>, "a16w16");
         reg.back().name += "_flat";
         // ---- skinny kernels with A (row-major bf16 B: A and B) copied

@@ -96,7 +96,6 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     static_assert(MOE == kMoeNone || (BPRE && !OUT_F32), "MoE stages: preshuffled B, bf16 output");
     using Cfg = FlatCfg<KA, BM>;
     constexpr int BN = 256;
-    constexpr int NS = Cfg::NS;
     constexpr int FA = Cfg::FA;
     constexpr int MA = BM / 32;           // 32-row A tiles per wave (all rows of the tile)
     constexpr int NB = 2;                 // 32-column B tiles per wave
@@ -105,7 +104,6 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     constexpr int AG = BM / 32;           // A scale groups in the tile
     constexpr int SCA = (AG + 3) / 4;     // A scale chunks
     static_assert(SCA + 2 <= 4, "scale chunks: one per wave");
-    static_assert(NS >= 2, "two LDS stages minimum");
     static_assert(A_CH % 4 == 0, "A chunks split over 4 waves");
     constexpr int NA = A_CH / 4;          // A DMAs per wave per stage
     constexpr int NDMA = NA + (MX ? 1 : 0);   // + one scale chunk (MX)
@@ -118,17 +116,23 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     // tile's lanes share one scale byte (op_sel) and a tile pair one dword pair
     constexpr bool PAIRED = MX && MOE == kMoeNone;
     static_assert(!PAIRED || MA % 2 == 0, "tile pairs");
-    // bf16 with row-major B: B is loaded whole 128-byte row lines at a time
-    // (8 rows per load, like the A copies) into registers two stages ahead,
-    // then transposed through a wave-private 8 KiB LDS region into the MFMA
-    // operand layout one stage before use.  A direct operand load of
-    // row-major B touches 32 rows x 32 bytes per instruction and runs at a
-    // quarter of the full-line rate in the memory pipeline.
+    // bf16 with row-major B (BLDS): B is copied global -> LDS in whole
+    // 128-byte row lines (8 rows per copy, like A) into two wave-private 8 KiB
+    // regions used in turn (stage t in region t % 2), and the MFMA operands
+    // are read from there.  A direct operand load of row-major B touches 32
+    // rows x 32 bytes per instruction and runs at a quarter of the full-line
+    // rate in the memory pipeline.  The A ring gives the regions its fourth
+    // slot (NS = 3 for BM = 256).
     constexpr bool BLDS = !MX && !BPRE && MOE == kMoeNone;
     constexpr int BPRIV = 8192;   // 64 rows x 128 B per wave
-    static_assert(!BLDS || NS * Cfg::STAGE_KB + 4 * BPRIV / 1024 <= 160, "ring + private B fit the LDS");
+    constexpr int NPRIV = BLDS ? 2 : 0;
+    constexpr int NS = (Cfg::NS * Cfg::STAGE_KB + 4 * NPRIV * BPRIV / 1024 <= 160)
+                           ? Cfg::NS
+                           : (160 - 4 * NPRIV * BPRIV / 1024) / Cfg::STAGE_KB;
+    static_assert(NS >= (BLDS ? 3 : 2), "LDS ring depth");
+    static_assert(NS * Cfg::STAGE_KB + 4 * NPRIV * BPRIV / 1024 <= 160, "ring + private B fit the LDS");
 
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES + (BLDS ? 4 * BPRIV : 0)];
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * STAGE_BYTES + 4 * NPRIV * BPRIV];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) & 3;
@@ -227,10 +231,10 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
             b_off[j] = (64 * wave + (PAIRED ? swap45(32 * j + (lane & 31)) : 32 * j + (lane & 31))) * (int)p.ldb +
                        (lane >> 5) * 16;
     }
-    // BLDS: raw load q = the wave's B rows 8q..8q+7 (lane: row 8q + l/8), lane
-    // l fetching 16-byte piece (l%8) ^ swz(row) so that its store to the
-    // private region (granule 64q + l) leaves row r's piece p at r*128 +
-    // ((p ^ swz(r)) * 16), the layout of the A copies (swz(r) = (r>>1)&7)
+    // BLDS: copy q = the wave's B rows 8q..8q+7 (lane: row 8q + l/8), lane l
+    // fetching 16-byte piece (l%8) ^ swz(row) so that its granule 64q + l of
+    // the region holds row r's piece p at r*128 + ((p ^ swz(r)) * 16), the
+    // layout of the A copies (swz(r) = (r>>1)&7)
     int braw_off[BLDS ? 8 : 1];
     if constexpr (BLDS) {
 #pragma unroll
@@ -297,7 +301,6 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
 
     i32x4_t af[2][MA][FA];
     i32x4_t bq[2][NB][4];          // [stage parity][tile][k-step]
-    i32x4_t braw[BLDS ? 2 : 1][8];  // BLDS: raw row loads of stages t+1, t+2 (slot t % 2)
     i32x4_t bfr[2][NB];            // BLDS: operands of the current / next k-step
     int sa_pk[MA] = {}, sb_pk[NB] = {};   // packed scale bytes of the stage being multiplied
 
@@ -381,26 +384,24 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
 #pragma unroll
         for (int j = 0; j < NB; ++j) bq[bpar][j][s] = load_b(t + 2, j, s);
     };
-    // BLDS: raw loads q0 .. q0+3 of stage t into braw[rb]; the raw stage in
-    // braw[rb] into the private region; the operand of k-step s (tile j: rows
-    // 32j + l%32, piece 2s + l/32) into bfr[slot]
-    uint8_t* const bpriv = smem + NS * STAGE_BYTES + wave * BPRIV;
-    auto load_raw = [&](int t, int rb, int q0) {
-        const __amdgpu_buffer_rsrc_t r = t < nstages ? b_rsrc : null_rsrc;
-#pragma unroll
-        for (int q = q0; q < q0 + 4; ++q)
-            braw[rb][q] = __builtin_amdgcn_raw_buffer_load_b128(r, braw_off[q], (kt0 + t) * 128, 0);
-    };
-    auto write_raw = [&](int rb) {
-#pragma unroll
-        for (int q = 0; q < 8; ++q) *reinterpret_cast<i32x4_t*>(bpriv + q * 1024 + lane * 16) = braw[rb][q];
-    };
-    auto read_bfr = [&](int s, int slot) {
+    // BLDS: the operand of k-step s (tile j: rows 32j + l%32, piece 2s +
+    // l/32) of a stage of parity par into bfr[slot]
+    uint8_t* const bpriv0 = smem + NS * STAGE_BYTES + wave * BPRIV;         // even stages
+    uint8_t* const bpriv1 = smem + NS * STAGE_BYTES + (4 + wave) * BPRIV;   // odd stages
+    auto read_bfr = [&](int s, int slot, int par) {
+        const uint8_t* reg = par ? bpriv1 : bpriv0;
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             const int rr = 32 * j + (lane & 31);
-            bfr[slot][j] = *reinterpret_cast<const i32x4_t*>(bpriv + rr * 128 + (((2 * s + (lane >> 5)) ^ a_swz) * 16));
+            bfr[slot][j] = *reinterpret_cast<const i32x4_t*>(reg + rr * 128 + (((2 * s + (lane >> 5)) ^ a_swz) * 16));
         }
+    };
+    // BLDS: the copies of B stage t (8 rows x 128 B each) into its region
+    auto dma_b = [&](int t, int q0, int q1) {
+        const __amdgpu_buffer_rsrc_t r = t < nstages ? b_rsrc : null_rsrc;
+        uint8_t* reg = (t & 1) ? bpriv1 : bpriv0;
+#pragma unroll
+        for (int q = q0; q < q1; ++q) dma16(r, reg + q * 1024, braw_off[q], (kt0 + t) * 128);
     };
 
     // Each k-step is its own scheduling region (sched_barrier fences): the LDS
@@ -420,8 +421,8 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
             else dma16(rs, base + (A_CH + wave) * 1024, sc_off, (kt0 + t) * 256);
         }
     };
-    // BLDS issue order per stage: raw loads in k-steps 0 and 1, the copies in
-    // k-steps 2 (D3 of them) and 3
+    // BLDS issue order per stage: the A copies in k-steps 1 and 2 (D3, then
+    // the rest), the B copies in k-step 3
     constexpr int D3 = (NDMA + 1) / 2;
     auto dma_half = [&](int t, int h) {
         const bool live = t < nstages;
@@ -435,8 +436,11 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     // the end of iteration t (all of them from later iterations): the loads of
     // NS-3 whole stages, then those of stage t before its wait
     constexpr int LOADS_ITER = NDMA + NBL;
-    constexpr int PRE_WAIT = BLDS ? NBL + D3 : NDMA + 3 * NB;
-    constexpr int WAIT_N = NS >= 3 ? (NS - 3) * LOADS_ITER + PRE_WAIT : 0;
+    // BLDS: the copies of B stage t+1 go out in k-step 3 of stage t-1, and
+    // after them only the A copies of stage t+NS-1 (k-steps 1, 2 of stage t)
+    // before the wait that publishes stage t+1: WAIT_N = NDMA
+    constexpr int PRE_WAIT = BLDS ? NDMA : NDMA + 3 * NB;
+    constexpr int WAIT_N = BLDS ? NDMA : (NS >= 3 ? (NS - 3) * LOADS_ITER + PRE_WAIT : 0);
     static_assert(WAIT_N < 64, "vmcnt range");
     auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
     // order inside a k-step region: one LDS read after each of the first RD
@@ -460,32 +464,29 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         using S2 = std::integral_constant<int, 2>;
         using S3 = std::integral_constant<int, 3>;
         if constexpr (BLDS) {
-            // k-steps 0, 1: raw loads of stage t+2 into the registers of stage
-            // t (in the private region since k-step 2 of stage t-1); k-steps 2,
-            // 3: the copies of stage t+NS-1.  The raw stage t+1 goes to the
-            // private region in k-step 2, right after the last operand read of
-            // stage t from it (the wave's own LDS order keeps them apart), and
-            // its k-step 0 comes back after the barrier.  (Writing it after the
-            // barrier instead delays that read: 1.67 against 1.57 us per stage
-            // at 8192^3.)
+            // k-steps 1, 2: the A copies of stage t+NS-1 (NS = 3: t+2);
+            // k-step 3, after the barrier: the B copies of stage t+2 into the
+            // region of stage t, whose last operand read (k-step 3's, issued
+            // in k-step 2) the wait before the barrier has completed.
+            // (Loading B into registers two stages ahead and writing it to
+            // one region with ds_write instead, with a 4-slot A ring,
+            // measured 3-5% slower on the large bf16 shapes.)
             read_a(t, 1, 1);
-            read_bfr(1, 1);
-            load_raw(t + 2, bpar, 0);
+            read_bfr(1, 1, bpar);
             mma(0, bpar, S0{}, sa_pk, sb_pk);
-            pace2(RD + NB, 4);
+            pace2(RD + NB, 0);
             fence();
             read_a(t, 2, 0);
-            read_bfr(2, 0);
-            load_raw(t + 2, bpar, 4);
+            read_bfr(2, 0, bpar);
+            dma_half(t + NS - 1, 0);
             mma(1, bpar, S1{}, sa_pk, sb_pk);
-            pace2(RD + NB, 4);
+            pace2(RD + NB, D3);
             fence();
             read_a(t, 3, 1);
-            read_bfr(3, 1);
-            write_raw(bpar ^ 1);
-            dma_half(t + NS - 1, 0);
+            read_bfr(3, 1, bpar);
+            dma_half(t + NS - 1, 1);
             mma(0, bpar, S2{}, sa_pk, sb_pk);
-            pace2(RD + NB, D3);
+            pace2(RD + NB, NDMA - D3);
             fence();
             wait_vmcnt_lgkm0<WAIT_N>();
             asm volatile("" ::: "memory");
@@ -493,10 +494,10 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
             asm volatile("" ::: "memory");
             fence();
             read_a(t + 1, 0, 0);
-            read_bfr(0, 0);
-            dma_half(t + NS - 1, 1);
+            read_bfr(0, 0, bpar ^ 1);
+            dma_b(t + 2, 0, 8);
             mma(1, bpar, S3{}, sa_pk, sb_pk);
-            pace2(RD + NB, NDMA - D3);
+            pace2(RD + NB, NBL);
             fence();
             return;
         }
@@ -541,15 +542,14 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         fence();
     };
 
-    // prologue: B stages 0, 1 first (BLDS: raw), then A stages 0..NS-2 (so that at the loop
+    // prologue: B stages 0, 1 first (BLDS: copies), then A stages 0..NS-2 (so that at the loop
     // head at least as many loads follow each B load as in the steady state,
     // and the compiler's B waits there stay as loose as in the loop).
     // The wait at the end of stage t (vmcnt WAIT_N) publishes the copies of
     // stage t+1 only if at least WAIT_N loads were issued after them.  For a
     // copy issued here (stage t+1 <= NS-2) that is (NS-3-t)*NDMA later
-    // prologue copies + t whole stages + the NDMA + 3*NB loads of stage t
-    // before its wait (PRE_WAIT), fewer than WAIT_N for the first stages of a
-    // 4-slot ring.  Those copies are waited for here, with stage 0's: they
+    // prologue copies + t whole stages + the loads of stage t before its wait
+    // (PRE_WAIT), fewer than WAIT_N for the first stages of a 4-slot ring.  Those copies are waited for here, with stage 0's: they
     // were issued right after it.
     constexpr int PRO_WAITED = [] {
         int d = 0;
@@ -558,11 +558,8 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         return d;
     }();
     if constexpr (BLDS) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-            load_raw(t, t, 0);
-            load_raw(t, t, 4);
-        }
+        dma_b(0, 0, 8);
+        dma_b(1, 0, 8);
     } else {
 #pragma unroll
         for (int s = 0; s < 4; ++s)
@@ -583,10 +580,7 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     __builtin_amdgcn_sched_barrier(0);
     read_scales(0, sa_pk, sb_pk);
     read_a(0, 0, 0);
-    if constexpr (BLDS) {
-        write_raw(0);
-        read_bfr(0, 0);
-    }
+    if constexpr (BLDS) read_bfr(0, 0, 0);
 
     // the loop runs an even number of stages; an odd last stage is a zero stage
     for (int t = 0; t < nstages; t += 2) {

@@ -16,7 +16,7 @@ a region's copies last (the fewest followers).
 
 Kernels modelled: gemm_flat.h ``flat_body`` (prologue and main loop; both
 its issue orders: B operand loads spread over the k-steps, and the BLDS order
-of row-major bf16 B, raw row loads first and the copies after),
+of row-major bf16 B, A copies before the wait and B copies after it),
 gemm_t32.h ``gemm_t32_kernel``, gemm_flat_persist.h (prologue, tile
 transitions).  A wrong count here (the flat kernel's former prologue wait of
 (NS - 2) * NDMA) lets the first stage read a slot whose copies may still be
@@ -91,13 +91,13 @@ def run_flat(ns, ndma, nb, nstages, prologue_wait=flat_prologue_wait):
 
 
 def flat_blds_waits(ns, ndma):
-    """gemm_flat.h with row-major bf16 B through the private LDS region
-    (BLDS): per stage 8 raw B loads (k-steps 0, 1), then the copies, D3 of
-    them before the wait; returns (WAIT_N, prologue vmcnt)"""
-    nbl, d3 = 8, (ndma + 1) // 2
-    loads_iter = ndma + nbl
-    pre_wait = nbl + d3
-    wait_n = (ns - 3) * loads_iter + pre_wait if ns >= 3 else 0
+    """gemm_flat.h with row-major bf16 B copied into two wave-private LDS
+    regions (BLDS): per stage the A copies of stage t+NS-1 before the wait,
+    the 8 B copies of stage t+2 after it; returns (WAIT_N, prologue vmcnt)
+    with the kernel's formulas (PRE_WAIT = NDMA)"""
+    loads_iter = ndma + 8
+    pre_wait = ndma
+    wait_n = ndma
     waited = 0
     for t in range(ns - 2):
         if (ns - 3 - t) * ndma + t * loads_iter + pre_wait < wait_n:
@@ -106,24 +106,23 @@ def flat_blds_waits(ns, ndma):
 
 
 def run_flat_blds(ns, ndma, nstages, waits=flat_blds_waits):
-    """issue order of the BLDS stage: raw loads of stage t+2 (4 + 4), copies
-    of stage t+NS-1 (D3, the wait publishing stage t+1, the rest)"""
+    """issue order: prologue B copies of stages 0, 1, A copies of stages
+    0..NS-2; stage t: A copies of stage t+NS-1, the wait publishing stage t+1
+    (its A and B copies), then the B copies of stage t+2"""
     wait_n, pro = waits(ns, ndma)
-    d3 = (ndma + 1) // 2
     w = Wave()
     w.issue(("B", 0), 8)
     w.issue(("B", 1), 8)
     for t in range(ns - 1):
         w.issue(("A", t), ndma)
     w.wait(pro)
-    bad = [] if w.complete(("A", 0)) else [0]
+    bad = [] if w.complete(("A", 0)) and w.complete(("B", 0)) else [0]
     for t in range(nstages + nstages % 2):
-        w.issue(("B", t + 2), 8)
-        w.issue(("A", t + ns - 1), d3)
+        w.issue(("A", t + ns - 1), ndma)
         w.wait(wait_n)
-        if not w.complete(("A", t + 1)):
+        if not (w.complete(("A", t + 1)) and w.complete(("B", t + 1))):
             bad.append(t + 1)
-        w.issue(("A", t + ns - 1), ndma - d3)
+        w.issue(("B", t + 2), 8)
     return bad
 
 
@@ -237,18 +236,27 @@ def test_persistent_kernel_waits(ka, bm, eb2, nstages):
     assert run_persist(ndma, 2, nst, nstages, tiles=3) == []
 
 
+def _blds_ring(bm):
+    """(NS, NDMA) of the BLDS flat kernel: the A ring gives 64 KiB to the B regions"""
+    ns, ndma = _flat_cfg("bf16", bm)
+    stage_kb = bm // 8
+    ns = ns if ns * stage_kb + 64 <= 160 else (160 - 64) // stage_kb
+    return ns, ndma
+
+
 @pytest.mark.parametrize("bm", [128, 256])
 @pytest.mark.parametrize("nstages", [1, 2, 3, 8, 64])
 def test_flat_blds_waits(bm, nstages):
-    ns, ndma = _flat_cfg("bf16", bm)
+    ns, ndma = _blds_ring(bm)
+    assert ns == (3 if bm == 256 else 4)
     assert run_flat_blds(ns, ndma, nstages) == []
 
 
-def test_flat_blds_model_catches_the_plain_wait():
-    """The plain flat wait (NDMA + 3 NB before the wait) is too loose for the
-    BLDS order, whose last copies of a stage come after its raw loads."""
-    def plain(ns, ndma):
-        return (ns - 3) * (ndma + 8) + ndma + 6, (ns - 3) * ndma
+def test_flat_blds_model_catches_a_loose_wait():
+    """A wait that also lets the B copies of the stage being published stay
+    outstanding (NDMA + 8) leaves them unchecked."""
+    def loose(ns, ndma):
+        return ndma + 8, (ns - 2) * ndma
 
-    ns, ndma = _flat_cfg("bf16", 256)
-    assert run_flat_blds(ns, ndma, 8, waits=plain) != []
+    ns, ndma = _blds_ring(256)
+    assert run_flat_blds(ns, ndma, 8, waits=loose) != []
