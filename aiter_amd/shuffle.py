@@ -26,7 +26,7 @@ def shuffle_weight(x: torch.Tensor, layout=(16, 16), use_int4=False, pad_k_to: i
     original_k = x.shape[-1]
     if pad_k_to:
         if pad_k_to < 0:
-            raise ValueError(f"pad_k_to must be non-negative, got {pad_k_to}")
+            raise ValueError(f"shuffle_weight: pad_k_to is {pad_k_to}; it pads K up to a multiple and cannot be negative")
         padded = (original_k + pad_k_to - 1) // pad_k_to * pad_k_to
         if padded != original_k:
             x = F.pad(x.contiguous(), (0, padded - original_k), value=0)
@@ -34,8 +34,8 @@ def shuffle_weight(x: torch.Tensor, layout=(16, 16), use_int4=False, pad_k_to: i
     BK = IK * 2
     K = 16 // x.element_size() if not use_int4 else 32
     BN = IN
-    assert x.shape[-2] % BN == 0, f"{x.shape[-2]} % {BN} == {x.shape[-2] % BN}"
-    assert x.shape[-1] % BK == 0, f"{x.shape[-1]} % {BK} == {x.shape[-1] % BK}"
+    assert x.shape[-2] % BN == 0, f"shuffle_weight: {x.shape[-2]} rows, not a whole number of {BN}-row blocks"
+    assert x.shape[-1] % BK == 0, f"shuffle_weight: last dim {x.shape[-1]} is not a multiple of {BK}"
     x_ = x.view(-1, x.shape[-2] // BN, BN, x.shape[-1] // BK, BK // K, K)
     x_ = x_.permute(0, 1, 3, 4, 2, 5).contiguous()
     x_ = x_.view(*x.shape).view(x_type)
