@@ -595,6 +595,15 @@ def profile_workload(dev, name):
     elif name == "bf16_8192x8192x28672":
         a, b = bf16(8192, 28672), bf16(8192, 28672)
         fn = lambda: aiter_amd.gemm_a16w16(a, b)
+    elif name == "bf16_256x8192x28672":
+        a, b = bf16(256, 28672), bf16(8192, 28672)
+        fn = lambda: aiter_amd.gemm_a16w16(a, b)
+    elif name == "bf16_32x7168x2048":
+        a, b = bf16(32, 2048), bf16(7168, 2048)
+        fn = lambda: aiter_amd.gemm_a16w16(a, b)
+    elif name == "fused_rms_mxfp4_8192":
+        x, w = bf16(8192, 8192), bf16(1, 8192).view(-1)
+        fn = lambda: aiter_amd.fused_rms_mxfp4_quant(x, w, 1e-6, shuffle=True)
     else:
         raise SystemExit(f"unknown workload {name}")
     fn()
