@@ -343,6 +343,61 @@ def test_tile_instances_odd_stage_counts(cuda, m, n, k):
                 assert ok, f"{name}: {msg}"
 
 
+BF16_K_CASES = [(300, 528, 64), (257, 512, 192), (64, 272, 576), (520, 784, 320)]
+
+
+@pytest.mark.parametrize("m,n,k", BF16_K_CASES)
+def test_bf16_tile_instances_odd_stage_counts(cuda, m, n, k):
+    """Every bf16 tile instance (row-major and preshuffled B) with K/64 = 1,
+    3, 9, 5 (a single stage, odd stage counts: the row-major flat tile uses
+    two B regions by stage parity and pads to an even count) on ragged M and
+    N, called twice in a row with different data."""
+    import aiter_amd
+
+    for b_pre in (False, True):
+        for row in _kernels("a16w16", skinny=False, b_pre=b_pre):
+            name, split = row[1], row[6]
+            for seed in (31, 32):
+                announce(f"bf16 tile {name} {m}x{n}x{k} seed {seed}")
+                a = bf16_operand(m, k, seed)
+                b = bf16_operand(n, k, seed + 100)
+                ref = O.bf16_bits_to_f32(O.f32_to_bf16_bits(O.bf16_bits_to_f32(a) @ O.bf16_bits_to_f32(b).T))
+                bt_np = O.shuffle_weight(b) if b_pre else b
+                at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+                bt = _dev(bt_np.view(np.int16), cuda).view(torch.bfloat16)
+                out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+                aiter_amd.gemm_a16w16_asm(at, bt, out, splitK=2 if split else 0, kernelName=name, bpreshuffle=b_pre)
+                torch.cuda.synchronize()
+                ok, msg = allclose_report(out.float().cpu().numpy(), ref)
+                assert ok, f"{name}: {msg}"
+
+
+@pytest.mark.parametrize("k", [64, 192, 576, 2112])
+def test_bf16_skinny_instances_k_pairs(cuda, k):
+    """Every bf16 skinny instance with K/64 = 1, 3, 9, 33 k-pairs over its 8
+    waves (waves with no pair, fewer pairs than the load pipeline's depth,
+    odd counts), N = 272 (17 column blocks: a 32-column workgroup past N)."""
+    import aiter_amd
+
+    n = 272
+    for b_pre in (False, True):
+        for row in _kernels("a16w16", skinny=True, b_pre=b_pre):
+            name, bm, split = row[1], row[4], row[6]
+            m = max(1, bm - 3)
+            announce(f"bf16 skinny {name} {m}x{n}x{k}")
+            a = bf16_operand(m, k, 41)
+            b = bf16_operand(n, k, 42)
+            ref = O.bf16_bits_to_f32(O.f32_to_bf16_bits(O.bf16_bits_to_f32(a) @ O.bf16_bits_to_f32(b).T))
+            bt_np = O.shuffle_weight(b) if b_pre else b
+            at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+            bt = _dev(bt_np.view(np.int16), cuda).view(torch.bfloat16)
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+            aiter_amd.gemm_a16w16_asm(at, bt, out, splitK=2 if split else 0, kernelName=name, bpreshuffle=b_pre)
+            torch.cuda.synchronize()
+            ok, msg = allclose_report(out.float().cpu().numpy(), ref)
+            assert ok, f"{name}: {msg}"
+
+
 @pytest.mark.parametrize("m,n,k", [(8192, 2048, 512), (2048, 8192, 512), (4608, 4096, 256)])
 def test_tile_instances_more_tiles_than_cus(cuda, m, n, k):
     """Every A4W4 tile instance on grids of 512-2304 tiles (more tiles than
