@@ -398,6 +398,36 @@ def test_bf16_skinny_instances_k_pairs(cuda, k):
             assert ok, f"{name}: {msg}"
 
 
+@pytest.mark.parametrize("k", [256, 768, 2304, 8448])
+def test_mx_skinny_instances_k_pairs(cuda, k):
+    """Every A4W4 and A8W4 skinny instance (preshuffled B) with K/256 = 1, 3,
+    9, 33 k-pairs over its 8 waves, N = 272 (17 column blocks)."""
+    import aiter_amd
+    from aiter_amd._lib import call
+
+    n = 272
+    for fam in ("a4w4", "a8w4"):
+        for row in _kernels(fam, skinny=True):
+            name, bm, split = row[1], row[4], row[6]
+            if split:
+                continue   # the split forms: test_gpu_splitk_tiles and the every-instance sweep
+            m = max(1, bm - 3)
+            announce(f"{fam} skinny {name} {m}x{n}x{k}")
+            if fam == "a4w4":
+                a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=51)
+                out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
+                aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda),
+                                        _dev(b_ss, cuda), out, kernelName=name)
+            else:
+                a_q, a_ss, b_q, b_ss, ref = _a8w4_case(m, n, k, seed=52)
+                out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+                call("mxfp8_mxfp4_gemm_asm", _dev(a_q, cuda).view(torch.float8_e4m3fn),
+                     _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda), _dev(b_ss, cuda), out, name, 0)
+            torch.cuda.synchronize()
+            ok, msg = allclose_report(_bf16_np(out[:m]), ref)
+            assert ok, f"{name}: {msg}"
+
+
 @pytest.mark.parametrize("m,n,k", [(8192, 2048, 512), (2048, 8192, 512), (4608, 4096, 256)])
 def test_tile_instances_more_tiles_than_cus(cuda, m, n, k):
     """Every A4W4 tile instance on grids of 512-2304 tiles (more tiles than
