@@ -27,6 +27,17 @@ namespace aiter_amd {
 
 enum OpKind : int { kFp4 = 4, kFp8 = 0, kBf16 = 16 };
 
+// cache-policy operand of a buffer load: nt, for data that one launch reads
+// exactly once (weights at decode sizes), so it does not displace what the
+// other workgroups re-read from L2
+constexpr int kLoadNt = 2;
+
+// plain load of data read once per launch (nt)
+template <typename T>
+AA_DEV T load_once(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
+}
+
 template <int KIND> struct OpTraits;
 template <> struct OpTraits<kFp4> {
     static constexpr int frags_per_step = 1;   // byte-fragments per MFMA k-step
@@ -437,7 +448,7 @@ AA_DEV void skinny_load(SkinnyPair<KA, MF, NB>& d, int pr, const uint8_t* const*
     for (int h = 0; h < 2; ++h) {
         const int s = 2 * pr + h;
 #pragma unroll
-        for (int j = 0; j < NB; ++j) d.b[h][j] = *reinterpret_cast<const i32x4_t*>(bsrc[j] + (int64_t)s * BSTEP);
+        for (int j = 0; j < NB; ++j) d.b[h][j] = load_once<i32x4_t>(bsrc[j] + (int64_t)s * BSTEP);
 #pragma unroll
         for (int i = 0; i < MF; ++i)
 #pragma unroll
@@ -448,7 +459,7 @@ AA_DEV void skinny_load(SkinnyPair<KA, MF, NB>& d, int pr, const uint8_t* const*
     }
     if constexpr (P::SCALED) {
 #pragma unroll
-        for (int g = 0; g < P::SBN; ++g) d.sb[g] = *reinterpret_cast<const int*>(sbp[g] + (int64_t)pr * 256);
+        for (int g = 0; g < P::SBN; ++g) d.sb[g] = load_once<int>(sbp[g] + (int64_t)pr * 256);
 #pragma unroll
         for (int g = 0; g < P::SGRP; ++g) d.sa[g] = *reinterpret_cast<const int*>(sap[g] + (int64_t)pr * 256);
     }

@@ -137,6 +137,8 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
 
     // third `part` of the copies of stage t into its ring slot
     constexpr int DMA_PART = (NDMA + 2) / 3;
+    // decode-sized tiles with one row of tiles read every B byte once
+    const bool b_once = BM <= 64 && p.tiles_m == 1;
     auto dma_part = [&](int t, int part) {
         const bool live = t < nstages;
         const __amdgpu_buffer_rsrc_t ra = live ? a_rsrc : null_rsrc;
@@ -147,8 +149,13 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
         for (int q = part * DMA_PART; q < (part + 1) * DMA_PART && q < NDMA; ++q) {
             if (q < NA)
                 dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], (t_base + t) * A_ROW_BYTES);
-            else if (q < NA + NBW)
-                dma16(rb, base + (A_CH + wave + 4 * (q - NA)) * 1024, b_off[q - NA], (t_base + t) * B_STAGE_OFF);
+            else if (q < NA + NBW) {
+                uint8_t* dst = base + (A_CH + wave + 4 * (q - NA)) * 1024;
+                if (b_once)
+                    dma16<kLoadNt>(rb, dst, b_off[q - NA], (t_base + t) * B_STAGE_OFF);
+                else
+                    dma16(rb, dst, b_off[q - NA], (t_base + t) * B_STAGE_OFF);
+            }
             else
                 dma16(rs, base + (A_CH + B_CH + wave) * 1024, sc_off, (t_base + t) * 256);
         }

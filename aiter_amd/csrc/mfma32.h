@@ -31,8 +31,9 @@ AA_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
 }
 
 // global -> LDS copy of one 1 KiB chunk (16 bytes per lane, lane order)
+template <int AUX = 0>
 AA_DEV void dma16(__amdgpu_buffer_rsrc_t r, uint8_t* lds_chunk, int voff, int soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AA_LDS void*)lds_chunk, 16, voff, soff, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (AA_LDS void*)lds_chunk, 16, voff, soff, 0, AUX);
 }
 
 // s_waitcnt with only the vmcnt field constrained (expcnt/lgkmcnt left at max)
