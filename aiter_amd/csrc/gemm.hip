@@ -97,7 +97,10 @@ void launch_lds_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
 
 template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
 void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT><<<grid, 256, 0, s>>>(p);
+    if (p.tiles_m == 1)
+        gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT, true><<<grid, 256, 0, s>>>(p);
+    else
+        gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT, false><<<grid, 256, 0, s>>>(p);
 }
 
 template <int KA, int MF, bool BP, bool SPLIT, bool OF, int NB = 1>

@@ -45,7 +45,9 @@ struct T32Cfg {
 // SPLIT: blockIdx.y takes stages [y*S, y*S + S) of K (S = p.k_steps_per_split)
 // and writes its fp32 partial tile to slice y of p.ws ([splits][M][N]); a
 // second kernel sums the slices (fixed order, so results are deterministic).
-template <int KA, bool BPRE, int BM, int BN, int WAVES_M, bool OUT_F32, bool SPLIT = false>
+// B_ONCE: the launch has one row of tiles (p.tiles_m == 1), so every B byte
+// is read once and its copies carry the nt cache policy.
+template <int KA, bool BPRE, int BM, int BN, int WAVES_M, bool OUT_F32, bool SPLIT = false, bool B_ONCE = false>
 __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
     apply_batch(p);
     using Cfg = T32Cfg<KA, BPRE, BM, BN>;
@@ -137,8 +139,6 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
 
     // third `part` of the copies of stage t into its ring slot
     constexpr int DMA_PART = (NDMA + 2) / 3;
-    // decode-sized tiles with one row of tiles read every B byte once
-    const bool b_once = BM <= 64 && p.tiles_m == 1;
     auto dma_part = [&](int t, int part) {
         const bool live = t < nstages;
         const __amdgpu_buffer_rsrc_t ra = live ? a_rsrc : null_rsrc;
@@ -150,11 +150,8 @@ __global__ __launch_bounds__(256, 1) void gemm_t32_kernel(GemmParams p) {
             if (q < NA)
                 dma16(ra, base + (wave + 4 * q) * 1024, a_off[q], (t_base + t) * A_ROW_BYTES);
             else if (q < NA + NBW) {
-                uint8_t* dst = base + (A_CH + wave + 4 * (q - NA)) * 1024;
-                if (b_once)
-                    dma16<kLoadNt>(rb, dst, b_off[q - NA], (t_base + t) * B_STAGE_OFF);
-                else
-                    dma16(rb, dst, b_off[q - NA], (t_base + t) * B_STAGE_OFF);
+                dma16<B_ONCE ? kLoadNt : 0>(rb, base + (A_CH + wave + 4 * (q - NA)) * 1024, b_off[q - NA],
+                                            (t_base + t) * B_STAGE_OFF);
             }
             else
                 dma16(rs, base + (A_CH + B_CH + wave) * 1024, sc_off, (t_base + t) * 256);
