@@ -95,9 +95,16 @@ void launch_lds_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
         gemm_lds_persist_kernel<BP, true><<<grid, 256, 0, s>>>(p);
 }
 
+// B (e2m1 for the MX families, bf16 otherwise) large enough for nt loads
+template <int KA>
+bool b_streams(const GemmParams& p) {
+    const int64_t elems = (int64_t)p.N * p.K;
+    return (KA == kBf16 ? elems * 2 : elems / 2) >= kNtMinBytes;
+}
+
 template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
 void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
-    if (p.tiles_m == 1)
+    if (p.tiles_m == 1 && b_streams<KA>(p))
         gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT, true><<<grid, 256, 0, s>>>(p);
     else
         gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT, false><<<grid, 256, 0, s>>>(p);
@@ -105,7 +112,10 @@ void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
 
 template <int KA, int MF, bool BP, bool SPLIT, bool OF, int NB = 1>
 void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
+    if (b_streams<KA>(p))
+        gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB, true><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
+    else
+        gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB, false><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
 }
 
 template <int KA, int MF, bool BP, int NB, int NW = kSkinnyWaves, int S = 2, bool BL = false>
@@ -114,7 +124,10 @@ void launch_skinny_alds(const GemmParams& p, dim3 grid, hipStream_t s) {
     // with 32-bit offsets
     AA_CHECK((int64_t)p.M * p.lda < (1LL << 31) && (int64_t)32 * p.ldb < (1LL << 31),
              "skinny through-LDS kernel: A or a 32-row B panel larger than 2 GiB");
-    gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL><<<grid, 64 * NW, 0, s>>>(p);
+    if (b_streams<KA>(p))
+        gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, true><<<grid, 64 * NW, 0, s>>>(p);
+    else
+        gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, false><<<grid, 64 * NW, 0, s>>>(p);
 }
 
 std::vector<Instance>& registry() {

@@ -38,6 +38,20 @@ AA_DEV T load_once(const uint8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const T*>(p));
 }
 
+// B-operand load, nt when NT
+template <bool NT, typename T>
+AA_DEV T load_b(const uint8_t* p) {
+    if constexpr (NT)
+        return load_once<T>(p);
+    else
+        return *reinterpret_cast<const T*>(p);
+}
+
+// Weights read once per launch stream from HBM faster with the nt policy
+// (a 470 MB row-major matrix: 6.6 TB/s against 5.7 TB/s), but decode
+// launches over a few MB ran slower with it; launchers pick nt from this size.
+constexpr int64_t kNtMinBytes = 16LL << 20;
+
 template <int KIND> struct OpTraits;
 template <> struct OpTraits<kFp4> {
     static constexpr int frags_per_step = 1;   // byte-fragments per MFMA k-step
@@ -438,7 +452,7 @@ struct SkinnyPair {
     int sa[SGRP];
 };
 
-template <int KA, int MF, int NB, bool B_PRE>
+template <int KA, int MF, int NB, bool B_PRE, bool NT>
 AA_DEV void skinny_load(SkinnyPair<KA, MF, NB>& d, int pr, const uint8_t* const* bsrc, const uint8_t* const* asrc,
                         const bool* arow_ok, const uint8_t* const* sbp, const uint8_t* const* sap) {
     using P = SkinnyPair<KA, MF, NB>;
@@ -448,7 +462,7 @@ AA_DEV void skinny_load(SkinnyPair<KA, MF, NB>& d, int pr, const uint8_t* const*
     for (int h = 0; h < 2; ++h) {
         const int s = 2 * pr + h;
 #pragma unroll
-        for (int j = 0; j < NB; ++j) d.b[h][j] = load_once<i32x4_t>(bsrc[j] + (int64_t)s * BSTEP);
+        for (int j = 0; j < NB; ++j) d.b[h][j] = load_b<NT, i32x4_t>(bsrc[j] + (int64_t)s * BSTEP);
 #pragma unroll
         for (int i = 0; i < MF; ++i)
 #pragma unroll
@@ -459,7 +473,7 @@ AA_DEV void skinny_load(SkinnyPair<KA, MF, NB>& d, int pr, const uint8_t* const*
     }
     if constexpr (P::SCALED) {
 #pragma unroll
-        for (int g = 0; g < P::SBN; ++g) d.sb[g] = load_once<int>(sbp[g] + (int64_t)pr * 256);
+        for (int g = 0; g < P::SBN; ++g) d.sb[g] = load_b<NT, int>(sbp[g] + (int64_t)pr * 256);
 #pragma unroll
         for (int g = 0; g < P::SGRP; ++g) d.sa[g] = *reinterpret_cast<const int*>(sap[g] + (int64_t)pr * 256);
     }
@@ -492,7 +506,7 @@ AA_DEV void skinny_mma(const SkinnyPair<KA, MF, NB>& d, f32x4_t (*acc)[NB]) {
 
 // NB column blocks of 16 per workgroup share each A fragment (NB = 2: the
 // two halves of one 32-row B scale group, so one scale dword serves both)
-template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB = 1>
+template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB = 1, bool NT = false>
 __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
     static_assert(NB == 1 || NB == 2, "one or two column blocks per workgroup");
     apply_batch(p);
@@ -554,10 +568,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
         int pr = p_begin + wave;
         if (pr < p_end) {
             SkinnyPair<KA, MF, NB> cur;
-            skinny_load<KA, MF, NB, B_PRE>(cur, pr, bsrc, asrc, arow_ok, sbp, sap);
+            skinny_load<KA, MF, NB, B_PRE, NT>(cur, pr, bsrc, asrc, arow_ok, sbp, sap);
             for (pr += NW; pr < p_end; pr += NW) {
                 SkinnyPair<KA, MF, NB> nxt;
-                skinny_load<KA, MF, NB, B_PRE>(nxt, pr, bsrc, asrc, arow_ok, sbp, sap);
+                skinny_load<KA, MF, NB, B_PRE, NT>(nxt, pr, bsrc, asrc, arow_ok, sbp, sap);
                 skinny_mma<KA, MF, NB, BH>(cur, acc);
                 cur = nxt;
             }

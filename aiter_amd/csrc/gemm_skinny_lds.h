@@ -57,7 +57,10 @@ struct SkinnyLdsStage {
     int sa[SGRP];
 };
 
-template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB, int S = 2, bool BL = false>
+// NT: B and its scales are loaded with the nt cache policy (picked at launch
+// for weights large enough to stream)
+template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB, int S = 2, bool BL = false,
+          bool NT = false>
 __global__ __launch_bounds__(64 * NW) void gemm_skinny_alds_kernel(GemmParams p) {
     static_assert(NB == 1 || NB == 2, "one or two column blocks per workgroup");
     using C = SkinnyLdsCfg<KA, MF, NW, B_PRE, SPLIT, OUT_F32, NB, S, BL>;
@@ -140,18 +143,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_alds_kernel(GemmParams p)
         for (int c = 0; c < C::NCP; ++c) dma16(ar, dst + c * 1024, a_voff[c], pr * C::ROWB);
         if constexpr (BL) {
 #pragma unroll
-            for (int c = 0; c < 2 * NB; ++c) dma16<kLoadNt>(br, dst + C::ABUF + c * 1024, b_voff[c], pr * 128);
+            for (int c = 0; c < 2 * NB; ++c) dma16<NT ? kLoadNt : 0>(br, dst + C::ABUF + c * 1024, b_voff[c], pr * 128);
         } else {
             constexpr int BSTEP = B_PRE ? 1024 : 64;
 #pragma unroll
             for (int h = 0; h < 2; ++h)
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
-                    d.b[h][j] = load_once<i32x4_t>(bsrc[j] + (int64_t)(2 * pr + h) * BSTEP);
+                    d.b[h][j] = load_b<NT, i32x4_t>(bsrc[j] + (int64_t)(2 * pr + h) * BSTEP);
         }
         if constexpr (C::SCALED) {
 #pragma unroll
-            for (int g = 0; g < C::SBN; ++g) d.sb[g] = load_once<int>(sbp[g] + (int64_t)pr * 256);
+            for (int g = 0; g < C::SBN; ++g) d.sb[g] = load_b<NT, int>(sbp[g] + (int64_t)pr * 256);
 #pragma unroll
             for (int g = 0; g < C::SGRP; ++g) d.sa[g] = *reinterpret_cast<const int*>(sap[g] + (int64_t)pr * 256);
         }

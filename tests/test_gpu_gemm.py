@@ -428,6 +428,44 @@ def test_mx_skinny_instances_k_pairs(cuda, k):
             assert ok, f"{name}: {msg}"
 
 
+def test_streamed_weight_instances(cuda):
+    """Launches whose weights reach the nt-load size (16 MiB): every bf16
+    skinny instance and every bf16 tile with one row of tiles at
+    16x4096x2048, every non-split A4W4 skinny instance at 16x8192x4096."""
+    import aiter_amd
+
+    m, n, k = 16, 4096, 2048
+    a = bf16_operand(m, k, 61)
+    b = bf16_operand(n, k, 62)
+    ref = O.bf16_bits_to_f32(O.f32_to_bf16_bits(O.bf16_bits_to_f32(a) @ O.bf16_bits_to_f32(b).T))
+    at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+    for b_pre in (False, True):
+        bt = _dev((O.shuffle_weight(b) if b_pre else b).view(np.int16), cuda).view(torch.bfloat16)
+        for row in _kernels("a16w16", b_pre=b_pre):
+            name, skinny, bm, split = row[1], row[3], row[4], row[6]
+            if not skinny and bm < m:
+                continue
+            announce(f"bf16 streamed-weight {name} {m}x{n}x{k}")
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+            aiter_amd.gemm_a16w16_asm(at, bt, out, splitK=2 if split else 0, kernelName=name, bpreshuffle=b_pre)
+            torch.cuda.synchronize()
+            ok, msg = allclose_report(out.float().cpu().numpy(), ref)
+            assert ok, f"{name}: {msg}"
+    n, k = 8192, 4096
+    a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=63)
+    bq = _dev(O.shuffle_weight(b_q), cuda)
+    for row in _kernels("a4w4", skinny=True):
+        name, split = row[1], row[6]
+        if split:
+            continue
+        announce(f"a4w4 streamed-weight {name} {m}x{n}x{k}")
+        out = torch.empty((32, n), dtype=torch.bfloat16, device=cuda)
+        aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), bq, _dev(a_ss, cuda), _dev(b_ss, cuda), out, kernelName=name)
+        torch.cuda.synchronize()
+        ok, msg = allclose_report(_bf16_np(out[:m]), ref)
+        assert ok, f"{name}: {msg}"
+
+
 @pytest.mark.parametrize("m,n,k", [(8192, 2048, 512), (2048, 8192, 512), (4608, 4096, 256)])
 def test_tile_instances_more_tiles_than_cus(cuda, m, n, k):
     """Every A4W4 tile instance on grids of 512-2304 tiles (more tiles than
