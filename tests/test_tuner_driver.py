@@ -14,6 +14,9 @@ import pytest
 from aiter_amd import tuner
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+# The stand-in worker imports the package (and torch with it): a cold import on
+# a loaded machine has taken more than 5 s, so the watchdog leaves room for it.
+WATCHDOG_S = 20.0
 
 FAKE = textwrap.dedent('''
     import sys, time
@@ -25,7 +28,7 @@ FAKE = textwrap.dedent('''
     if m == 2:
         sys.exit(3)                      # a worker that dies
     if m == 3:
-        time.sleep(60)                   # a worker that hangs
+        time.sleep(300)                  # a worker that hangs
     tuner.write_row(out, "a4w4", {"gfx": "gfx950", "cu_num": 256, "M": m, "N": n, "K": k, "kernelId": 7,
                                   "splitK": 0, "us": 1.0 + m, "kernelName": "a4w4_skinny_m32", "tflops": 1.0,
                                   "bw": 1.0, "errRatio": 0.0})
@@ -45,18 +48,18 @@ def fake_worker(tmp_path, monkeypatch):
 def test_driver_isolates_failures_and_resumes(tmp_path, fake_worker):
     out = str(tmp_path / "tuned.csv")
     shapes = [(1, 256, 512), (2, 256, 512), (3, 256, 512), (4, 256, 512)]
-    res = tuner.drive("a4w4", shapes, out, 5, 0.05, False, timeout=5.0, worker_cmd=fake_worker)
+    res = tuner.drive("a4w4", shapes, out, 5, 0.05, False, timeout=WATCHDOG_S, worker_cmd=fake_worker)
     assert res["tuned"] == [(1, 256, 512), (4, 256, 512)]
     assert [s for s, _ in res["failed"]] == [(2, 256, 512), (3, 256, 512)]
     assert "exit 3" in res["failed"][0][1] and res["failed"][1][1] == "timeout"
     df = pd.read_csv(out)
     assert sorted(df.M.tolist()) == [1, 4]          # each shape's row landed when it finished
     # resume: finished shapes are skipped, failed ones are tried again
-    res2 = tuner.drive("a4w4", shapes, out, 5, 0.05, False, timeout=5.0, worker_cmd=fake_worker)
+    res2 = tuner.drive("a4w4", shapes, out, 5, 0.05, False, timeout=WATCHDOG_S, worker_cmd=fake_worker)
     assert res2["skipped"] == [(1, 256, 512), (4, 256, 512)]
     assert len(res2["failed"]) == 2
     # --all retunes every shape; rows are replaced, not duplicated
-    res3 = tuner.drive("a4w4", [(1, 256, 512)], out, 5, 0.05, True, timeout=5.0, worker_cmd=fake_worker)
+    res3 = tuner.drive("a4w4", [(1, 256, 512)], out, 5, 0.05, True, timeout=WATCHDOG_S, worker_cmd=fake_worker)
     assert res3["tuned"] == [(1, 256, 512)]
     assert sorted(pd.read_csv(out).M.tolist()) == [1, 4]
 
