@@ -129,6 +129,8 @@ SIGNATURES = {
     "aiter_amd_resolve_kernel_name": ([ctypes.c_char_p] + [ctypes.c_int] * 4 + [ctypes.c_int64], ctypes.c_int),
     "aiter_amd_resolve_opus_kid": ([ctypes.c_int, ctypes.c_int, ctypes.c_int64], ctypes.c_int),
     "gemm_workspace_reserve": ([ctypes.c_int, _S, ctypes.c_size_t], ctypes.c_int),
+    "aiter_amd_workspace_bytes": ([ctypes.c_int, _S], ctypes.c_int64),
+    "aiter_amd_workspace_release": ([ctypes.c_int, _S], ctypes.c_int),
     "hbm_stream_read": ([_T, _T, ctypes.c_int, _S], ctypes.c_int),
 }
 

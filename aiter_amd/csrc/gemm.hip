@@ -15,13 +15,7 @@
 #include <string>
 #include <vector>
 
-#include "gemm_kernels.h"
-#include "mfma32.h"
-#include "gemm_flat.h"
-#include "gemm_flat_persist.h"
-#include "gemm_lds_persist.h"
-#include "gemm_skinny_lds.h"
-#include "gemm_t32.h"
+#include "gemm_registry.h"
 #include "out_quant.h"
 
 namespace aiter_amd {
@@ -45,287 +39,18 @@ int device_cu_count(int dev) {
 
 namespace {
 
-enum Family : int { kA4W4 = 0, kA8W4 = 1, kA16W16 = 2 };
 
-struct Variant {
-    bool a_pre, b_pre, out_f32;
-};
-
-using LaunchFn = void (*)(const GemmParams&, dim3, hipStream_t);
-
-struct Instance {
-    int id;
-    std::string name;
-    Family fam;
-    bool skinny;
-    int bm, bn;   // tile: block tile; skinny: bm = 16*MF rows covered, bn = 16
-    bool split;   // skinny split-K over blocks
-    Variant var;
-    LaunchFn fn;
-    bool persistent = false;   // grid of min(tiles, CUs) workgroups walking the tiles
-    int rank = 0;              // among skinny forms of one shape the heuristic takes the highest
-};
-
-template <int KA, int KB, int BM, int BN, bool AP, bool BP, bool OF>
-void launch_tile(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_tile_kernel<KA, KB, BM, BN, AP, BP, OF><<<grid, 256, 0, s>>>(p);
-}
-
-constexpr int kSkinnyWaves = 8;
-
-
-template <int KA, int BM, bool OF = false, bool BP = true>
-void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
-    gemm_flat_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
-}
-
-template <int KA, int BM, bool OF = false, bool BP = true>
-void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
-    if (p.alpha == 1.0f)
-        gemm_flat_persist_kernel<KA, BM, OF, BP, false, false><<<grid, 256, 0, s>>>(p);
-    else
-        gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
-}
-
-template <bool BP>
-void launch_lds_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
-    if (p.alpha == 1.0f)
-        gemm_lds_persist_kernel<BP, false><<<grid, 256, 0, s>>>(p);
-    else
-        gemm_lds_persist_kernel<BP, true><<<grid, 256, 0, s>>>(p);
-}
-
-// B (e2m1 for the MX families, bf16 otherwise) large enough for nt loads
-template <int KA>
-bool b_streams(const GemmParams& p) {
-    const int64_t elems = (int64_t)p.N * p.K;
-    return (KA == kBf16 ? elems * 2 : elems / 2) >= kNtMinBytes;
-}
-
-template <int KA, bool BP, int BM, int BN, int WMW, bool OF = false, bool SPLIT = false>
-void launch_t32(const GemmParams& p, dim3 grid, hipStream_t s) {
-    if (p.tiles_m == 1 && b_streams<KA>(p))
-        gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT, true><<<grid, 256, 0, s>>>(p);
-    else
-        gemm_t32_kernel<KA, BP, BM, BN, WMW, OF, SPLIT, false><<<grid, 256, 0, s>>>(p);
-}
-
-template <int KA, int MF, bool BP, bool SPLIT, bool OF, int NB = 1>
-void launch_skinny(const GemmParams& p, dim3 grid, hipStream_t s) {
-    if (b_streams<KA>(p))
-        gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB, true><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
-    else
-        gemm_skinny_kernel<KA, MF, kSkinnyWaves, BP, SPLIT, OF, NB, false><<<grid, 64 * kSkinnyWaves, 0, s>>>(p);
-}
-
-template <int KA, int MF, bool BP, int NB, int NW = kSkinnyWaves, int S = 2, bool BL = false>
-void launch_skinny_alds(const GemmParams& p, dim3 grid, hipStream_t s) {
-    // A (and a workgroup's B rows) are addressed through buffer descriptors
-    // with 32-bit offsets
-    AA_CHECK((int64_t)p.M * p.lda < (1LL << 31) && (int64_t)32 * p.ldb < (1LL << 31),
-             "skinny through-LDS kernel: A or a 32-row B panel larger than 2 GiB");
-    if (b_streams<KA>(p))
-        gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, true><<<grid, 64 * NW, 0, s>>>(p);
-    else
-        gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, false><<<grid, 64 * NW, 0, s>>>(p);
-}
 
 std::vector<Instance>& registry() {
     static std::vector<Instance> reg;
     static std::once_flag once;
     std::call_once(once, [] {
-        int id = 0;
-        auto tile = [&](Family f, int bm, int bn, Variant v, LaunchFn fn, const char* fam) {
-            std::string nm = std::string(fam) + "_tile_" + std::to_string(bm) + "x" + std::to_string(bn);
-            if (v.a_pre) nm += "_apre";
-            if (!v.b_pre) nm += "_bplain";
-            if (v.out_f32) nm += "_f32";
-            reg.push_back({id++, nm, f, false, bm, bn, false, v, fn});
-        };
-        auto skinny = [&](Family f, int mf, bool split, Variant v, LaunchFn fn, const char* fam, int bn = 16) {
-            std::string nm = std::string(fam) + "_skinny_m" + std::to_string(16 * mf);
-            if (bn != 16) nm += "_n" + std::to_string(bn);
-            if (split) nm += "_splitk";
-            if (v.a_pre) nm += "_apre";
-            if (!v.b_pre) nm += "_bplain";
-            if (v.out_f32) nm += "_f32";
-            reg.push_back({id++, nm, f, true, 16 * mf, bn, split, v, fn});
-        };
-        // ---- a4w4 (B preshuffled): 32x32x64 tile kernels; the 256-column
-        // tiles read B straight into registers (gemm_flat.h), the others stage
-        // A and B through LDS (gemm_t32.h) ----
-        const Variant pre{false, true, false}, plain{false, false, false};
-        tile(kA4W4, 256, 256, pre, launch_flat<kFp4, 256>, "a4w4");
-        tile(kA4W4, 256, 128, pre, launch_t32<kFp4, true, 256, 128, 2>, "a4w4");
-        tile(kA4W4, 128, 256, pre, launch_flat<kFp4, 128>, "a4w4");
-        tile(kA4W4, 128, 128, pre, launch_t32<kFp4, true, 128, 128, 2>, "a4w4");
-        tile(kA4W4, 64, 256, pre, launch_t32<kFp4, true, 64, 256, 1>, "a4w4");
-        tile(kA4W4, 64, 128, pre, launch_t32<kFp4, true, 64, 128, 1>, "a4w4");
-        skinny(kA4W4, 1, false, pre, launch_skinny<kFp4, 1, true, false, false>, "a4w4");
-        skinny(kA4W4, 2, false, pre, launch_skinny<kFp4, 2, true, false, false>, "a4w4");
-        skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false>, "a4w4");
-        skinny(kA4W4, 1, true, pre, launch_skinny<kFp4, 1, true, true, false>, "a4w4");
-        skinny(kA4W4, 2, true, pre, launch_skinny<kFp4, 2, true, true, false>, "a4w4");
-        skinny(kA4W4, 4, true, pre, launch_skinny<kFp4, 4, true, true, false>, "a4w4");
-        // a4w4 with row-major B (bpreshuffle = 0)
-        tile(kA4W4, 128, 128, plain, launch_t32<kFp4, false, 128, 128, 2>, "a4w4");
-        tile(kA4W4, 64, 128, plain, launch_t32<kFp4, false, 64, 128, 1>, "a4w4");
-        skinny(kA4W4, 1, false, plain, launch_skinny<kFp4, 1, false, false, false>, "a4w4");
-        skinny(kA4W4, 2, false, plain, launch_skinny<kFp4, 2, false, false, false>, "a4w4");
-        skinny(kA4W4, 4, false, plain, launch_skinny<kFp4, 4, false, false, false>, "a4w4");
-        // ---- a8w4 ----
-        const Variant a8{false, true, false}, a8p{true, true, false};
-        tile(kA8W4, 128, 256, a8, launch_flat<kFp8, 128>, "a8w4");
-        tile(kA8W4, 128, 128, a8, launch_t32<kFp8, true, 128, 128, 2>, "a8w4");
-        tile(kA8W4, 64, 256, a8, launch_t32<kFp8, true, 64, 256, 1>, "a8w4");
-        tile(kA8W4, 64, 128, a8, launch_t32<kFp8, true, 64, 128, 1>, "a8w4");
-        tile(kA8W4, 128, 256, a8p, launch_tile<kFp8, kFp4, 128, 256, true, true, false>, "a8w4");
-        tile(kA8W4, 128, 128, a8p, launch_tile<kFp8, kFp4, 128, 128, true, true, false>, "a8w4");
-        tile(kA8W4, 64, 128, a8p, launch_tile<kFp8, kFp4, 64, 128, true, true, false>, "a8w4");
-        skinny(kA8W4, 1, false, a8, launch_skinny<kFp8, 1, true, false, false>, "a8w4");
-        skinny(kA8W4, 2, false, a8, launch_skinny<kFp8, 2, true, false, false>, "a8w4");
-        skinny(kA8W4, 4, false, a8, launch_skinny<kFp8, 4, true, false, false>, "a8w4");
-        skinny(kA8W4, 1, true, a8, launch_skinny<kFp8, 1, true, true, false>, "a8w4");
-        skinny(kA8W4, 2, true, a8, launch_skinny<kFp8, 2, true, true, false>, "a8w4");
-        skinny(kA8W4, 4, true, a8, launch_skinny<kFp8, 4, true, true, false>, "a8w4");
-        // ---- a16w16 ----
-        for (int of = 0; of < 2; ++of) {
-            for (int bp = 0; bp < 2; ++bp) {
-                const Variant v{false, bp != 0, of != 0};
-// bf16 tiles: the 256-wide preshuffled ones read B straight into registers
-#define AA_T16(BM, BN, WMW)                                                                \
-    tile(kA16W16, BM, BN, v,                                                               \
-         of ? (bp ? ((BN == 256 && BM >= 128) ? launch_flat<kBf16, (BM >= 128 ? BM : 128), true>  \
-                                              : launch_t32<kBf16, true, BM, BN, WMW, true>)       \
-                  : launch_t32<kBf16, false, BM, BN, WMW, true>)                                  \
-            : (bp ? ((BN == 256 && BM >= 128) ? launch_flat<kBf16, (BM >= 128 ? BM : 128), false> \
-                                              : launch_t32<kBf16, true, BM, BN, WMW, false>)      \
-                  : launch_t32<kBf16, false, BM, BN, WMW, false>),                                \
-         "a16w16");
-                AA_T16(256, 256, 2) AA_T16(256, 128, 2) AA_T16(128, 256, 2) AA_T16(128, 128, 2)
-                AA_T16(64, 128, 1) AA_T16(64, 64, 2)
-#undef AA_T16
-#define AA_S16(MF, SP)                                                                     \
-    skinny(kA16W16, MF, SP, v,                                                             \
-           of ? (bp ? launch_skinny<kBf16, MF, true, SP, true>                             \
-                    : launch_skinny<kBf16, MF, false, SP, true>)                           \
-              : (bp ? launch_skinny<kBf16, MF, true, SP, false>                            \
-                    : launch_skinny<kBf16, MF, false, SP, false>),                         \
-           "a16w16");
-                AA_S16(1, false) AA_S16(2, false) AA_S16(4, false)
-                AA_S16(1, true) AA_S16(2, true) AA_S16(4, true)
-#undef AA_S16
-            }
-        }
-        // ---- persistent forms of the flat tiles (gemm_flat_persist.h);
-        // appended so that the ids above stay stable ----
-        auto persist = [&](Family f, int bm, Variant v, LaunchFn fn, const char* fam) {
-            tile(f, bm, 256, v, fn, fam);
-            reg.back().name += "_persist";
-            reg.back().persistent = true;
-        };
-        persist(kA4W4, 256, pre, launch_flat_persist<kFp4, 256>, "a4w4");
-        persist(kA4W4, 128, pre, launch_flat_persist<kFp4, 128>, "a4w4");
-        persist(kA8W4, 128, a8, launch_flat_persist<kFp8, 128>, "a8w4");
-        persist(kA16W16, 256, Variant{false, true, false}, launch_flat_persist<kBf16, 256>, "a16w16");
-        persist(kA16W16, 128, Variant{false, true, false}, launch_flat_persist<kBf16, 128>, "a16w16");
-        // ---- split-K forms of the smaller t32 tiles (K split over gridDim.y,
-        // f32 partial slices summed by splitk_reduce_kernel), for shapes
-        // whose tiles cannot fill the CUs ----
-        auto tsplit = [&](Family f, int bm, int bn, Variant v, LaunchFn fn, const char* fam) {
-            std::string nm = std::string(fam) + "_tile_" + std::to_string(bm) + "x" + std::to_string(bn) + "_splitk";
-            if (v.a_pre) nm += "_apre";
-            if (!v.b_pre) nm += "_bplain";
-            if (v.out_f32) nm += "_f32";
-            reg.push_back({id++, nm, f, false, bm, bn, true, v, fn});
-        };
-        tsplit(kA4W4, 64, 128, pre, launch_t32<kFp4, true, 64, 128, 1, false, true>, "a4w4");
-        tsplit(kA4W4, 64, 256, pre, launch_t32<kFp4, true, 64, 256, 1, false, true>, "a4w4");
-        tsplit(kA4W4, 128, 128, pre, launch_t32<kFp4, true, 128, 128, 2, false, true>, "a4w4");
-        tsplit(kA4W4, 64, 128, plain, launch_t32<kFp4, false, 64, 128, 1, false, true>, "a4w4");
-        tsplit(kA8W4, 64, 128, a8, launch_t32<kFp8, true, 64, 128, 1, false, true>, "a8w4");
-        tsplit(kA8W4, 64, 256, a8, launch_t32<kFp8, true, 64, 256, 1, false, true>, "a8w4");
-        for (int of = 0; of < 2; ++of) {
-            for (int bp = 0; bp < 2; ++bp) {
-                const Variant v{false, bp != 0, of != 0};
-#define AA_T16S(BM, BN, WMW)                                                                      \
-    tsplit(kA16W16, BM, BN, v,                                                                    \
-           of ? (bp ? launch_t32<kBf16, true, BM, BN, WMW, true, true>                            \
-                    : launch_t32<kBf16, false, BM, BN, WMW, true, true>)                          \
-              : (bp ? launch_t32<kBf16, true, BM, BN, WMW, false, true>                           \
-                    : launch_t32<kBf16, false, BM, BN, WMW, false, true>),                        \
-           "a16w16");
-                AA_T16S(64, 64, 2) AA_T16S(64, 128, 1) AA_T16S(128, 128, 2)
-#undef AA_T16S
-            }
-        }
-        // ---- a4w4 with row-major B on the flat kernels (B straight to VGPRs:
-        // 16 contiguous bytes of one row per lane) ----
-        tile(kA4W4, 256, 256, plain, launch_flat<kFp4, 256, false, false>, "a4w4");
-        persist(kA4W4, 256, plain, launch_flat_persist<kFp4, 256, false, false>, "a4w4");
-        // ---- a4w4 with f32 output (the tile that mxfp4_gemm_asm quantises to
-        // e2m1 / MXFP8) ----
-        // (no 256x256 flat f32 tile: its epilogue spills; the persistent form does not)
-        const Variant pre32{false, true, true};
-        tile(kA4W4, 128, 256, pre32, launch_flat<kFp4, 128, true>, "a4w4");
-        tile(kA4W4, 128, 128, pre32, launch_t32<kFp4, true, 128, 128, 2, true>, "a4w4");
-        tile(kA4W4, 64, 128, pre32, launch_t32<kFp4, true, 64, 128, 1, true>, "a4w4");
-        skinny(kA4W4, 1, false, pre32, launch_skinny<kFp4, 1, true, false, true>, "a4w4");
-        skinny(kA4W4, 2, false, pre32, launch_skinny<kFp4, 2, true, false, true>, "a4w4");
-        skinny(kA4W4, 4, false, pre32, launch_skinny<kFp4, 4, true, false, true>, "a4w4");
-        skinny(kA4W4, 1, true, pre32, launch_skinny<kFp4, 1, true, true, true>, "a4w4");
-        skinny(kA4W4, 2, true, pre32, launch_skinny<kFp4, 2, true, true, true>, "a4w4");
-        skinny(kA4W4, 4, true, pre32, launch_skinny<kFp4, 4, true, true, true>, "a4w4");
-        tsplit(kA4W4, 64, 128, pre32, launch_t32<kFp4, true, 64, 128, 1, true, true>, "a4w4");
-        persist(kA4W4, 256, pre32, launch_flat_persist<kFp4, 256, true>, "a4w4");
-        // ---- skinny with 32 columns per workgroup (one A fragment serves two
-        // B blocks); appended last so that earlier kernel ids stay put ----
-        skinny(kA4W4, 1, false, pre, launch_skinny<kFp4, 1, true, false, false, 2>, "a4w4", 32);
-        skinny(kA4W4, 2, false, pre, launch_skinny<kFp4, 2, true, false, false, 2>, "a4w4", 32);
-        const Variant a8n{false, true, false};
-        skinny(kA8W4, 1, false, a8n, launch_skinny<kFp8, 1, true, false, false, 2>, "a8w4", 32);
-        skinny(kA8W4, 2, false, a8n, launch_skinny<kFp8, 2, true, false, false, 2>, "a8w4", 32);
-        const Variant b16p{false, true, false}, b16r{false, false, false};
-        skinny(kA16W16, 1, false, b16p, launch_skinny<kBf16, 1, true, false, false, 2>, "a16w16", 32);
-        skinny(kA16W16, 2, false, b16p, launch_skinny<kBf16, 2, true, false, false, 2>, "a16w16", 32);
-        skinny(kA16W16, 1, false, b16r, launch_skinny<kBf16, 1, false, false, false, 2>, "a16w16", 32);
-        skinny(kA16W16, 2, false, b16r, launch_skinny<kBf16, 2, false, false, false, 2>, "a16w16", 32);
-        // ---- bf16 256x256 persistent tiles with A and B both through LDS in
-        // half-width ring slots (gemm_lds_persist.h) ----
-        persist(kA16W16, 256, b16r, launch_lds_persist<false>, "a16w16");
-        persist(kA16W16, 256, b16p, launch_lds_persist<true>, "a16w16");
-        reg.back().name = "a16w16_tile_256x256_lds_persist";
-        // ---- A4W4 64-row skinny with 32 columns per workgroup ----
-        skinny(kA4W4, 4, false, pre, launch_skinny<kFp4, 4, true, false, false, 2>, "a4w4", 32);
-        // ---- bf16 row-major B on the flat tiles: whole-line B copies into
-        // wave-private LDS regions (gemm_flat.h, BLDS) ----
-        tile(kA16W16, 256, 256, b16r, launch_flat<kBf16, 256, false, false>, "a16w16");
-        reg.back().name += "_flat";
-        // ---- skinny kernels with A (row-major bf16 B: A and B) copied
-        // through LDS in whole lines (gemm_skinny_lds.h); rank 1: the
-        // heuristic prefers them over the register-load forms above ----
-        auto staged = [&](Family f, int mf, Variant v, LaunchFn fn, const char* fam, int bn, const char* tag,
-                          int rank = 1) {
-            skinny(f, mf, false, v, fn, fam, bn);
-            reg.back().name += tag;
-            reg.back().rank = rank;
-        };
-        staged(kA16W16, 1, b16r, launch_skinny_alds<kBf16, 1, false, 2, 8, 2, true>, "a16w16", 32, "_lds");
-        staged(kA16W16, 2, b16r, launch_skinny_alds<kBf16, 2, false, 2, 8, 2, true>, "a16w16", 32, "_lds");
-        staged(kA16W16, 4, b16r, launch_skinny_alds<kBf16, 4, false, 2, 4, 2, true>, "a16w16", 32, "_lds");
-        staged(kA16W16, 1, b16r, launch_skinny_alds<kBf16, 1, false, 1, 8, 2, true>, "a16w16", 16, "_lds");
-        staged(kA16W16, 1, b16r, launch_skinny_alds<kBf16, 1, false, 1, 8, 3, true>, "a16w16", 16, "_lds_s3", 0);
-        staged(kA16W16, 2, b16r, launch_skinny_alds<kBf16, 2, false, 1, 8, 2, true>, "a16w16", 16, "_lds");
-        staged(kA16W16, 2, b16p, launch_skinny_alds<kBf16, 2, true, 2>, "a16w16", 32, "_alds");
-        staged(kA16W16, 4, b16p, launch_skinny_alds<kBf16, 4, true, 2>, "a16w16", 32, "_alds");
-        staged(kA4W4, 2, pre, launch_skinny_alds<kFp4, 2, true, 2>, "a4w4", 32, "_alds");
-        staged(kA4W4, 4, pre, launch_skinny_alds<kFp4, 4, true, 2>, "a4w4", 32, "_alds");
-        staged(kA4W4, 2, pre, launch_skinny_alds<kFp4, 2, true, 1>, "a4w4", 16, "_alds");
-        staged(kA8W4, 2, a8n, launch_skinny_alds<kFp8, 2, true, 2>, "a8w4", 32, "_alds");
-        // ---- split-K forms of the 256-row and 256-column bf16 row-major tiles
-        // (M = 256 with long K: every B byte read once) ----
-        tsplit(kA16W16, 256, 128, b16r, launch_t32<kBf16, false, 256, 128, 2, false, true>, "a16w16");
-        tsplit(kA16W16, 128, 256, b16r, launch_t32<kBf16, false, 128, 256, 2, false, true>, "a16w16");
+        RegBuilder b{reg};
+        b.part_mx();
+        b.part_bf16<false>();
+        b.part_bf16<true>();
+        b.part_persist_split();
+        b.part_rest();
     });
     return reg;
 }
@@ -570,10 +295,18 @@ struct WsVal {
     size_t bytes = 0;
 };
 
-float* workspace(int dev, hipStream_t st, size_t bytes, int slot = 0) {
+std::mutex& workspace_mutex() {
     static std::mutex mu;
+    return mu;
+}
+std::map<WsKey, WsVal>& workspace_map() {
     static std::map<WsKey, WsVal> ws;
-    std::lock_guard<std::mutex> lk(mu);
+    return ws;
+}
+
+float* workspace(int dev, hipStream_t st, size_t bytes, int slot = 0) {
+    std::lock_guard<std::mutex> lk(workspace_mutex());
+    auto& ws = workspace_map();
     WsVal& w = ws[{dev, st, slot}];
     if (w.bytes < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
@@ -599,6 +332,8 @@ struct GemmCall {
     const char* kernel_name;
     int kernel_id;    // < 0: use name / heuristic
     int log2_split;   // < 0: heuristic
+    // > 0: this many K splits (a literal KBatch, overrides log2_split)
+    int split_count = 0;
     // batch > 1: one launch with gridDim.z = batch; A, B, out describe batch 0
     // and the strides (bytes; bias in elements) step to the next batch
     int batch = 1;
@@ -742,7 +477,9 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     } else if (inst->skinny && inst->split) {
         splits = skinny_splits((int)((N + 15) / 16), ksteps, cus);
     }
-    if (inst->skinny && inst->split && c.log2_split >= 0) splits = 1 << c.log2_split;
+    // requested split count (0: the launcher chooses)
+    const int req_splits = c.split_count > 0 ? c.split_count : (c.log2_split >= 0 ? 1 << std::min(c.log2_split, 16) : 0);
+    if (inst->skinny && inst->split && req_splits > 0) splits = req_splits;
     if (inst->skinny) AA_CHECK(M <= inst->bm, "skinny kernel ", inst->name, " covers M <= ", inst->bm);
 
     if (!inst->skinny) {
@@ -753,7 +490,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         if (inst->split) {
             // split-K tile: stages of K over gridDim.y, f32 slices, then a sum
             const int nst = (int)(K / (scaled ? 256 : 64));
-            int sp = c.log2_split >= 0 ? (1 << c.log2_split) : tile_splits(tiles, nst, cus);
+            int sp = req_splits > 0 ? req_splits : tile_splits(tiles, nst, cus);
             if (batched) sp = 1;
             sp = std::max(1, std::min(sp, nst));
             p.k_steps_per_split = (nst + sp - 1) / sp;
@@ -1221,13 +958,13 @@ int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
     (void)semaphore;
     return safe_call([&] {
         DeviceGuard g(A ? A->device_id : -1);
-        int l2 = -1;
-        if (splitK > 1) {
-            l2 = 0;
-            while ((1 << (l2 + 1)) <= splitK) ++l2;
-        }
+        // splitK is a literal split count, capped at 16
+        // (csrc/py_itfs_cu/asm_gemm_a16w16.cu:111-114): 1 runs one pass; none
+        // (<= 0) lets the launcher choose (the reference raises for 1 with a
+        // split-K kernel; every split instance here has a one-pass twin)
         GemmCall c{kA16W16, {false, bpreshuffle != 0, out && out->dtype == AITER_DTYPE_fp32}, A, B,
-                   nullptr, nullptr, out, bias, 1.0f, 1.0f, kernelName, -1, l2};
+                   nullptr, nullptr, out, bias, 1.0f, 1.0f, kernelName, -1, -1};
+        if (splitK >= 1) c.split_count = std::min(splitK, 16);
         run_gemm(c, reinterpret_cast<hipStream_t>(stream));
     });
 }
@@ -1277,6 +1014,13 @@ static void opus_batched(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t*
     }
     GemmCall c{kA16W16, {false, false, Y->dtype == AITER_DTYPE_fp32}, &a, &w, nullptr, nullptr, &y, bptr,
                1.0f, 1.0f, nullptr, opus_kid ? -1 : kernelId, splitK > 0 ? splitK : -1};
+    // the opus API passes a literal KBatch with its kernel id, <= 1 meaning
+    // one pass (aiter/ops/opus/gemm_op_a16w16.py:488); the CK batched API
+    // passes its log2
+    if (opus_kid) {
+        c.log2_split = -1;
+        c.split_count = kernelId >= 0 ? std::max(splitK, 1) : 0;
+    }
     if (opus_kid && kernelId >= 0)
         AA_CHECK(decode_opus_kid(kernelId, &c.ref_tile), "unknown opus kernel id ", kernelId,
                  " (not in the gfx950 opus table)");
@@ -1453,6 +1197,40 @@ int fused_gemm_afp4wfp4_a16w16(aiter_tensor_t* x_fp4, aiter_tensor_t* w_fp4, ait
         GemmCall c{kA16W16, {false, false, false}, x_bf16, w_bf16, nullptr, nullptr, y_bf16, bias_bf16,
                    1.0f, 1.0f, kernel_bf16, -1, -1};
         run_gemm(c, st);
+    });
+}
+
+// Bytes of the split-K workspace held for (device, stream), 0 if none
+// (introspection: the tests read what a call reserved).
+int64_t aiter_amd_workspace_bytes(int device, aiter_stream_t stream) {
+    std::lock_guard<std::mutex> lk(workspace_mutex());
+    auto& ws = workspace_map();
+    auto it = ws.find(WsKey{device, reinterpret_cast<hipStream_t>(stream), 0});
+    return it == ws.end() ? 0 : (int64_t)it->second.bytes;
+}
+
+// Frees every library workspace held for (device, stream) after the
+// stream's work completes; the next call that needs one allocates it again.
+int aiter_amd_workspace_release(int device, aiter_stream_t stream) {
+    return safe_call([&] {
+        DeviceGuard g(device);
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        AA_HIP(hipStreamIsCapturing(st, &cs));
+        AA_CHECK(cs == hipStreamCaptureStatusNone, "workspaces cannot be released during graph capture");
+        std::lock_guard<std::mutex> lk(workspace_mutex());
+        auto& ws = workspace_map();
+        for (auto it = ws.begin(); it != ws.end();) {
+            if (it->first.dev == device && it->first.st == st) {
+                if (it->second.ptr) {
+                    AA_HIP(hipStreamSynchronize(st));
+                    AA_HIP(hipFree(it->second.ptr));
+                }
+                it = ws.erase(it);
+            } else {
+                ++it;
+            }
+        }
     });
 }
 

@@ -2,9 +2,10 @@
 
 ``gemm_a16w16_opus(A, B, bias, dtype, kernelId, splitK, out)`` takes bf16
 A [b, M, K] (or [M, K]) and B [b, N, K] (or [N, K]) and returns
-Y [b, M, N] = A @ B^T (+ bias [N] or [b, N]).  ``kernelId`` indexes this
-library's kernel table (``aiter_amd._lib.kernel_table()``); None uses the
-tuned CSV / heuristic.
+Y [b, M, N] = A @ B^T (+ bias [N] or [b, N]).  ``kernelId`` is a reference
+opus kernel id (csrc/opus_gemm/opus_gemm_common.py:238-513), run on this
+library's kernel of the same tile (or its heuristic choice where it has
+none), with ``splitK`` the literal split count; None uses the heuristic.
 """
 from __future__ import annotations
 
@@ -47,7 +48,15 @@ def _validate_and_reshape(A: Tensor, B: Tensor, bias: Tensor | None):
 
 def opus_gemm_a16w16_tune(XQ: Tensor, WQ: Tensor, Y: Tensor, bias: Tensor | None = None, kernelId: int = 0,
                           splitK: int = 0) -> Tensor:
-    """Explicit-kernel entry (csrc/opus_gemm/opus_gemm.cu:294-350)."""
+    """Explicit-kernel entry (csrc/opus_gemm/opus_gemm.cu:294-350).  ``splitK``
+    is a literal split count (KBatch); 0 or 1 runs one pass.
+
+    Older positional calls ``opus_gemm_a16w16_tune(XQ, WQ, Y, kernelId, splitK)``
+    keep working as in aiter/ops/opus/gemm_op_a16w16.py:196-210: an int in the
+    bias slot is the kernel id and the next positional int the split count."""
+    if isinstance(bias, int) and not isinstance(bias, bool):
+        new_split = splitK if (splitK != 0 and kernelId == 0) else kernelId
+        kernelId, splitK, bias = bias, new_split, None
     call("opus_gemm_a16w16_tune", XQ, WQ, Y, bias, int(kernelId), int(splitK))
     return Y
 

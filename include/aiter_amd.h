@@ -116,7 +116,8 @@ int mxfp8_mxfp4_gemm_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* S
  * out[M,N] (bf16 or f32) = A[M,K] @ B[N,K]^T (+ bias f32 [N]).  B row-major
  * or preshuffled (bpreshuffle=1, shuffle_weight (16,16)).  `semaphore` is
  * accepted for signature compatibility and unused (split-K partials go to a
- * library-owned per-stream workspace). */
+ * library-owned per-stream workspace).  splitK is a literal split count,
+ * capped at 16 (asm_gemm_a16w16.cu:111-114); <= 0 lets the launcher choose. */
 int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
                     aiter_tensor_t* semaphore, aiter_tensor_t* bias, int splitK,
                     const char* kernelName, int bpreshuffle, aiter_stream_t stream);
@@ -127,7 +128,9 @@ int gemm_a16w16_asm(aiter_tensor_t* A, aiter_tensor_t* B, aiter_tensor_t* out,
  * kid (csrc/opus_gemm/opus_gemm_common.py:238-513: 4-9, 200-223, 300-315,
  * 1400-1404 and their +1000 / +2000..+4000 / +5000 variants): the kernel of
  * the same tile here when there is one and M > 32, else the heuristic
- * choice; ids outside the gfx950 table are an error; < 0 = heuristic. */
+ * choice; ids outside the gfx950 table are an error; < 0 = heuristic.
+ * splitK is the literal KBatch of that kernel id, <= 1 one pass
+ * (aiter/ops/opus/gemm_op_a16w16.py:488). */
 int opus_gemm(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
               aiter_tensor_t* bias, aiter_stream_t stream);
 int opus_gemm_a16w16_tune(aiter_tensor_t* XQ, aiter_tensor_t* WQ, aiter_tensor_t* Y,
@@ -329,6 +332,17 @@ int aiter_amd_resolve_opus_kid(int kid, int out_f32, int64_t M);
  * tensor of csrc/py_itfs_cu/asm_gemm_a16w16.cu:192-205 and
  * aiter/ops/opus/gemm_op_opus.py (opus_gemm_workspace_init). */
 int gemm_workspace_reserve(int device, aiter_stream_t stream, size_t bytes);
+
+/* Introspection, no counterpart in the reference: bytes of the split-K
+ * workspace currently held for (device, stream), 0 if none.  Tests read it
+ * to check the split count a call used (fp32 partials: splits * M * N * 4). */
+int64_t aiter_amd_workspace_bytes(int device, aiter_stream_t stream);
+
+/* No counterpart in the reference: frees every library workspace held for
+ * (device, stream) once the stream's queued work has completed (a later call
+ * that needs one allocates it again).  Not allowed during graph capture.
+ * Returns 0 or -1 (message in aiter_get_last_error). */
+int aiter_amd_workspace_release(int device, aiter_stream_t stream);
 
 /* ---- calibration ---------------------------------------------------------
  * No counterpart in the reference: a plain streaming read of src (contiguous

@@ -89,6 +89,38 @@ def test_opus_reference_kernel_ids(cuda, kid, m, n, k):
     _bf16_check(out, x, w, m, n, kid + 2, bias.numpy())
 
 
+@pytest.mark.parametrize("entry,split,expect", [("opus", 5, 5), ("opus", 4, 4), ("opus", 1, 0), ("opus", 0, 0),
+                                                ("asm", 5, 5), ("asm", 1, 0)])
+def test_split_count_is_literal(cuda, entry, split, expect):
+    """splitK of the opus API and of gemm_a16w16_asm is a literal split count
+    (aiter/ops/opus/gemm_op_a16w16.py:488, csrc/py_itfs_cu/asm_gemm_a16w16.cu:113-114;
+    <= 1 runs one pass).  Opus kid 200 (64x64) and the reference's 64x64 split-K ASM
+    name are split-K tiles here too; the call reserves its f32 partials,
+    splits * M * N * 4 bytes, in the stream's workspace, so the stream's
+    workspace size after the call, released first, gives the split count it
+    ran (torch hands out pooled streams, which earlier calls may have used)."""
+    import aiter_amd
+    from aiter_amd._lib import lib
+
+    m, n, k = 64, 1024, 1280   # 20 K stages of 64: 5 and 4 splits divide them evenly
+    announce(f"split count {entry} splitK={split}")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        x = _randn_bf16(m, k, 40 + split, cuda)
+        w = _randn_bf16(n, k, 41 + split, cuda)
+        assert lib().aiter_amd_workspace_release(cuda.index or 0, s.cuda_stream) == 0
+        if entry == "opus":
+            out = aiter_amd.gemm_a16w16_opus(x, w, kernelId=200, splitK=split)
+        else:
+            out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+            aiter_amd.gemm_a16w16_asm(x, w, out, splitK=split,
+                                      kernelName="_ZN5aiter39bf16gemm_fp32bf16_tn_64x64_splitk_cleanE")
+        s.synchronize()
+        held = lib().aiter_amd_workspace_bytes(cuda.index or 0, s.cuda_stream)
+    assert held == expect * m * n * 4, f"workspace {held} B, expected {expect} splits of {m}x{n} f32"
+    _bf16_check(out, x, w, m, n, 42 + split)
+
+
 def test_opus_unknown_kernel_id_raises(cuda):
     import aiter_amd
 
