@@ -604,6 +604,21 @@ def profile_workload(dev, name):
     elif name == "fused_rms_mxfp4_8192":
         x, w = bf16(8192, 8192), bf16(1, 8192).view(-1)
         fn = lambda: aiter_amd.fused_rms_mxfp4_quant(x, w, 1e-6, shuffle=True)
+    elif _shape_workload(name):
+        # "<a4w4|bf16|a8w4>_<M>x<N>x<K>": that GEMM through its public entry
+        fam, (m, n, k) = _shape_workload(name)
+        if fam == "a4w4":
+            aq, as_, bq, bs = quantised_operands(m, n, k, 0, dev)
+            fn = lambda: aiter_amd.gemm_a4w4(aq, bq, as_, bs)
+        elif fam == "a8w4":
+            x, w = bf16(m, k), bf16(n, k)
+            wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+            wq = aiter_amd.shuffle_weight(wq)
+            xq, xs = aiter_amd.dynamic_mxfp8_quant(x, shuffle=True)
+            fn = lambda: aiter_amd.gemm_a8w4_mxfp8(xq, wq, xs, ws, a_preshuffle=False)
+        else:
+            a, b = bf16(m, k), bf16(n, k)
+            fn = lambda: aiter_amd.gemm_a16w16(a, b)
     else:
         raise SystemExit(f"unknown workload {name}")
     fn()
@@ -614,6 +629,16 @@ def profile_workload(dev, name):
         fn()
     torch.cuda.synchronize()
     log(f"profile workload done: copy {COPY_BYTES} B x6, {name} x3 (+1 warm-up call)")
+
+
+def _shape_workload(name):
+    """("a4w4" | "bf16" | "a8w4", (M, N, K)) for a workload named
+    "<family>_<M>x<N>x<K>", else None."""
+    fam, _, dims = name.partition("_")
+    parts = dims.split("x")
+    if fam not in ("a4w4", "bf16", "a8w4") or len(parts) != 3 or not all(p.isdigit() for p in parts):
+        return None
+    return fam, tuple(int(p) for p in parts)
 
 
 def traffic_from_profiles():

@@ -50,3 +50,12 @@ def allclose_report(got: np.ndarray, ref: np.ndarray, rtol=1e-2, atol=1e-2):
     idx = np.argwhere(bad)[:5]
     return False, (f"{n_bad}/{bad.size} elements out of tolerance; max err {err.max():.4g}; "
                    f"first {[tuple(i) + (got[tuple(i)], ref[tuple(i)]) for i in idx]}")
+
+
+def tile_samples(n: int, band: int, seed: int) -> np.ndarray:
+    """One index in every band of `band` consecutive indices of range(n)
+    (random offset inside the band): a grid of row samples x column samples
+    then touches every output tile of `band` x `band` or larger."""
+    rs = np.random.default_rng(seed)
+    starts = np.arange(0, n, band)
+    return np.array([s + rs.integers(0, min(band, n - s)) for s in starts], dtype=np.int64)

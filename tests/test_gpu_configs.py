@@ -22,7 +22,7 @@ import torch
 
 from oracle import mx_oracle as O
 from tests.conftest import announce
-from tests.mx_inputs import allclose_report, mxfp4_operand
+from tests.mx_inputs import allclose_report, mxfp4_operand, tile_samples
 
 pytestmark = pytest.mark.gpu
 
@@ -92,22 +92,37 @@ def test_decode_a4w4_all_elements(cuda, m, mode):
 
 
 # ------------------------------------------------------------------ long-K prefill
+def _grid(m, n, n_rows, n_cols, seed):
+    """Sampled rows x columns: for M or N beyond 128, one index in every band
+    of 128 (so the grid touches every output tile of every instance) plus
+    random ones."""
+    rows = _sample(m, n_rows, seed)
+    cols = _sample(n, n_cols, seed + 1)
+    if m > 128:
+        rows = np.union1d(rows, tile_samples(m, 128, seed + 2))
+    if n > 128:
+        cols = np.union1d(cols, tile_samples(n, 128, seed + 3))
+    return rows, cols
+
+
 def _a4w4_on_the_fly(m, n, k, seed, cuda, n_rows=16, n_cols=256, what=""):
     """bf16 N(0,1) activations and weights quantised on the GPU
-    (get_triton_quant(per_1x32)), weights preshuffled, gemm_a4w4 through the
-    tuned table; quant bytes and sampled outputs checked."""
+    (get_triton_quant(per_1x32)), weights preshuffled, the tuned dispatch of
+    gemm_a4w4 into a NaN-filled output; every output element finite (every
+    tile written), quant bytes and sampled outputs checked."""
     import aiter_amd
+    from aiter_amd.gemm_op_a4w4 import _gemm_a4w4_into
 
     quant = aiter_amd.get_triton_quant(aiter_amd.QuantType.per_1x32)
     x = _randn_bf16(m, k, seed, cuda)
     w = _randn_bf16(n, k, seed + 1, cuda)
     xq, xs = quant(x, shuffle=True)
     wq, ws = quant(w, shuffle=True)
-    out = aiter_amd.gemm_a4w4(xq, aiter_amd.shuffle_weight(wq), xs, ws)
-    torch.cuda.synchronize()
-    assert out.shape == (m, n)
-    rows = _sample(m, n_rows, seed + 2)
-    cols = _sample(n, n_cols, seed + 3)
+    out = torch.full(((m + 31) // 32 * 32, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+    _gemm_a4w4_into(xq, aiter_amd.shuffle_weight(wq), xs, ws, out, None, 1.0, 0.0, True)
+    out = out[:m]
+    assert bool(torch.isfinite(out).all()), f"{what}: output elements left unwritten (NaN)"
+    rows, cols = _grid(m, n, n_rows, n_cols, seed + 2)
     a_q, a_s = _check_fp4_rows(x, xq, xs, rows, f"{what} activation quant")
     b_q, b_s = _check_fp4_rows(w, wq, ws, cols, f"{what} weight quant")
     ref = O.bf16_bits_to_f32(O.gemm_a4w4_ref(a_q, b_q, a_s, b_s))
@@ -169,6 +184,8 @@ def test_sweep_bf16(cuda, m, n, k):
     table; sampled outputs against the f32 matmul of the bf16 operands."""
     import aiter_amd
 
+    from aiter_amd import tuned_gemm
+
     announce(f"sweep bf16 {m}x{n}x{k}")
     seed = 2000 + m + n + k
     x = _randn_bf16(m, k, seed, cuda)
@@ -176,9 +193,14 @@ def test_sweep_bf16(cuda, m, n, k):
     out = aiter_amd.gemm_a16w16(x, w)
     torch.cuda.synchronize()
     assert out.shape == (m, n) and out.dtype == torch.bfloat16
-    rows = _sample(m, 16, seed + 2)
-    cols = _sample(n, 256, seed + 3)
+    # the same dispatch into a NaN-filled output: every tile written, same bits
+    cfg = aiter_amd.get_GEMM_A16W16_config(m, n, k, False, str(x.dtype), str(x.dtype), False, False)
+    poisoned = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+    tuned_gemm._run(x, w, None, torch.bfloat16, False, cfg, out=poisoned)
+    assert bool(torch.isfinite(poisoned).all()), "output elements left unwritten (NaN)"
+    rows, cols = _grid(m, n, 16, 256, seed + 2)
     a_bits = _take_rows(x, rows).view(torch.int16).cpu().numpy().view(np.uint16)
     b_bits = _take_rows(w, cols).view(torch.int16).cpu().numpy().view(np.uint16)
     ref = O.bf16_bits_to_f32(O.gemm_a16w16_ref(a_bits, b_bits))
     _check_out(out, rows, cols, ref, "gemm_a16w16")
+    _check_out(poisoned, rows, cols, ref, "gemm_a16w16 into a NaN-filled output")

@@ -118,6 +118,95 @@ def test_fused_gemm_split_cat(cuda, m, d, s1, s2, s3, preshuffled):
         assert ok, f"{what}: {msg}"
 
 
+def _force_a4w4_row(monkeypatch, tmp_path, m, n, k, name):
+    """A tuned A4W4 table holding one row, (m, n, k) -> kernel `name`."""
+    import pandas as pd
+
+    from aiter_amd import config, gemm_op_a4w4
+
+    row = {"gfx": "gfx950", "cu_num": 256, "M": m, "N": n, "K": k, "kernelId": 0, "splitK": 0, "us": 1.0,
+           "kernelName": name, "tflops": 1.0, "bw": 1.0, "errRatio": 0.0}
+    p = tmp_path / "a4w4_one_row.csv"
+    pd.DataFrame([row]).to_csv(p, index=False)
+    monkeypatch.setenv("AITER_CONFIG_GEMM_A4W4", str(p))
+    monkeypatch.setenv("GPU_ARCHS", "gfx950")
+    monkeypatch.setenv("CU_NUM", "256")
+    for f in (config.get_gfx, config.get_cu_num, gemm_op_a4w4._a4w4_table, gemm_op_a4w4.get_GEMM_config):
+        f.cache_clear()
+
+
+def _clear_tables():
+    from aiter_amd import config, gemm_op_a4w4
+
+    for f in (config.get_gfx, config.get_cu_num, gemm_op_a4w4._a4w4_table, gemm_op_a4w4.get_GEMM_config):
+        f.cache_clear()
+
+
+# the epilogue paths of the long-K decode shapes the Triton ops serve:
+# * skinny split-K (heuristic at M = 16, N = 2048: 128 column blocks, half the
+#   CUs) -> the fused operation in splitk_finish_kernel;
+# * a split tile named by the tuned table, long K -> in splitk_reduce_kernel;
+# * the persistent 256x256 tile named by the tuned table -> the host runs its
+#   one-tile twin, which carries the operation.
+EPI_PATHS = [
+    ("skinny_splitk", 16, 2048, 8192, None),
+    ("tile_splitk", 64, 1024, 8192, "a4w4_tile_64x128_splitk"),
+    ("persistent_twin", 512, 2048, 1024, "a4w4_tile_256x256_persist"),
+]
+
+
+@pytest.mark.parametrize("path,m,n,k,name", EPI_PATHS)
+@pytest.mark.parametrize("preshuffled", [True, False])
+def test_fused_mul_add_epilogue_paths(cuda, monkeypatch, tmp_path, path, m, n, k, name, preshuffled):
+    import aiter_amd
+
+    if name is not None:
+        if not preshuffled:
+            pytest.skip("tuned rows name preshuffled-B kernels only; the plain form runs the heuristic")
+        _force_a4w4_row(monkeypatch, tmp_path, m, n, k, name)
+    announce(f"fused mul_add path={path} {m}x{n}x{k} pre={preshuffled}")
+    try:
+        a_q, a_s, a_ss, b_q, b_s, b_ss, c = _case(m, n, k, 61)
+        x, w, xs, ws = _operands(cuda, preshuffled, m, n, k, a_q, a_s, a_ss, b_q, b_s, b_ss)
+        a, a_ref = _mul_add_operand("bf16", m, n, 62, cuda)
+        b, b_ref = _mul_add_operand("f32", m, n, 63, cuda)
+        op = aiter_amd.fused_gemm_afp4wfp4_preshuffle_add_mul if preshuffled else aiter_amd.fused_gemm_afp4wfp4_mul_add
+        y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+        out = op(x, w, xs, ws, a, b, torch.bfloat16, y=y, fuse_type=0)
+        torch.cuda.synchronize()
+    finally:
+        _clear_tables()
+    ref = O.bf16_bits_to_f32(O.mul_add_ref(c, a_ref, b_ref, 0))
+    ok, msg = allclose_report(out.float().cpu().numpy(), ref)
+    assert ok, msg
+
+
+@pytest.mark.parametrize("path,m,n,k,name", EPI_PATHS)
+def test_fused_split_cat_epilogue_paths(cuda, monkeypatch, tmp_path, path, m, n, k, name):
+    import aiter_amd
+
+    d, s2, s3 = 4, 128, 32
+    s1 = n // d - s2
+    if name is not None:
+        _force_a4w4_row(monkeypatch, tmp_path, m, n, k, name)
+    announce(f"fused split_cat path={path} {m}x{n}x{k}")
+    try:
+        a_q, a_s, a_ss, b_q, b_s, b_ss, c = _case(m, n, k, 71)
+        x, w, xs, ws = _operands(cuda, True, m, n, k, a_q, a_s, a_ss, b_q, b_s, b_ss)
+        y = to_bf16_f32(randn((m, d, s3), 72))
+        c1, c2 = aiter_amd.fused_gemm_afp4wfp4_preshuffle_split_cat(x, w, _dev(y, cuda).to(torch.bfloat16), xs, ws,
+                                                                     s1, s2, torch.bfloat16)
+        torch.cuda.synchronize()
+    finally:
+        _clear_tables()
+    r1, r2 = O.split_cat_ref(O.bf16_bits_to_f32(O.f32_to_bf16_bits(c)), y, s1, s2)
+    g1, g2 = c1.float().cpu().numpy(), c2.float().cpu().numpy()
+    assert np.array_equal(g1[:, :, s1:], y), "y must be copied unchanged"
+    for got, ref, what in ((g1[:, :, :s1], r1[:, :, :s1], "c1"), (g2, r2, "c2")):
+        ok, msg = allclose_report(got, ref)
+        assert ok, f"{what}: {msg}"
+
+
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("preshuffled", [True, False])
 @pytest.mark.parametrize("m", [1, 16, 64, 300])

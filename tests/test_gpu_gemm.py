@@ -9,7 +9,7 @@ import torch
 
 from oracle import mx_oracle as O
 from tests.conftest import announce
-from tests.mx_inputs import allclose_report, bf16_operand, mxfp4_operand, mxfp8_operand
+from tests.mx_inputs import allclose_report, bf16_operand, mxfp4_operand, mxfp8_operand, tile_samples
 
 pytestmark = pytest.mark.gpu
 
@@ -122,25 +122,28 @@ def test_gemm_a4w4_bias_alpha_beta(cuda):
         assert ok, f"{name}: {msg}"
 
 
-def test_gemm_a4w4_full_size_spot_check(cuda):
-    """M=N=K=8192 (BASELINE prefill config): 256 random (m, n) outputs
-    against the oracle's f32 dot products of the dequantised rows."""
+def test_gemm_a4w4_full_size_every_tile(cuda):
+    """M=N=K=8192 (BASELINE prefill config) through the tuned dispatch into a
+    NaN-filled output: every element finite (every tile written), and one
+    element of every 128x128 block (64 x 64 samples: every tile of every
+    instance) against the oracle's f32 dot products of the dequantised rows."""
     import aiter_amd
+    from aiter_amd.gemm_op_a4w4 import _gemm_a4w4_into
 
     m = n = k = 8192
-    announce("a4w4 8192^3 spot check")
+    announce(f"a4w4 8192^3 every tile, kernel={aiter_amd.get_GEMM_config(m, n, k)}")
     g = torch.Generator(device="cpu").manual_seed(0)
     x = torch.randn((m, k), generator=g, dtype=torch.float32).to(torch.bfloat16).to(cuda)
     w = torch.randn((n, k), generator=g, dtype=torch.float32).to(torch.bfloat16).to(cuda)
     xq, xs = aiter_amd.dynamic_mxfp4_quant(x, shuffle=True)
     wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
-    out = aiter_amd.gemm_a4w4(xq, aiter_amd.shuffle_weight(wq), xs, ws)
-    torch.cuda.synchronize()
-    rs = np.random.default_rng(1)
-    rows = rs.choice(m, 16, replace=False)
-    cols = rs.choice(n, 16, replace=False)
-    a_q = xq.view(torch.uint8)[rows].cpu().numpy()
-    b_q = wq.view(torch.uint8)[cols].cpu().numpy()
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+    _gemm_a4w4_into(xq, aiter_amd.shuffle_weight(wq), xs, ws, out, None, 1.0, 0.0, True)
+    assert bool(torch.isfinite(out).all()), "output elements left unwritten (NaN)"
+    rows = tile_samples(m, 128, 1)
+    cols = tile_samples(n, 128, 2)
+    a_q = xq.view(torch.uint8)[torch.from_numpy(rows).to(cuda)].cpu().numpy()
+    b_q = wq.view(torch.uint8)[torch.from_numpy(cols).to(cuda)].cpu().numpy()
     xs_np = xs.view(torch.uint8).cpu().numpy()
     ws_np = ws.view(torch.uint8).cpu().numpy()
     a_s = O.unshuffle_scale(xs_np, m, k // 32)[rows]

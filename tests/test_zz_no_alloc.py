@@ -59,3 +59,50 @@ def test_no_alloc_rejects_oversized_partials(cuda):
     out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
     with pytest.raises(RuntimeError, match="scratch"):
         call("gemm_a4w4_asm_noalloc", A, B, As, Bs, out, "a4w4_tile_64x128_splitk", None, 1.0, 0.0, 1, 4)
+
+
+def test_no_alloc_reserves_nothing_and_captures(cuda):
+    """The no-allocation entry never touches the library workspace: on a
+    stream whose workspace was released it leaves the workspace at 0 bytes
+    (gemm_a4w4_asm on another released stream reserves its split-K partials
+    there, which shows the probe sees a reservation), and it captures in a
+    HIP graph on that stream, where a workspace reservation would raise;
+    every replay equals the eager output."""
+    from aiter_amd._lib import call, lib
+
+    m, n, k = 16, 2048, 16384     # skinny split-K (heuristic): partials needed
+    announce(f"no-alloc workspace probe and graph capture {m}x{n}x{k}")
+    A, B, As, Bs, ref = _case(m, n, k, 95, cuda)
+    dev = cuda.index or 0
+    pad = (m + 31) // 32 * 32
+
+    s_lib = torch.cuda.Stream()
+    with torch.cuda.stream(s_lib):
+        out_lib = torch.empty((pad, n), dtype=torch.bfloat16, device=cuda)
+        assert lib().aiter_amd_workspace_release(dev, s_lib.cuda_stream) == 0
+        call("gemm_a4w4_asm", A, B, As, Bs, out_lib, None, None, 1.0, 0.0, 1, 0)
+        s_lib.synchronize()
+    assert lib().aiter_amd_workspace_bytes(dev, s_lib.cuda_stream) > 0
+
+    s = torch.cuda.Stream()
+    assert s.cuda_stream != s_lib.cuda_stream
+    with torch.cuda.stream(s):
+        eager = torch.full((pad, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+        assert lib().aiter_amd_workspace_release(dev, s.cuda_stream) == 0
+        call("gemm_a4w4_asm_noalloc", A, B, As, Bs, eager, None, None, 1.0, 0.0, 1, 0)
+        s.synchronize()
+        assert lib().aiter_amd_workspace_bytes(dev, s.cuda_stream) == 0
+        out = torch.full((pad, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            call("gemm_a4w4_asm_noalloc", A, B, As, Bs, out, None, None, 1.0, 0.0, 1, 0)
+        for i in range(3):
+            out.fill_(float("nan"))
+            g.replay()
+            s.synchronize()
+            assert torch.equal(out[:m], eager[:m]), f"replay {i} differs from the eager no-alloc output"
+        assert lib().aiter_amd_workspace_bytes(dev, s.cuda_stream) == 0
+    assert torch.equal(eager[:m], out_lib[:m])
+    ok, msg = allclose_report(eager[:m].float().cpu().numpy(), ref)
+    assert ok, msg
