@@ -75,13 +75,20 @@ def sweep_shapes(family: str):
 
 
 # ---------------------------------------------------------------- references
-def _dequant_fp4(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
-    """fp4x2 [R, K/2] + plain e8m0 [R, K/32] -> f32 [R, K] (aiter/utility/fp4_utils.py:25-52,213-221)."""
+def _dequant_fp4(q: torch.Tensor, s: torch.Tensor, chunk: int = 4096) -> torch.Tensor:
+    """fp4x2 [R, K/2] + plain e8m0 [R, K/32] -> f32 [R, K] (aiter/utility/fp4_utils.py:25-52,213-221),
+    `chunk` rows at a time (the index temporaries of a whole large weight would
+    take several times its f32 size)."""
     lut = torch.tensor(E2M1, dtype=torch.float32, device=q.device)
     q = q.view(torch.uint8)
-    codes = torch.stack((q & 0xF, q >> 4), dim=-1).reshape(q.shape[0], -1).long()
-    scale = torch.exp2(s.view(torch.uint8).float() - 127.0).repeat_interleave(32, dim=1)
-    return lut[codes] * scale
+    s = s.view(torch.uint8)
+    out = torch.empty((q.shape[0], q.shape[1] * 2), dtype=torch.float32, device=q.device)
+    for r0 in range(0, q.shape[0], chunk):
+        qq = q[r0:r0 + chunk]
+        codes = torch.stack((qq & 0xF, qq >> 4), dim=-1).reshape(qq.shape[0], -1).int()
+        scale = torch.exp2(s[r0:r0 + chunk].float() - 127.0).repeat_interleave(32, dim=1)
+        out[r0:r0 + chunk] = lut[codes] * scale
+    return out
 
 
 def _dequant_fp8(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
@@ -93,6 +100,26 @@ def err_ratio(out: torch.Tensor, ref: torch.Tensor, rtol=1e-2, atol=1e-2) -> flo
     """Fraction of elements outside atol + rtol*|ref| (aiter/test_common.py:479-490)."""
     bad = (out.float() - ref).abs() > atol + rtol * ref.abs()
     return bad.float().mean().item()
+
+
+REF_ROWS = 256   # above this many rows the candidates are checked on a seeded row sample
+
+
+def _ref_rows(M: int, dev) -> torch.Tensor | None:
+    """Rows of the output the candidates are checked on: all (None) up to
+    2 * REF_ROWS rows, else REF_ROWS seeded ones, so the f32 reference of a
+    large shape stays small."""
+    if M <= 2 * REF_ROWS:
+        return None
+    g = torch.Generator(device="cpu").manual_seed(M)
+    return torch.randperm(M, generator=g)[:REF_ROWS].sort().values.to(dev)
+
+
+def iters_for(flop: float, nbytes: float, cap: int) -> int:
+    """Calls per timed graph replay: about 2 ms of work (at 4 PFLOP/s or
+    5 TB/s, whichever is slower), between 2 and `cap`."""
+    est = max(flop / 4e15, nbytes / 5e12, 1e-6)
+    return max(2, min(cap, int(2e-3 / est)))
 
 
 # ---------------------------------------------------------------- timing
@@ -170,21 +197,24 @@ def tune_mx(family: str, M: int, N: int, K: int, iters: int, max_err_ratio: floa
     b = torch.randn((N, K), generator=g).to(dev)
     bq, bs_plain = dynamic_mxfp4_quant(b, shuffle=False)
     _, bs = dynamic_mxfp4_quant(b, shuffle=True)
+    rows = _ref_rows(M, dev)
     if family == "a4w4":
         aq, as_plain = dynamic_mxfp4_quant(a, shuffle=False)
         _, as_ = dynamic_mxfp4_quant(a, shuffle=True)
-        deq_a = _dequant_fp4(aq, as_plain)
+        deq_a = _dequant_fp4(aq if rows is None else aq[rows], as_plain if rows is None else as_plain[rows])
         a_bytes = M * K // 2
     else:
         aq, as_plain = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=False)
         _, as_ = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=True)
-        deq_a = _dequant_fp8(aq, as_plain)
+        deq_a = _dequant_fp8(aq if rows is None else aq[rows], as_plain if rows is None else as_plain[rows])
         a_bytes = M * K
+    del a, b
     prev_tf32 = torch.backends.cuda.matmul.allow_tf32
     torch.backends.cuda.matmul.allow_tf32 = False
     ref = deq_a @ _dequant_fp4(bq, bs_plain).t()
     torch.backends.cuda.matmul.allow_tf32 = prev_tf32
-    del a, b, deq_a
+    del deq_a
+    iters = iters_for(2.0 * M * N * K, a_bytes + N * K / 2 + 2 * M * N, iters)
     bqs = shuffle_weight(bq)
     n_copies = _copies(bqs.numel() + bs.numel())
     wq = [bqs] + [bqs.clone() for _ in range(n_copies - 1)]
@@ -208,7 +238,7 @@ def tune_mx(family: str, M: int, N: int, K: int, iters: int, max_err_ratio: floa
         except RuntimeError as e:
             _log(f"  skip {name}: {e}")
             continue
-        er = err_ratio(out[:M], ref)
+        er = err_ratio(out[:M] if rows is None else out[rows], ref)
         if er > max_err_ratio:
             _log(f"  reject {name} split {l2}: errRatio {er:.4f}")
             continue
@@ -236,12 +266,14 @@ def tune_bf16(M: int, N: int, K: int, bias: bool, otype: torch.dtype, bpreshuffl
     a = torch.randn((M, K), generator=g).to(dtypes.bf16).to(dev)
     b = torch.randn((N, K), generator=g).to(dtypes.bf16).to(dev)
     bias_t = torch.randn((N,), generator=g).to(dev) if bias else None
+    rows = _ref_rows(M, dev)
     prev_tf32 = torch.backends.cuda.matmul.allow_tf32
     torch.backends.cuda.matmul.allow_tf32 = False
-    ref = a.float() @ b.float().t()
+    ref = (a if rows is None else a[rows]).float() @ b.float().t()
     torch.backends.cuda.matmul.allow_tf32 = prev_tf32
     if bias_t is not None:
         ref = ref + bias_t
+    iters = iters_for(2.0 * M * N * K, 2.0 * (M * K + N * K + M * N), iters)
     bw_ = shuffle_weight(b) if bpreshuffle else b
     n_copies = _copies(bw_.numel() * 2)
     wb = [bw_] + [bw_.clone() for _ in range(n_copies - 1)]
@@ -260,7 +292,7 @@ def tune_bf16(M: int, N: int, K: int, bias: bool, otype: torch.dtype, bpreshuffl
         except RuntimeError as e:
             _log(f"  skip {name}: {e}")
             continue
-        er = err_ratio(out, ref)
+        er = err_ratio(out if rows is None else out[rows], ref)
         if er > max_err_ratio:
             _log(f"  reject {name} split {split}: errRatio {er:.4f}")
             continue
@@ -446,11 +478,15 @@ def _probe_arch(timeout: float):
     return gfx, int(cu)
 
 
-def worker_args(family: str, shape, tune_file: str, iters: int, max_err_ratio: float, compare: bool,
+def worker_args(family: str, shapes, tune_file: str, iters: int, max_err_ratio: float, compare: bool,
                 min_improvement_pct: float) -> list:
-    """Command-line arguments of the worker that tunes `shape`: the effective
-    improvement threshold is passed as is (``=`` form: it may be negative)."""
-    args = ["--family", family, "--worker", _shape_arg(family, shape), "-o", tune_file, "--iters", str(iters),
+    """Command-line arguments of the worker that tunes `shapes` (one shape
+    tuple or a list of them, passed ';'-separated): the effective improvement
+    threshold is passed as is (``=`` form: it may be negative)."""
+    if isinstance(shapes, tuple):
+        shapes = [shapes]
+    spec = ";".join(_shape_arg(family, s) for s in shapes)
+    args = ["--family", family, "--worker", spec, "-o", tune_file, "--iters", str(iters),
             f"--errRatio={max_err_ratio}"]
     if compare:
         args += ["--compare", f"--min_improvement_pct={min_improvement_pct}"]
@@ -458,37 +494,58 @@ def worker_args(family: str, shape, tune_file: str, iters: int, max_err_ratio: f
 
 
 def drive(family: str, shapes, tune_file: str, iters: int, max_err_ratio: float, retune_all: bool,
-          timeout: float, compare: bool = False, min_improvement_pct: float = 3.0, worker_cmd=None) -> dict:
-    """Tune `shapes` one worker process each.  Returns {"tuned": [...],
-    "skipped": [...], "failed": [(shape, reason)]}.  `worker_cmd` (tests)
-    replaces the worker's command line prefix."""
+          timeout: float, compare: bool = False, min_improvement_pct: float = 3.0, worker_cmd=None,
+          batch: int = 1, time_budget: float | None = None) -> dict:
+    """Tune `shapes`, `batch` shapes per worker process (each shape's row is
+    merged as soon as it is done; the watchdog allows `timeout` seconds per
+    shape of the batch).  Returns {"tuned": [...], "skipped": [...],
+    "failed": [(shape, reason)]}; after a failed worker, the shapes of its
+    batch that have no row yet are failed.  No new batch starts after
+    `time_budget` seconds (the rest is listed under "left").  `worker_cmd`
+    (tests) replaces the worker's command line prefix."""
     import subprocess
 
     gfx, cu = _probe_arch(max(60.0, timeout))
     done = set() if retune_all else tuned_keys(tune_file, family)
     res = {"tuned": [], "skipped": [], "failed": []}
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    todo = []
     for s in shapes:
         if _shape_key(family, gfx, cu, s) in done:
             _log(f"{family} {s}: already in {tune_file}, skipped")
             res["skipped"].append(s)
-            continue
-        _log(f"{family} {s}")
+        else:
+            todo.append(s)
+    batch = max(1, int(batch))
+    t_start = time.time()
+    for b0 in range(0, len(todo), batch):
+        group = todo[b0:b0 + batch]
+        _log(f"{family} {group[0] if len(group) == 1 else group}")
         cmd = list(worker_cmd) if worker_cmd else [sys.executable, "-m", "aiter_amd.tuner"]
-        cmd += worker_args(family, s, tune_file, iters, max_err_ratio, compare, min_improvement_pct)
+        cmd += worker_args(family, group, tune_file, iters, max_err_ratio, compare, min_improvement_pct)
+        if time_budget is not None and time.time() - t_start > time_budget:
+            _log(f"  time budget of {time_budget:.0f} s spent: {len(todo) - b0} shapes left for a resumed run")
+            res["left"] = todo[b0:]
+            break
+        reason = None
         try:
-            r = subprocess.run(cmd, cwd=root, timeout=timeout, capture_output=True, text=True)
-            sys.stdout.write(r.stdout)
+            # the worker's progress lines go straight to this process's stdout
+            sys.stdout.flush()
+            r = subprocess.run(cmd, cwd=root, timeout=timeout * len(group), stderr=subprocess.PIPE, text=True)
             if r.returncode != 0:
                 reason = f"worker exit {r.returncode}: {(r.stderr or '').strip().splitlines()[-1:]}"
+        except subprocess.TimeoutExpired:
+            reason = f"no result within {timeout * len(group):.0f} s"
+        if reason is None:
+            res["tuned"].extend(group)
+            continue
+        have = tuned_keys(tune_file, family)
+        for s in group:
+            if _shape_key(family, gfx, cu, s) in have and (retune_all or _shape_key(family, gfx, cu, s) not in done):
+                res["tuned"].append(s)
+            else:
                 _log(f"  FAILED {s}: {reason}")
                 res["failed"].append((s, reason))
-                continue
-        except subprocess.TimeoutExpired:
-            _log(f"  FAILED {s}: no result within {timeout:.0f} s")
-            res["failed"].append((s, "timeout"))
-            continue
-        res["tuned"].append(s)
     return res
 
 
@@ -509,6 +566,10 @@ def main(argv=None):
     ap.add_argument("--min_improvement_pct", type=float, default=3.0)
     ap.add_argument("--no_isolate", action="store_true",
                     help="tune every shape in this process (no worker processes, no watchdog)")
+    ap.add_argument("--batch", type=int, default=1,
+                    help="shapes per worker process (saves the process start-up; a failure costs the batch)")
+    ap.add_argument("--time_budget", type=float, default=None,
+                    help="start no new worker after this many seconds (a rerun resumes)")
     ap.add_argument("--worker", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args(argv)
     if args.worker is not None:
@@ -516,8 +577,13 @@ def main(argv=None):
         if not torch.cuda.is_available():
             print("the tuner needs a GPU", file=sys.stderr)
             return 2
-        return worker(args.family, _parse_shape(args.family, args.worker), args.tune_file, args.iters,
-                      args.errRatio, args.compare, args.min_improvement_pct)
+        for spec in args.worker.split(";"):
+            rc = worker(args.family, _parse_shape(args.family, spec), args.tune_file, args.iters,
+                        args.errRatio, args.compare, args.min_improvement_pct)
+            torch.cuda.empty_cache()
+            if rc:
+                return rc
+        return 0
     min_pct = args.min_improvement_pct if (args.compare and args.update_improved) else -1e30
     if args.untune_file:
         shapes = _read_untuned(args.untune_file, args.family)
@@ -542,7 +608,7 @@ def main(argv=None):
         _log(f"done in {time.time() - t0:.0f} s")
         return 0
     res = drive(args.family, shapes, args.tune_file, args.iters, args.errRatio, args.all, args.timeout,
-                args.compare, min_pct)
+                args.compare, min_pct, batch=args.batch, time_budget=args.time_budget)
     _log(f"tuned {len(res['tuned'])}, skipped {len(res['skipped'])}, failed {len(res['failed'])} "
          f"in {time.time() - t0:.0f} s")
     return 1 if res["failed"] else 0

@@ -22,16 +22,16 @@ FAKE = textwrap.dedent('''
     import sys, time
     from aiter_amd import tuner
     a = sys.argv[1:]
-    shape = tuner._parse_shape(a[a.index("--family") + 1], a[a.index("--worker") + 1])
     out = a[a.index("-o") + 1]
-    m, n, k = shape
-    if m == 2:
-        sys.exit(3)                      # a worker that dies
-    if m == 3:
-        time.sleep(300)                  # a worker that hangs
-    tuner.write_row(out, "a4w4", {"gfx": "gfx950", "cu_num": 256, "M": m, "N": n, "K": k, "kernelId": 7,
-                                  "splitK": 0, "us": 1.0 + m, "kernelName": "a4w4_skinny_m32", "tflops": 1.0,
-                                  "bw": 1.0, "errRatio": 0.0})
+    for spec in a[a.index("--worker") + 1].split(";"):
+        m, n, k = tuner._parse_shape(a[a.index("--family") + 1], spec)
+        if m == 2:
+            sys.exit(3)                  # a worker that dies
+        if m == 3:
+            time.sleep(300)              # a worker that hangs
+        tuner.write_row(out, "a4w4", {"gfx": "gfx950", "cu_num": 256, "M": m, "N": n, "K": k, "kernelId": 7,
+                                      "splitK": 0, "us": 1.0 + m, "kernelName": "a4w4_skinny_m32", "tflops": 1.0,
+                                      "bw": 1.0, "errRatio": 0.0})
 ''')
 
 
@@ -51,7 +51,7 @@ def test_driver_isolates_failures_and_resumes(tmp_path, fake_worker):
     res = tuner.drive("a4w4", shapes, out, 5, 0.05, False, timeout=WATCHDOG_S, worker_cmd=fake_worker)
     assert res["tuned"] == [(1, 256, 512), (4, 256, 512)]
     assert [s for s, _ in res["failed"]] == [(2, 256, 512), (3, 256, 512)]
-    assert "exit 3" in res["failed"][0][1] and res["failed"][1][1] == "timeout"
+    assert "exit 3" in res["failed"][0][1] and "no result within" in res["failed"][1][1]
     df = pd.read_csv(out)
     assert sorted(df.M.tolist()) == [1, 4]          # each shape's row landed when it finished
     # resume: finished shapes are skipped, failed ones are tried again
@@ -62,6 +62,18 @@ def test_driver_isolates_failures_and_resumes(tmp_path, fake_worker):
     res3 = tuner.drive("a4w4", [(1, 256, 512)], out, 5, 0.05, True, timeout=WATCHDOG_S, worker_cmd=fake_worker)
     assert res3["tuned"] == [(1, 256, 512)]
     assert sorted(pd.read_csv(out).M.tolist()) == [1, 4]
+
+
+def test_driver_batches_shapes(tmp_path, fake_worker):
+    """Several shapes per worker: each finished shape keeps its row; a worker
+    that dies fails the shapes of its batch without a row, and the next batch
+    runs."""
+    out = str(tmp_path / "tuned.csv")
+    shapes = [(1, 256, 512), (2, 256, 512), (4, 256, 512), (5, 256, 512), (6, 256, 512)]
+    res = tuner.drive("a4w4", shapes, out, 5, 0.05, False, timeout=WATCHDOG_S, worker_cmd=fake_worker, batch=2)
+    assert res["tuned"] == [(1, 256, 512), (4, 256, 512), (5, 256, 512), (6, 256, 512)]
+    assert [s for s, _ in res["failed"]] == [(2, 256, 512)]
+    assert sorted(pd.read_csv(out).M.tolist()) == [1, 4, 5, 6]
 
 
 def test_write_row_replaces_same_key(tmp_path):
