@@ -132,6 +132,7 @@ SIGNATURES = {
     "aiter_amd_workspace_bytes": ([ctypes.c_int, _S], ctypes.c_int64),
     "aiter_amd_workspace_release": ([ctypes.c_int, _S], ctypes.c_int),
     "hbm_stream_read": ([_T, _T, ctypes.c_int, _S], ctypes.c_int),
+    "hbm_stream_read_cfg": ([_T, _T] + [ctypes.c_int] * 4 + [_S], ctypes.c_int),
 }
 
 

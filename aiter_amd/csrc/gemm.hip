@@ -51,6 +51,7 @@ std::vector<Instance>& registry() {
         b.part_bf16<true>();
         b.part_persist_split();
         b.part_rest();
+        b.part_direct();
     });
     return reg;
 }
@@ -351,6 +352,9 @@ struct GemmCall {
     // output operation fused into the epilogue (fused_gemm_afp4wfp4_*); the
     // persistent kernels do not carry it, their one-tile twins do
     EpiOp epi{};
+    // plan only: a non-split skinny call stores its prepared parameters
+    // here instead of launching (the caller launches them in a combined grid)
+    GemmParams* capture = nullptr;
 };
 
 // split-K partial buffer of a call: the call's scratch when it brings one
@@ -364,10 +368,67 @@ float* split_buffer(const GemmCall& c, int dev, hipStream_t st, size_t need) {
     return workspace(dev, st, need);
 }
 
+// rows [m0, m0 + rows) of a tensor viewed as 2-D (row-major rows of its
+// last dimension), as a 2-D descriptor
+aiter_tensor_t row_slice(const aiter_tensor_t* t, int64_t m0, int64_t rows, const char* what) {
+    const int64_t ld = row_stride_2d(t, what);
+    aiter_tensor_t v = *t;
+    v.ptr = static_cast<uint8_t*>(t->ptr) + m0 * ld * (int64_t)dtype_size(t->dtype);
+    v.ndim = 2;
+    v.shape[0] = rows;
+    v.shape[1] = cols_2d(t);
+    v.strides[0] = ld;
+    v.strides[1] = 1;
+    v.numel = (size_t)(rows * cols_2d(t));
+    return v;
+}
+
+void run_gemm(const GemmCall& c, hipStream_t stream);
+
+// The kernels address A, out and the scales through 32-bit byte offsets: a
+// call whose output or A reaches 2 GiB runs as row chunks of a multiple of
+// 256 rows (shuffled scales keep whole 32-row groups contiguous, so a chunk's
+// A scales start m0 * K/32 bytes in).  Returns false when no chunking is needed.
+bool run_gemm_chunked(const GemmCall& c, hipStream_t stream) {
+    const int64_t M = rows_2d(c.A);
+    const int64_t orow = row_stride_2d(c.out, "out") * (int64_t)dtype_size(c.out->dtype);
+    const int64_t arow = row_stride_2d(c.A, "A") * (int64_t)dtype_size(c.A->dtype);
+    const int64_t lim = (int64_t)1 << 31;
+    if (M <= 256 || (M * orow < lim && M * arow < lim)) return false;
+    AA_CHECK(c.batch == 1 && !c.capture && !c.out_fp4 && !c.epi.kind,
+             "a GEMM with 2 GiB or more of output or A runs in row chunks: no batch, fused epilogue or fp4 output");
+    const int64_t chunk = std::min((lim - 1) / orow, (lim - 1) / arow) / 256 * 256;
+    AA_CHECK(chunk >= 256, "rows of out or A too long for 32-bit offsets");
+    const int64_t kb = c.fam == kA16W16 ? 0 : (c.fam == kA4W4 ? cols_2d(c.A) * 2 : cols_2d(c.A)) / 32;
+    for (int64_t m0 = 0; m0 < M; m0 += chunk) {
+        const int64_t rows = std::min(chunk, M - m0);
+        aiter_tensor_t a = row_slice(c.A, m0, rows, "A"), o = row_slice(c.out, m0, rows, "out"), as{}, bias{};
+        GemmCall cc = c;
+        cc.A = &a;
+        cc.out = &o;
+        if (c.As) {
+            as = *c.As;
+            as.ptr = static_cast<uint8_t*>(c.As->ptr) + m0 * kb;
+            as.ndim = 1;
+            as.shape[0] = (int64_t)c.As->numel - m0 * kb;
+            as.strides[0] = 1;
+            as.numel = (size_t)as.shape[0];
+            cc.As = &as;
+        }
+        if (c.bias && rows_2d(c.bias) > 1) {
+            bias = row_slice(c.bias, m0, rows, "bias");
+            cc.bias = &bias;
+        }
+        run_gemm(cc, stream);
+    }
+    return true;
+}
+
 void run_gemm(const GemmCall& c, hipStream_t stream) {
     check_tensor(c.A, "A", 2);
     check_tensor(c.B, "B", 2);
     check_tensor(c.out, "out", 2);
+    if (run_gemm_chunked(c, stream)) return;
     const bool scaled = c.fam != kA16W16;
     const int64_t M = rows_2d(c.A), N = rows_2d(c.B);
     int64_t K;
@@ -481,6 +542,7 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     const int req_splits = c.split_count > 0 ? c.split_count : (c.log2_split >= 0 ? 1 << std::min(c.log2_split, 16) : 0);
     if (inst->skinny && inst->split && req_splits > 0) splits = req_splits;
     if (inst->skinny) AA_CHECK(M <= inst->bm, "skinny kernel ", inst->name, " covers M <= ", inst->bm);
+    AA_CHECK(!c.capture || (inst->skinny && !inst->split && !batched), "planned calls take non-split skinny kernels");
 
     if (!inst->skinny) {
         p.tiles_m = (int)((M + inst->bm - 1) / inst->bm);
@@ -569,6 +631,10 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
             twin->fn(p, dim3(grid.x, 1, c.batch), stream);
         } else {
             p.k_steps_per_split = kpairs;
+            if (c.capture) {
+                *c.capture = p;
+                return;
+            }
             inst->fn(p, dim3(grid.x, 1, c.batch), stream);
         }
     }
@@ -686,7 +752,7 @@ aiter_tensor_t fused_scales(const aiter_tensor_t* sc, bool shuffled, int64_t R, 
 // (the Triton preshuffled ops' convention), otherwise both are plain
 void fused_a4w4(const aiter_tensor_t* x, const aiter_tensor_t* w, const aiter_tensor_t* xs, const aiter_tensor_t* ws,
                 bool preshuffled, const aiter_tensor_t* out, const aiter_tensor_t* bias, const EpiOp& epi,
-                const char* kernel_name, hipStream_t st) {
+                const char* kernel_name, hipStream_t st, GemmParams* capture = nullptr) {
     check_tensor(x, "x", 2);
     check_tensor(w, "w", 2);
     const int64_t M = rows_2d(x), K = cols_2d(x) * 2;
@@ -708,6 +774,7 @@ void fused_a4w4(const aiter_tensor_t* x, const aiter_tensor_t* w, const aiter_te
     const aiter_tensor_t wsv = fused_scales(ws, preshuffled, N, K, dev, st, 4, "w_scale");
     GemmCall c{kA4W4, {false, preshuffled, false}, x, &wv, &xsv, &wsv, out, bias, 1.0f, 1.0f, kernel_name, -1, -1};
     c.epi = epi;
+    c.capture = capture;
     run_gemm(c, st);
 }
 
@@ -1179,7 +1246,10 @@ int fused_gemm_afp4wfp4_split_cat(aiter_tensor_t* x, aiter_tensor_t* w, aiter_te
 
 // fused_gemm_afp4wfp4_a16w16 (aiter/ops/triton/gemm/fused/fused_gemm_afp4wfp4_a16w16.py:23-254):
 // y_fp4 = x_fp4 w_fp4^T (+ bias_fp4) and y_bf16 = x_bf16 w_bf16^T (+ bias_bf16)
-// over the same M and K, bf16 out; biases f32 [N]; two launches on `stream`.
+// over the same M and K, bf16 out; biases f32 [N].  M <= 64 with no kernel
+// named: both GEMMs in one grid over both GEMMs' column blocks
+// (skinny_pair_kernel, as the reference's one Triton grid of
+// cdiv(N_fp4) + cdiv(N_bf16) tiles, :145-155); otherwise two launches.
 int fused_gemm_afp4wfp4_a16w16(aiter_tensor_t* x_fp4, aiter_tensor_t* w_fp4, aiter_tensor_t* x_fp4_scale,
                                aiter_tensor_t* w_fp4_scale, aiter_tensor_t* bias_fp4, aiter_tensor_t* y_fp4,
                                const char* kernel_fp4, aiter_tensor_t* x_bf16, aiter_tensor_t* w_bf16,
@@ -1193,6 +1263,32 @@ int fused_gemm_afp4wfp4_a16w16(aiter_tensor_t* x_fp4, aiter_tensor_t* w_fp4, ait
         AA_CHECK(rows_2d(x_fp4) == rows_2d(x_bf16), "x_fp4 and x_bf16 must have the same M");
         AA_CHECK(cols_2d(x_fp4) * 2 == cols_2d(x_bf16), "x_fp4 and x_bf16 must have the same K");
         hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        const int64_t M = rows_2d(x_fp4);
+        const bool named = (kernel_fp4 && kernel_fp4[0]) || (kernel_bf16 && kernel_bf16[0]);
+        if (M > 0 && M <= 64 && !named) {
+            const int mf = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+            const std::string n4 = "a4w4_skinny_m" + std::to_string(16 * mf) + (preshuffled ? "" : "_bplain");
+            const std::string n16 = "a16w16_skinny_m" + std::to_string(16 * mf) + "_bplain";
+            GemmParams pa{}, pb{};
+            fused_a4w4(x_fp4, w_fp4, x_fp4_scale, w_fp4_scale, preshuffled != 0, y_fp4, bias_fp4, EpiOp{},
+                       n4.c_str(), st, &pa);
+            GemmCall c{kA16W16, {false, false, false}, x_bf16, w_bf16, nullptr, nullptr, y_bf16, bias_bf16,
+                       1.0f, 1.0f, n16.c_str(), -1, -1};
+            c.capture = &pb;
+            run_gemm(c, st);
+            const int nblk_a = (pa.N + 15) / 16, nblk_b = (pb.N + 15) / 16;
+            if (nblk_a + nblk_b == 0) return;
+            const dim3 grid((unsigned)(nblk_a + nblk_b));
+#define AA_PAIR(MF)                                                                               \
+    (preshuffled ? skinny_pair_kernel<MF, true><<<grid, 512, 0, st>>>(pa, pb, nblk_a)             \
+                 : skinny_pair_kernel<MF, false><<<grid, 512, 0, st>>>(pa, pb, nblk_a))
+            if (mf == 1) AA_PAIR(1);
+            else if (mf == 2) AA_PAIR(2);
+            else AA_PAIR(4);
+#undef AA_PAIR
+            AA_HIP(hipGetLastError());
+            return;
+        }
         fused_a4w4(x_fp4, w_fp4, x_fp4_scale, w_fp4_scale, preshuffled != 0, y_fp4, bias_fp4, EpiOp{}, kernel_fp4, st);
         GemmCall c{kA16W16, {false, false, false}, x_bf16, w_bf16, nullptr, nullptr, y_bf16, bias_bf16,
                    1.0f, 1.0f, kernel_bf16, -1, -1};

@@ -506,10 +506,11 @@ AA_DEV void skinny_mma(const SkinnyPair<KA, MF, NB>& d, f32x4_t (*acc)[NB]) {
 
 // NB column blocks of 16 per workgroup share each A fragment (NB = 2: the
 // two halves of one 32-row B scale group, so one scale dword serves both)
-template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB = 1, bool NT = false>
-__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
+// The skinny GEMM of one workgroup: column blocks bx * NB .. +NB, K split
+// `by` (the __global__ below; also one half of the fused pair kernel)
+template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB, bool NT>
+AA_DEV void skinny_body(const GemmParams& p, int bx, int by) {
     static_assert(NB == 1 || NB == 2, "one or two column blocks per workgroup");
-    apply_batch(p);
     constexpr bool SCALED = OpTraits<KA>::scaled;
     constexpr int KPAIR = SCALED ? 256 : 64;               // elements per k-pair
     constexpr int SGRP = (MF + 1) / 2;                     // 32-row A scale groups
@@ -517,9 +518,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * 16 * NB;
+    const int n0 = bx * 16 * NB;
     const int total_pairs = p.K / KPAIR;
-    const int p_begin = blockIdx.y * p.k_steps_per_split;   // k_steps_per_split counts pairs here
+    const int p_begin = by * p.k_steps_per_split;   // k_steps_per_split counts pairs here
     const int p_end = min(total_pairs, p_begin + p.k_steps_per_split);
 
     const uint8_t* bsrc[NB];
@@ -606,6 +607,98 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
             store_frag<OUT_F32>(p, s, m, n);
         }
     }
+}
+
+template <int KA, int MF, int NW, bool B_PRE, bool SPLIT, bool OUT_F32, int NB = 1, bool NT = false>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_kernel(GemmParams p) {
+    apply_batch(p);
+    skinny_body<KA, MF, NW, B_PRE, SPLIT, OUT_F32, NB, NT>(p, blockIdx.x, blockIdx.y);
+}
+
+// Two skinny GEMMs of the same M in one grid (fused_gemm_afp4wfp4_a16w16 at
+// decode sizes): workgroups [0, nblk_a) compute the MXFP4 GEMM `pa`, the rest
+// the bf16 GEMM `pb`, one pass over K each (16-column blocks, 8 waves).
+template <int MF, bool BPRE_A>
+__global__ __launch_bounds__(512) void skinny_pair_kernel(GemmParams pa, GemmParams pb, int nblk_a) {
+    if ((int)blockIdx.x < nblk_a)
+        skinny_body<kFp4, MF, 8, BPRE_A, false, false, 1, false>(pa, blockIdx.x, 0);
+    else
+        skinny_body<kBf16, MF, 8, false, false, false, 1, false>(pb, blockIdx.x - nblk_a, 0);
+}
+
+// Skinny (decode) GEMM for short K: every wave owns 16*NB output columns and
+// the whole K range, at most KP k-pairs.  All of a wave's loads (B, A and
+// both scale tensors, KP register sets) are issued before its first MFMA and
+// the wave stores its own columns: no split-K, no reduction through LDS, no
+// barrier, one launch.  With K = 2048 (8 k-pairs) a wave keeps 8 x 2 KiB of
+// B in flight, so the 448 waves of N = 7168 hold the whole weight in flight
+// at once.  NWC independent waves per workgroup (consecutive column blocks).
+template <int KA, int MF, int NB, int KP, bool B_PRE, bool OUT_F32, bool NT, int NWC>
+__global__ __launch_bounds__(64 * NWC) void gemm_skinny_direct_kernel(GemmParams p) {
+    static_assert(NB == 1 || NB == 2, "one or two column blocks per wave");
+    apply_batch(p);
+    constexpr bool SCALED = OpTraits<KA>::scaled;
+    constexpr int KPAIR = SCALED ? 256 : 64;
+    constexpr int SGRP = (MF + 1) / 2;
+    constexpr int SBN = (NB + 1) / 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int n0 = (blockIdx.x * NWC + wave) * 16 * NB;
+    if (n0 >= p.N) return;
+    const int npairs = p.K / KPAIR;   // <= KP (checked on the host)
+
+    const uint8_t* bsrc[NB];
+#pragma unroll
+    for (int j = 0; j < NB; ++j) {
+        const int nb0 = min(n0 + 16 * j, (p.N - 1) / 16 * 16);
+        if constexpr (B_PRE)
+            bsrc[j] = p.B + (int64_t)nb0 * p.ldb + lane * 16;
+        else
+            bsrc[j] = p.B + (int64_t)min(nb0 + (lane & 15), p.N - 1) * p.ldb + (lane >> 4) * 16;
+    }
+    const uint8_t* asrc[MF];
+    bool arow_ok[MF];
+#pragma unroll
+    for (int i = 0; i < MF; ++i) {
+        const int row = i * 16 + (lane & 15);
+        arow_ok[i] = row < p.M;
+        asrc[i] = p.A + (int64_t)min(row, p.M - 1) * p.lda + (lane >> 4) * 16;
+    }
+    const uint8_t* sbp[SBN];
+    const uint8_t* sap[SGRP];
+    if constexpr (SCALED) {
+#pragma unroll
+        for (int g = 0; g < SBN; ++g) {
+            const int nb0 = min(n0 + 32 * g, (p.N - 1) / 16 * 16);
+            sbp[g] = p.Bs + (int64_t)(nb0 / 32) * 32 * p.sb_stride + lane * 4;
+        }
+#pragma unroll
+        for (int g = 0; g < SGRP; ++g)
+            sap[g] = p.As + (int64_t)min(g, p.sa_groups - 1) * 32 * p.sa_stride + lane * 4;
+    }
+
+    SkinnyPair<KA, MF, NB> st[KP];
+#pragma unroll
+    for (int u = 0; u < KP; ++u)
+        if (u < npairs) skinny_load<KA, MF, NB, B_PRE, NT>(st[u], u, bsrc, asrc, arow_ok, sbp, sap);
+
+    f32x4_t acc[MF][NB];
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto run = [&](auto bh) {
+        constexpr int BH = decltype(bh)::value;
+#pragma unroll
+        for (int u = 0; u < KP; ++u)
+            if (u < npairs) skinny_mma<KA, MF, NB, BH>(st[u], acc);
+    };
+    if (NB == 1 && ((n0 / 16) & 1)) run(std::integral_constant<int, 1>{});
+    else run(std::integral_constant<int, 0>{});
+#pragma unroll
+    for (int i = 0; i < MF; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) store_frag<OUT_F32>(p, acc[i][j], i * 16 + (lane & 15), n0 + 16 * j + 4 * (lane >> 4));
 }
 
 // f32 workspace -> output (+alpha, +bias) for the split-K skinny path.

@@ -5,7 +5,7 @@
 // Every kernel instance has a stable name and integer id (the `kernelName` /
 // `kernelId` the tuned CSVs refer to); ids are assigned in registration
 // order, which the parts keep: part_mx, part_bf16<false>, part_bf16<true>,
-// part_persist_split, part_rest.
+// part_persist_split, part_rest, part_direct.
 #pragma once
 
 #include <string>
@@ -106,6 +106,20 @@ void launch_skinny_alds(const GemmParams& p, dim3 grid, hipStream_t s) {
         gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, false><<<grid, 64 * NW, 0, s>>>(p);
 }
 
+// the short-K direct skinny kernel: KP k-pairs at most (K <= KP * 256 for
+// the MX families), NWC waves of one column block each per workgroup; the
+// launcher's grid counts column blocks
+template <int KA, int MF, int NB, int KP, bool BP = true, bool OF = false, int NWC = 4>
+void launch_skinny_direct(const GemmParams& p, dim3 grid, hipStream_t s) {
+    constexpr int KPAIR = OpTraits<KA>::scaled ? 256 : 64;
+    AA_CHECK(p.K / KPAIR <= KP, "direct skinny kernel: K = ", p.K, " is longer than its ", KP, " k-pairs");
+    const dim3 g((grid.x + NWC - 1) / NWC, 1, grid.z);
+    if (b_streams<KA>(p))
+        gemm_skinny_direct_kernel<KA, MF, NB, KP, BP, OF, true, NWC><<<g, 64 * NWC, 0, s>>>(p);
+    else
+        gemm_skinny_direct_kernel<KA, MF, NB, KP, BP, OF, false, NWC><<<g, 64 * NWC, 0, s>>>(p);
+}
+
 // Registration in id order (see the file comment).
 struct RegBuilder {
     std::vector<Instance>& reg;
@@ -153,6 +167,7 @@ struct RegBuilder {
     template <bool OF> void part_bf16();   // gemm_reg_bf16.hip (OF = false), gemm_reg_bf16_f32.hip (true)
     void part_persist_split();         // gemm_reg_split.hip
     void part_rest();                  // gemm_reg_rest.hip
+    void part_direct();                // gemm_reg_direct.hip
 };
 
 constexpr Variant kPre{false, true, false}, kPlain{false, false, false}, kPre32{false, true, true};

@@ -158,9 +158,13 @@ def fused_gemm_afp4wfp4_a16w16(x_fp4: Tensor, w_fp4: Tensor, x_fp4_scale: Tensor
     b16 = None if bias_bf16 is None else bias_bf16.float().contiguous()
     from .tuned_gemm import get_GEMM_A16W16_config
 
-    cfg = get_GEMM_A16W16_config(m, n_bf16, k, bias_bf16 is not None, str(dtypes.bf16), str(dtypes.bf16))
-    k16 = str(cfg.get("kernelName") or "") if cfg and cfg.get("libtype") == "aiter_amd" else ""
+    k4 = k16 = None
+    if m > 64:
+        # up to 64 rows the library runs both GEMMs in one grid (no kernel
+        # names); above, each GEMM takes its tuned kernel, two launches
+        cfg = get_GEMM_A16W16_config(m, n_bf16, k, bias_bf16 is not None, str(dtypes.bf16), str(dtypes.bf16))
+        k16 = str(cfg.get("kernelName") or "") if cfg and cfg.get("libtype") == "aiter_amd" else ""
+        k4 = _tuned_a4w4(m, n_fp4, k, is_fp4_preshuffled)
     call("fused_gemm_afp4wfp4_a16w16", _u8(x_fp4), _u8(w_fp4), _u8(x_fp4_scale), _u8(w_fp4_scale), b4, y_fp4,
-         _tuned_a4w4(m, n_fp4, k, is_fp4_preshuffled), x_bf16, w_bf16, b16, y_bf16, k16 or None,
-         int(bool(is_fp4_preshuffled)))
+         k4, x_bf16, w_bf16, b16, y_bf16, k16 or None, int(bool(is_fp4_preshuffled)))
     return y_fp4, y_bf16

@@ -115,6 +115,13 @@ def _ref_rows(M: int, dev) -> torch.Tensor | None:
     return torch.randperm(M, generator=g)[:REF_ROWS].sort().values.to(dev)
 
 
+def _rows_u8(t: torch.Tensor, rows: torch.Tensor | None) -> torch.Tensor:
+    """The rows `rows` (all when None) of a byte-typed tensor (e2m1 pairs,
+    e4m3, e8m0) as uint8: torch indexes none of those dtypes on the GPU."""
+    t = t.view(torch.uint8)
+    return t if rows is None else t[rows]
+
+
 def iters_for(flop: float, nbytes: float, cap: int) -> int:
     """Calls per timed graph replay: about 2 ms of work (at 4 PFLOP/s or
     5 TB/s, whichever is slower), between 2 and `cap`."""
@@ -201,12 +208,12 @@ def tune_mx(family: str, M: int, N: int, K: int, iters: int, max_err_ratio: floa
     if family == "a4w4":
         aq, as_plain = dynamic_mxfp4_quant(a, shuffle=False)
         _, as_ = dynamic_mxfp4_quant(a, shuffle=True)
-        deq_a = _dequant_fp4(aq if rows is None else aq[rows], as_plain if rows is None else as_plain[rows])
+        deq_a = _dequant_fp4(_rows_u8(aq, rows), _rows_u8(as_plain, rows))
         a_bytes = M * K // 2
     else:
         aq, as_plain = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=False)
         _, as_ = dynamic_mxfp8_quant(a.to(dtypes.bf16), shuffle=True)
-        deq_a = _dequant_fp8(aq if rows is None else aq[rows], as_plain if rows is None else as_plain[rows])
+        deq_a = _dequant_fp8(_rows_u8(aq, rows), _rows_u8(as_plain, rows))
         a_bytes = M * K
     del a, b
     prev_tf32 = torch.backends.cuda.matmul.allow_tf32
@@ -577,13 +584,18 @@ def main(argv=None):
         if not torch.cuda.is_available():
             print("the tuner needs a GPU", file=sys.stderr)
             return 2
+        # a shape that raises (no kernel passes, too large) costs only itself
+        rc = 0
         for spec in args.worker.split(";"):
-            rc = worker(args.family, _parse_shape(args.family, spec), args.tune_file, args.iters,
-                        args.errRatio, args.compare, args.min_improvement_pct)
+            try:
+                rc |= worker(args.family, _parse_shape(args.family, spec), args.tune_file, args.iters,
+                             args.errRatio, args.compare, args.min_improvement_pct)
+            except RuntimeError as e:
+                print(f"{spec}: {e}", file=sys.stderr, flush=True)
+                _log(f"  FAILED {spec}: {e}")
+                rc = 1
             torch.cuda.empty_cache()
-            if rc:
-                return rc
-        return 0
+        return rc
     min_pct = args.min_improvement_pct if (args.compare and args.update_improved) else -1e30
     if args.untune_file:
         shapes = _read_untuned(args.untune_file, args.family)

@@ -418,8 +418,41 @@ def bench_extra(dev):
                    "TFLOPs": round(flop / t / 1e12, 1), "GBps": round(2 * 16 * (mb * 4096 + 1024 * 4096 + mb * 1024) / t / 1e9, 1),
                    "loop_us": round(tl * 1e6, 1)})
     out["batched_bf16"] = bt
+    out["fused_gemm_afp4wfp4_a16w16"] = bench_fused_a16w16(dev)
     out["fused_moe_a4w4_deepseek"] = bench_moe(dev)
     return out
+
+
+def bench_fused_a16w16(dev, ms=(1, 16, 64), n4=4096, n16=256, k=7168):
+    """fused_gemm_afp4wfp4_a16w16 (an MXFP4 gate-up projection and the bf16
+    router of one layer over the same activations; DeepSeek-like N = 4096 and
+    256 experts, K = 7168): one grid over both GEMMs' column blocks at decode
+    sizes, against the two GEMMs called one after the other."""
+    import aiter_amd
+
+    g = torch.Generator(device="cpu").manual_seed(12)
+    res = []
+    for m in ms:
+        a = torch.randn((m, k), generator=g).to(dev)
+        w = torch.randn((n4, k), generator=g).to(dev)
+        wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+        wq = aiter_amd.shuffle_weight(wq)
+        aq, as_sh = aiter_amd.dynamic_mxfp4_quant(a, shuffle=True)
+        _, as_pl = aiter_amd.dynamic_mxfp4_quant(a, shuffle=False)
+        xb = a.to(torch.bfloat16)
+        wb = torch.randn((n16, k), generator=g).to(torch.bfloat16).to(dev)
+        # the preshuffled op's layouts: w [N/16, K*8], scales [rows/32, K], x scales plain below 32 rows
+        w_t = wq.view(torch.uint8).view(n4 // 16, k * 8)
+        ws_t = ws.view(torch.uint8).view(-1, k)
+        xs_t = as_sh.view(torch.uint8).view(-1, k) if m >= 32 else as_pl
+        fused = lambda: aiter_amd.fused_gemm_afp4wfp4_a16w16(aq, w_t, xs_t, ws_t, xb, wb, is_fp4_preshuffled=True)
+        apart = lambda: (aiter_amd.gemm_a4w4(aq, wq, as_sh, ws), aiter_amd.gemm_a16w16(xb, wb))
+        t = time_graph(fused, 20, 2)
+        t2 = time_graph(apart, 20, 2)
+        res.append({"M": m, "N_fp4": n4, "N_bf16": n16, "K": k, "us": round(t * 1e6, 2),
+                    "two_calls_us": round(t2 * 1e6, 2)})
+        log(f"fused_gemm_afp4wfp4_a16w16 {res[-1]}")
+    return res
 
 
 def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
@@ -452,15 +485,68 @@ def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
         fn = lambda: aiter_amd.fused_moe(x, w1, w2, tw, ti, quant_type=aiter_amd.QuantType.per_1x32, w1_scale=w1s,
                                          w2_scale=w2s)
         t = time_graph(fn, 10, 2)
+        stages = _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter)
         touched = int(torch.unique(ti).numel())
         nbytes = touched * per_expert + m * dim * 2 * 2
         flop = 2 * m * topk * (2 * inter * dim + dim * inter)
         out.append({"tokens": m, "us": round(t * 1e6, 1), "TFLOPs": round(flop / t / 1e12, 1),
                     "frac_mxfp4_peak": round(flop / t / 1e12 / PEAK_MXFP4, 4), "experts_touched": touched,
                     "GBps": round(nbytes / t / 1e9, 1), "frac_hbm": round(nbytes / t / 1e9 / PEAK_HBM, 4),
-                    "block_m": aiter_amd.get_block_size_M(m, topk, E, inter)})
+                    "block_m": aiter_amd.get_block_size_M(m, topk, E, inter), **stages})
         log(f"fused_moe tokens={m}: {out[-1]}")
     return out
+
+
+# the reference's tuned stage times (us1, us2) at model_dim 7168, inter_dim 256,
+# 257 experts, topk 9: aiter/configs/model_configs/dsv3_fp4_tuned_fmoe.csv:2,6,9,12,14
+REF_MOE_STAGES = {1: (11.3537, 7.5406), 16: (40.5338, 24.9519), 128: (87.5346, 54.4124),
+                  1024: (106.2571, 107.529), 4096: (191.9986, 283.9092)}
+
+
+def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter):
+    """Each launch group of fused_moe timed on its own (graph-replayed, inputs
+    from an eager run of the steps before it): the routing sort, the two
+    sorted activation quants, stage 1 (with its split-K reduce) and stage 2
+    (with moe_sum when the per-pair rows are reduced by slot), for a like-for-
+    like comparison with the reference's tuned us1 / us2 (stage kernels
+    only)."""
+    from aiter_amd import dtypes
+    from aiter_amd import fused_moe as FM
+
+    m = x.shape[0]
+    bm = FM.get_block_size_M(m, topk, E, inter)
+    reduce = FM._use_reduce(m, topk)
+    qt = int(aiter_amd.QuantType.per_1x32)
+    sort = lambda: FM.moe_sorting(ti, tw, E, dim, torch.bfloat16, bm, None, None, 0, accumulate=not reduce)
+    sids, sw, seids, nv, moe_buf = sort()
+    q1 = lambda: FM.fused_dynamic_mx_quant_moe_sort(x, sids, nv, m, topk, bm, dtypes.fp4x2, sorted_weights=sw)
+    a1, a1s = q1()
+    a2 = torch.empty((m, topk, inter), dtype=torch.bfloat16, device=x.device)
+    s1 = lambda: FM.ck_moe_stage1(a1, w1, w2, sids, seids, nv, a2, topk, "", w1s, a1s, bm, None, qt,
+                                  int(FM.ActivationType.Silu), splitk=0)
+    s1()
+    q2 = lambda: FM.fused_dynamic_mx_quant_moe_sort(a2.view(-1, inter), sids, nv, m, topk, bm, dtypes.fp4x2,
+                                                    sorted_weights=sw)
+    a2q, a2s = q2()
+    res = {"sort_us": time_graph(sort, 10, 2), "quant1_us": time_graph(q1, 10, 2), "stage1_us": time_graph(s1, 10, 2),
+           "quant2_us": time_graph(q2, 10, 2)}
+    if reduce:
+        per_pair = torch.empty((m, topk, dim), dtype=torch.bfloat16, device=x.device)
+        s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, per_pair, topk, "", w2s, a2s, bm, sw, qt)
+        s2()
+        res["stage2_us"] = time_graph(s2, 10, 2)
+        res["moe_sum_us"] = time_graph(lambda: FM.moe_sum(per_pair, moe_buf), 10, 2)
+    else:
+        s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, moe_buf, topk, "", w2s, a2s, bm, sw, qt)
+        res["stage2_us"] = time_graph(s2, 10, 2)
+        res["moe_sum_us"] = 0.0
+    res = {k: round(v * 1e6, 1) for k, v in res.items()}
+    res["stages_us"] = round(res["stage1_us"] + res["stage2_us"] + res["moe_sum_us"], 1)
+    if m in REF_MOE_STAGES:
+        r1, r2 = REF_MOE_STAGES[m]
+        res["ref_stage1_us"], res["ref_stage2_us"] = r1, r2
+        res["stages_vs_ref"] = round((r1 + r2) / res["stages_us"], 3)
+    return res
 
 
 def bf16_plumbing(dev):

@@ -352,6 +352,15 @@ int aiter_amd_workspace_release(int device, aiter_stream_t stream);
  * compared against; sink (one int32) only keeps the reads live. */
 int hbm_stream_read(aiter_tensor_t* src, aiter_tensor_t* sink, int grid, aiter_stream_t stream);
 
+/* The same calibration read with its launch shape and cache policy chosen:
+ * `unroll` 16-byte loads per thread in flight (1, 2, 4, 8), `block` threads
+ * per workgroup (64..1024, powers of two), `policy` the buffer-load cache
+ * bits (0, 1 sc0, 2 nt, 3, 16 sc1, 17, 18, 19) or -1 for the plain
+ * nontemporal load of hbm_stream_read; -2 (block 256) launches the same grid
+ * of empty workgroups: the launch floor.  No counterpart in the reference. */
+int hbm_stream_read_cfg(aiter_tensor_t* src, aiter_tensor_t* sink, int grid, int block, int unroll, int policy,
+                        aiter_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -209,11 +209,14 @@ def test_fused_split_cat_epilogue_paths(cuda, monkeypatch, tmp_path, path, m, n,
 
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("preshuffled", [True, False])
-@pytest.mark.parametrize("m", [1, 16, 64, 300])
-def test_fused_gemm_afp4wfp4_a16w16(cuda, m, preshuffled, bias):
+@pytest.mark.parametrize("m,n4,n16", [(1, 1024, 256), (16, 1024, 256), (33, 1040, 272), (64, 1024, 256),
+                                      (300, 1024, 256)])
+def test_fused_gemm_afp4wfp4_a16w16(cuda, m, n4, n16, preshuffled, bias):
+    """M <= 64: both GEMMs in one grid (skinny_pair_kernel; ragged column
+    block counts at M = 33); M = 300: two launches."""
     import aiter_amd
 
-    n4, n16, k = 1024, 256, 512
+    k = 512
     announce(f"fused a16w16 m={m} pre={preshuffled} bias={bias}")
     a_q, a_s, a_ss, b_q, b_s, b_ss, c = _case(m, n4, k, 21 + m)
     x, w, xs, ws = _operands(cuda, preshuffled, m, n4, k, a_q, a_s, a_ss, b_q, b_s, b_ss)

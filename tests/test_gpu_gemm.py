@@ -401,10 +401,12 @@ def test_bf16_skinny_instances_k_pairs(cuda, k):
             assert ok, f"{name}: {msg}"
 
 
-@pytest.mark.parametrize("k", [256, 768, 2304, 8448])
+@pytest.mark.parametrize("k", [256, 768, 2048, 2304, 4096, 8448])
 def test_mx_skinny_instances_k_pairs(cuda, k):
     """Every A4W4 and A8W4 skinny instance (preshuffled B) with K/256 = 1, 3,
-    9, 33 k-pairs over its 8 waves, N = 272 (17 column blocks)."""
+    8, 9, 16, 33 k-pairs over its waves, N = 272 (17 column blocks).  The
+    direct instances (``_direct_kP``) hold at most P k-pairs: longer K is
+    refused on the host."""
     import aiter_amd
     from aiter_amd._lib import call
 
@@ -415,6 +417,26 @@ def test_mx_skinny_instances_k_pairs(cuda, k):
             if split:
                 continue   # the split forms: test_gpu_splitk_tiles and the every-instance sweep
             m = max(1, bm - 3)
+            kp = int(name.rsplit("_k", 1)[1]) if "_direct_k" in name else None
+            if kp is not None and k // 256 > kp:
+                announce(f"{fam} skinny {name} {m}x{n}x{k}: refused")
+                with pytest.raises(RuntimeError, match="longer than"):
+                    if fam == "a4w4":
+                        out = torch.empty(((m + 31) // 32 * 32, n), dtype=torch.bfloat16, device=cuda)
+                        a_long = torch.zeros((m, k // 2), dtype=torch.uint8, device=cuda)
+                        b_long = torch.zeros((n, k // 2), dtype=torch.uint8, device=cuda)
+                        s_a = torch.zeros(((m + 255) // 256 * 256, k // 32), dtype=torch.uint8, device=cuda)
+                        s_b = torch.zeros(((n + 255) // 256 * 256, k // 32), dtype=torch.uint8, device=cuda)
+                        aiter_amd.gemm_a4w4_asm(a_long, b_long, s_a, s_b, out, kernelName=name)
+                    else:
+                        out = torch.empty((m, n), dtype=torch.bfloat16, device=cuda)
+                        call("mxfp8_mxfp4_gemm_asm",
+                             torch.zeros((m, k), dtype=torch.uint8, device=cuda).view(torch.float8_e4m3fn),
+                             torch.zeros((n, k // 2), dtype=torch.uint8, device=cuda),
+                             torch.zeros(((m + 255) // 256 * 256, k // 32), dtype=torch.uint8, device=cuda),
+                             torch.zeros(((n + 255) // 256 * 256, k // 32), dtype=torch.uint8, device=cuda),
+                             out, name, 0)
+                continue
             announce(f"{fam} skinny {name} {m}x{n}x{k}")
             if fam == "a4w4":
                 a_q, a_ss, b_q, b_ss, ref = _a4w4_case(m, n, k, seed=51)
@@ -461,6 +483,8 @@ def test_streamed_weight_instances(cuda):
         name, split = row[1], row[6]
         if split:
             continue
+        if "_direct_k" in name and k // 256 > int(name.rsplit("_k", 1)[1]):
+            continue   # K beyond the direct instance's k-pairs (refused: test_mx_skinny_instances_k_pairs)
         announce(f"a4w4 streamed-weight {name} {m}x{n}x{k}")
         out = torch.empty((32, n), dtype=torch.bfloat16, device=cuda)
         aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), bq, _dev(a_ss, cuda), _dev(b_ss, cuda), out, kernelName=name)
@@ -520,3 +544,51 @@ def test_hbm_stream_read_calibration(cuda):
     assert int(sink.item()) == 0
     with pytest.raises(RuntimeError, match="contiguous"):
         call("hbm_stream_read", buf[::2], sink, 64)
+
+
+def test_outputs_of_2gib_and_more_run_in_row_chunks(cuda):
+    """An output of 2 GiB or more (the reference's M = 16384, N = 106496 rows)
+    runs as row chunks (the kernels address out through 32-bit offsets):
+    A4W4 with bf16 out [16640, 65536] (2.03 GiB, chunks of 16128 rows) and bf16
+    with f32 out [8448, 65536] (2.06 GiB, chunks of 7936 rows); rows on both sides of the chunk
+    boundary, written into NaN-filled outputs, against the oracle."""
+    import aiter_amd
+
+    m, n, k = 16640, 65536, 256
+    announce(f"a4w4 {m}x{n}x{k}: 2 GiB output in row chunks")
+    g = torch.Generator(device="cpu").manual_seed(31)
+    x = torch.randn((m, k), generator=g).to(cuda)
+    w = torch.randn((n, k), generator=g).to(cuda)
+    xq, xs = aiter_amd.dynamic_mxfp4_quant(x, shuffle=True)
+    wq, ws = aiter_amd.dynamic_mxfp4_quant(w, shuffle=True)
+    out = torch.full(((m + 31) // 32 * 32, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.gemm_a4w4_asm(xq, aiter_amd.shuffle_weight(wq), xs, ws, out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out[:m]).all()), "output rows left unwritten"
+    rows = np.array([0, 5, 16127, 16128, 16129, m - 1])
+    cols = np.sort(np.random.default_rng(3).choice(n, 64, replace=False))
+    a_q = xq.view(torch.uint8)[torch.from_numpy(rows).to(cuda)].cpu().numpy()
+    b_q = wq.view(torch.uint8)[torch.from_numpy(cols).to(cuda)].cpu().numpy()
+    a_s = O.unshuffle_scale(xs.view(torch.uint8).cpu().numpy(), m, k // 32)[rows]
+    b_s = O.unshuffle_scale(ws.view(torch.uint8).cpu().numpy(), n, k // 32)[cols]
+    ref = O.bf16_bits_to_f32(O.gemm_a4w4_ref(a_q, b_q, a_s, b_s))
+    got = out[torch.from_numpy(rows).to(cuda)][:, torch.from_numpy(cols).to(cuda)].float().cpu().numpy()
+    ok, msg = allclose_report(got, ref)
+    assert ok, msg
+    del out, xq, xs, wq, ws, x, w
+
+    m, n, k = 8448, 65536, 128
+    announce(f"bf16 {m}x{n}x{k} f32 out: 2 GiB output in row chunks")
+    xb = torch.randn((m, k), generator=g).to(torch.bfloat16).to(cuda)
+    wb = torch.randn((n, k), generator=g).to(torch.bfloat16).to(cuda)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=cuda)
+    aiter_amd.gemm_a16w16_asm(xb, wb, out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "output rows left unwritten"
+    rows = np.array([0, 7935, 7936, m - 1])
+    a_bits = xb[torch.from_numpy(rows).to(cuda)].view(torch.int16).cpu().numpy().view(np.uint16)
+    b_bits = wb[torch.from_numpy(cols).to(cuda)].view(torch.int16).cpu().numpy().view(np.uint16)
+    ref = O.bf16_bits_to_f32(a_bits) @ O.bf16_bits_to_f32(b_bits).T
+    got = out[torch.from_numpy(rows).to(cuda)][:, torch.from_numpy(cols).to(cuda)].cpu().numpy()
+    ok, msg = allclose_report(got, ref)
+    assert ok, msg

@@ -18,9 +18,12 @@ Kernels modelled: gemm_flat.h ``flat_body`` (prologue and main loop; both
 its issue orders: B operand loads spread over the k-steps, and the BLDS order
 of row-major bf16 B, A copies before the wait and B copies after it),
 gemm_t32.h ``gemm_t32_kernel``, gemm_flat_persist.h (prologue, tile
-transitions).  A wrong count here (the flat kernel's former prologue wait of
-(NS - 2) * NDMA) lets the first stage read a slot whose copies may still be
-in flight: a timing-dependent wrong tile.
+transitions), gemm_skinny_lds.h (S pairs in flight, its up-front, steady and
+tail phases, buffer refills), gemm_lds_persist.h (two stage buffers, the
+epilogue's use of a stage buffer, tile transitions), and moe_stage2.h (no
+ring: its wave-private epilogue tile).  A wrong count here (the flat
+kernel's former prologue wait of (NS - 2) * NDMA) lets the first stage read a
+slot whose copies may still be in flight: a timing-dependent wrong tile.
 """
 import pytest
 
@@ -260,3 +263,206 @@ def test_flat_blds_model_catches_a_loose_wait():
 
     ns, ndma = _blds_ring(256)
     assert run_flat_blds(ns, ndma, 8, waits=loose) != []
+
+
+# --------------------------------------------------------------------------
+# gemm_skinny_lds.h: S k-pairs in flight per wave, each pair's A copies (and
+# row-major B copies or B register loads, and scale loads: LP vector-memory
+# operations) in register set / LDS buffer `pair % S`; the wait before a
+# pair's MFMAs is vmcnt(after * LP) with `after` = pairs issued after it.
+# The model follows the kernel's three phases (all pairs up front when there
+# are fewer than S; the steady loop; the tail of R remaining issues) and
+# checks that every wait covers its pair, every pair is consumed once and in
+# order, and no buffer is refilled before its pair was consumed.
+
+def skinny_lds_lp(ka, mf, nb, bl):
+    """vector-memory operations the kernel's issue() emits per k-pair: A
+    copies (16*MF rows of ROWB bytes, 64 lanes x 16 B each), B (BL: 2*NB
+    whole-line copies of 16*NB rows x 128 B; else two 16-byte halves per
+    column block), scale dword loads (one per 32-row group of A and of B)"""
+    rowb = 256 if ka == "fp8" else 128
+    ncp = 16 * mf * rowb // 1024
+    b_ops = (16 * nb * 128 // 1024) if bl else 2 * nb
+    scales = 0 if ka == "bf16" else (mf + 1) // 2 + (nb + 1) // 2
+    return ncp + b_ops + scales
+
+
+def run_skinny_lds(s, lp, npairs):
+    w = Wave()
+    bad = []
+    held = {}
+    consumed = []
+
+    def issue(pair, buf):
+        if buf in held and held[buf] not in consumed:
+            bad.append(("refilled before use", pair, buf))
+        held[buf] = pair
+        w.issue(("P", pair), lp)
+
+    def consume(buf, after):
+        pair = held[buf]
+        w.wait(after * lp)
+        if not w.complete(("P", pair)):
+            bad.append(("wait misses", pair))
+        consumed.append(pair)
+
+    if npairs < s:
+        for u in range(npairs):
+            issue(u, u)
+        for u in range(npairs):
+            consume(u, npairs - 1 - u)
+    else:
+        for u in range(s - 1):
+            issue(u, u)
+        t = 0
+        while t + 2 * s - 2 < npairs:
+            for u in range(s):
+                issue(t + u + s - 1, (u + s - 1) % s)
+                consume(u, s - 1)
+            t += s
+        rem = npairs - t - (s - 1)
+        assert 0 <= rem < s
+        for u in range(s - 1 + rem):
+            if u < rem:
+                issue(t + u + s - 1, (u + s - 1) % s)
+                consume(u % s, s - 1)
+            else:
+                consume(u % s, s - 2 + rem - u)
+    if consumed != list(range(npairs)):
+        bad.append(("consumed", consumed))
+    return bad
+
+
+# (KA, MF, NB, S, BL) of every gemm_skinny_alds_kernel instance the registry holds
+SKINNY_LDS = [("bf16", 1, 2, 2, True), ("bf16", 2, 2, 2, True), ("bf16", 4, 2, 2, True), ("bf16", 1, 1, 2, True),
+              ("bf16", 1, 1, 3, True), ("bf16", 2, 1, 2, True), ("bf16", 2, 2, 2, False), ("bf16", 4, 2, 2, False),
+              ("fp4", 2, 2, 2, False), ("fp4", 4, 2, 2, False), ("fp4", 2, 1, 2, False), ("fp8", 2, 2, 2, False)]
+
+
+@pytest.mark.parametrize("ka,mf,nb,s,bl", SKINNY_LDS)
+@pytest.mark.parametrize("npairs", list(range(1, 12)) + [33])
+def test_skinny_lds_waits(ka, mf, nb, s, bl, npairs):
+    lp = skinny_lds_lp(ka, mf, nb, bl)
+    assert (s - 1) * lp < 64          # the kernel's static_assert: vmcnt range
+    assert run_skinny_lds(s, lp, npairs) == []
+
+
+def test_skinny_lds_model_catches_a_short_tail_wait():
+    """With the tail's last wait one pair short (after - 1), the last pair's
+    operations may still be in flight."""
+    lp = skinny_lds_lp("fp4", 2, 2, False)
+
+    def short(s, lp, npairs):
+        w = Wave()
+        for u in range(npairs):
+            w.issue(("P", u), lp)
+        w.wait(lp)           # should be 0 for the last pair
+        return [] if w.complete(("P", npairs - 1)) else ["last pair"]
+
+    assert short(2, lp, 3) == ["last pair"]
+
+
+# --------------------------------------------------------------------------
+# gemm_lds_persist.h and the wave-private buffers: a symmetric trace of one
+# wave's LDS events (all waves run the same sequence between barriers).  A
+# read of a buffer needs its copies waited for (vmcnt) before a barrier that
+# precedes the read; a copy into a buffer needs every earlier read or
+# epilogue use of that buffer to be followed by an lgkmcnt(0) wait and a
+# barrier before the copy.
+
+def check_trace(events):
+    w = Wave()
+    bad = []
+    copies = {}          # buf -> tags of copies not yet published
+    published = set()    # (buf, tag) readable
+    pending_use = {}     # buf -> index of the last read / epilogue use not yet fenced
+    waited_uses = {}     # buf -> uses completed by an lgkmcnt(0) wait, awaiting a barrier
+    for i, ev in enumerate(events):
+        kind = ev[0]
+        if kind == "dma":
+            _, buf, tag, n = ev
+            if pending_use.get(buf) is not None or waited_uses.get(buf):
+                bad.append(("copy over unfenced use", i, buf))
+            w.issue((buf, tag), n)
+            copies.setdefault(buf, []).append(tag)
+            published.discard((buf, tag))
+        elif kind == "wait":
+            _, vm, lgkm0 = ev
+            w.wait(vm)
+            if lgkm0:
+                for b, u in list(pending_use.items()):
+                    if u is not None:
+                        waited_uses[b] = True
+                        pending_use[b] = None
+        elif kind == "barrier":
+            for b, tags in copies.items():
+                for t in list(tags):
+                    if w.complete((b, t)):
+                        published.add((b, t))
+                        tags.remove(t)
+            waited_uses.clear()
+        elif kind in ("read", "ep"):
+            _, buf, tag = ev
+            if kind == "read" and (buf, tag) not in published:
+                bad.append(("read before publish", i, buf, tag))
+            pending_use[buf] = i
+    return bad
+
+
+def lds_persist_trace(nst, tiles, ndma=16):
+    """gemm_lds_persist_kernel: two stage buffers; stage t (buffer t % 2)
+    issues the copies of stage t+1 into the other buffer, reads its own
+    buffer over 4 k-steps, waits vmcnt(0) lgkmcnt(0) + barrier, reads k-step 0
+    of the next stage; the last stage of a tile copies the next tile's stage
+    0; the epilogue stages the output through buffer 1, then lgkmcnt(0) +
+    barrier.  nst is even (the kernel pads K to an even stage count)."""
+    ev = [("dma", 0, (0, 0), ndma), ("wait", 0, True), ("barrier",), ("read", 0, (0, 0))]
+    for it in range(tiles):
+        for t in range(nst):
+            buf = t % 2
+            nxt = (it, t + 1) if t + 1 < nst else (it + 1, 0)
+            ev.append(("dma", buf ^ 1, nxt, ndma))
+            ev += [("read", buf, (it, t))] * 3
+            ev += [("wait", 0, True), ("barrier",), ("read", buf ^ 1, nxt)]
+        ev += [("ep", 1, None), ("wait", 63, True), ("barrier",)]
+    return ev
+
+
+@pytest.mark.parametrize("nst", [2, 4, 8, 64])
+@pytest.mark.parametrize("tiles", [1, 2, 5])
+def test_lds_persist_buffers(nst, tiles):
+    assert check_trace(lds_persist_trace(nst, tiles)) == []
+
+
+def test_lds_persist_model_catches_an_early_copy():
+    """Issuing the next stage's copies before the barrier that ends the reads
+    of that buffer (here: an odd stage count, so the tile's first copy lands in
+    the buffer the epilogue just used, before its barrier) is flagged."""
+    ev = lds_persist_trace(2, 2)
+    i = ev.index(("ep", 1, None))
+    bad_ev = ev[:i + 1] + [("dma", 1, ("x", 0), 16)] + ev[i + 1:]
+    assert check_trace(bad_ev) != []
+
+
+def test_moe_stage2_needs_no_ring_waits():
+    """moe_stage2.h keeps A and B in registers (the compiler orders their
+    loads and uses) and uses LDS only for a wave-private epilogue tile that the
+    same wave writes and then reads back: LDS operations of one wave complete
+    in issue order, so no wait or barrier publishes anything.  The model of
+    that tile: every read follows the wave's own write of the same bytes."""
+    bm = 32
+    written = set()
+    for i in range(bm // 32):
+        for lane in range(64):
+            r = 32 * i + (lane & 31)
+            for j in range(2):
+                for q in range(4):
+                    cc = 8 * j + 2 * q + (lane >> 5)
+                    written.add((r, (((cc >> 1) ^ (r & 7)) * 16) + (cc & 1) * 8))
+                    written.add((r, (((cc >> 1) ^ (r & 7)) * 16) + (cc & 1) * 8 + 4))
+    for r0 in range(0, bm, 8):
+        for lane in range(64):
+            r = r0 + (lane >> 3)
+            base = ((lane & 7) ^ (r & 7)) * 16
+            for b in range(0, 16, 4):
+                assert (r, base + b) in written
