@@ -609,15 +609,21 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
         splits = (kpairs + p.k_steps_per_split - 1) / p.k_steps_per_split;
         const dim3 grid((unsigned)((N + inst->bn - 1) / inst->bn), (unsigned)splits);
         if (inst->split && splits > 1) {
-            const size_t need = (size_t)M * N * sizeof(float);
-            p.ws = split_buffer(c, dev, stream, need);
             const int64_t n4 = (int64_t)M * N;
+            // f32 output with nothing to apply after the sum (no bias, alpha
+            // 1, no fused operation) and rows of exactly N: the partials add
+            // straight into the zeroed output, no workspace and no finish launch
+            const bool direct = c.var.out_f32 && p.ldd == N && !p.bias && p.alpha == 1.0f && !c.epi.kind;
+            p.ws = direct ? static_cast<float*>(p.D) : split_buffer(c, dev, stream, (size_t)n4 * sizeof(float));
             fill_zero_kernel<><<<dim3((unsigned)((n4 / 4 + 255) / 256 + 1)), 256, 0, stream>>>(p.ws, n4);
             inst->fn(p, grid, stream);
-            if (c.var.out_f32)
+            if (direct) {
+                // summed in place
+            } else if (c.var.out_f32) {
                 splitk_finish_kernel<true><<<dim3((unsigned)((n4 / 4 + 255) / 256)), 256, 0, stream>>>(p);
-            else
+            } else {
                 splitk_finish_kernel<false><<<dim3((unsigned)((n4 / 4 + 255) / 256)), 256, 0, stream>>>(p);
+            }
         } else if (inst->split) {
             // a split instance asked for one split runs its non-split twin
             // (the highest-ranked one, first registered among equals)

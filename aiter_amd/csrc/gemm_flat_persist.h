@@ -19,8 +19,8 @@
 // picked at run time inside the loop costs the register allocation dearly).
 //
 // Scope: no bias (the host uses the one-tile-per-workgroup kernel then),
-// alpha applied, K padded with zero stages to a multiple of 4 stages, at
-// least 8.  Results are bit-identical to gemm_flat_kernel: same MFMAs in the
+// alpha applied, K padded with zero stages to a multiple of 4 stages: 4, or
+// at least 8.  Results are bit-identical to gemm_flat_kernel: same MFMAs in the
 // same order per tile.
 #pragma once
 #include <type_traits>
@@ -78,8 +78,8 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     const int G = gridDim.x, blk = blockIdx.x;
     const int my_tiles = (n_tiles - blk + G - 1) / G;
     const int nstages = p.K / Cfg::K_STAGE;
-    // stages per tile: a multiple of 4, at least 8 (zero stages past K)
-    const int nst4 = nstages <= 8 ? 8 : (nstages + 3) & ~3;
+    // stages per tile: a multiple of 4 (zero stages past K); 4 or at least 8
+    const int nst4 = nstages <= 4 ? 4 : (nstages <= 8 ? 8 : (nstages + 3) & ~3);
 
     // tile-independent lane offsets; the tile origin is added per tile
     int a_off[NA];
@@ -363,24 +363,34 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
 
         read_scales(L0{}, sa_pk, sb_pk);
         read_a(L0{}, 0, 0);
-        // first four stages: the waits of stages 0 and 1 span the previous
-        // epilogue's stores (or the prologue's stand-ins)
-        stage(L0{}, WT{}, ca, csc, cnst, 3, cb, cnst, 2);
-        stage(L1{}, WT{}, ca, csc, cnst, 4, cb, cnst, 3);
-        stage(L2{}, WN{}, ca, csc, cnst, 5, cb, cnst, 4);
-        stage(L3{}, WN{}, ca, csc, cnst, 6, cb, cnst, 5);
-        for (int t = 4; t < nst4 - 4; t += 4) {
-            stage(L0{}, WN{}, ca, csc, cnst, t + 3, cb, cnst, t + 2);
-            stage(L1{}, WN{}, ca, csc, cnst, t + 4, cb, cnst, t + 3);
-            stage(L2{}, WN{}, ca, csc, cnst, t + 5, cb, cnst, t + 4);
-            stage(L3{}, WN{}, ca, csc, cnst, t + 6, cb, cnst, t + 5);
+        if (nst4 == 4) {
+            // a 4-stage tile (K <= 4 stages): its first four stages are its
+            // last four; the waits of stages 0 and 1 span the previous
+            // epilogue's stores, the look-ahead moves on to the next tile
+            stage(L0{}, WT{}, ca, csc, cnst, 3, cb, cnst, 2);
+            stage(L1{}, WT{}, xa, xsc, xnst, 0, cb, cnst, 3);
+            stage(L2{}, WN{}, xa, xsc, xnst, 1, xb, xnst, 0);
+            stage(L3{}, WN{}, xa, xsc, xnst, 2, xb, xnst, 1);
+        } else {
+            // first four stages: the waits of stages 0 and 1 span the previous
+            // epilogue's stores (or the prologue's stand-ins)
+            stage(L0{}, WT{}, ca, csc, cnst, 3, cb, cnst, 2);
+            stage(L1{}, WT{}, ca, csc, cnst, 4, cb, cnst, 3);
+            stage(L2{}, WN{}, ca, csc, cnst, 5, cb, cnst, 4);
+            stage(L3{}, WN{}, ca, csc, cnst, 6, cb, cnst, 5);
+            for (int t = 4; t < nst4 - 4; t += 4) {
+                stage(L0{}, WN{}, ca, csc, cnst, t + 3, cb, cnst, t + 2);
+                stage(L1{}, WN{}, ca, csc, cnst, t + 4, cb, cnst, t + 3);
+                stage(L2{}, WN{}, ca, csc, cnst, t + 5, cb, cnst, t + 4);
+                stage(L3{}, WN{}, ca, csc, cnst, t + 6, cb, cnst, t + 5);
+            }
+            // last four stages: the look-ahead moves on to the next tile
+            const int t4 = nst4 - 4;
+            stage(L0{}, WN{}, ca, csc, cnst, t4 + 3, cb, cnst, t4 + 2);
+            stage(L1{}, WN{}, xa, xsc, xnst, 0, cb, cnst, t4 + 3);
+            stage(L2{}, WN{}, xa, xsc, xnst, 1, xb, xnst, 0);
+            stage(L3{}, WN{}, xa, xsc, xnst, 2, xb, xnst, 1);
         }
-        // last four stages: the look-ahead moves on to the next tile
-        const int t4 = nst4 - 4;
-        stage(L0{}, WN{}, ca, csc, cnst, t4 + 3, cb, cnst, t4 + 2);
-        stage(L1{}, WN{}, xa, xsc, xnst, 0, cb, cnst, t4 + 3);
-        stage(L2{}, WN{}, xa, xsc, xnst, 1, xb, xnst, 0);
-        stage(L3{}, WN{}, xa, xsc, xnst, 2, xb, xnst, 1);
 
         // epilogue through ring slot 3: every wave finished reading it before
         // the last stage's barrier, and its next copy is issued in the next

@@ -107,9 +107,10 @@ void launch_skinny_alds(const GemmParams& p, dim3 grid, hipStream_t s) {
 }
 
 // the short-K direct skinny kernel: KP k-pairs at most (K <= KP * 256 for
-// the MX families), NWC waves of one column block each per workgroup; the
-// launcher's grid counts column blocks
-template <int KA, int MF, int NB, int KP, bool BP = true, bool OF = false, int NWC = 4>
+// the MX families), NWC waves of one column block each per workgroup (one:
+// N = 7168 gives 448 workgroups, spread over all CUs); the launcher's grid
+// counts column blocks
+template <int KA, int MF, int NB, int KP, bool BP = true, bool OF = false, int NWC = 1>
 void launch_skinny_direct(const GemmParams& p, dim3 grid, hipStream_t s) {
     constexpr int KPAIR = OpTraits<KA>::scaled ? 256 : 64;
     AA_CHECK(p.K / KPAIR <= KP, "direct skinny kernel: K = ", p.K, " is longer than its ", KP, " k-pairs");

@@ -74,18 +74,13 @@ int tile_from_name(const char* name, int stage, int block_m) {
     return stage == 1 ? block_m : std::min(block_m, 64);
 }
 
-// K = 512 (two 256-element windows) is instantiated only for MXFP8 A with
-// 64-row blocks, the one K = 512 form that matched the oracle on the GPU;
-// every other two-window form raises here (the host never selects one)
+// K = 256 or 512: one or two 256-element windows
 template <int KA, int BM>
 void launch_s2_kw(int kw, dim3 grid, const GemmParams& p, const MoeParams& mq, const MoeS2Params& sp, hipStream_t st) {
     if (kw == 1) {
         moe_stage2_stream_kernel<KA, BM, 1><<<grid, 256, 0, st>>>(p, mq, sp);
     } else if (kw == 2) {
-        if constexpr (KA == kFp8 && BM == 64)
-            moe_stage2_stream_kernel<KA, BM, 2><<<grid, 256, 0, st>>>(p, mq, sp);
-        else
-            fail("moe", "stream stage 2 with K = 512 exists for MXFP8 A with 64-row blocks only");
+        moe_stage2_stream_kernel<KA, BM, 2><<<grid, 256, 0, st>>>(p, mq, sp);
     } else {
         fail("moe", "stream stage 2: K / 256 must be 1 or 2");
     }
@@ -250,15 +245,11 @@ void run_stage(const StageArgs& s, hipStream_t st) {
             const int64_t n = mq.ws_rows * (mq.inter / 4);
             moe_stage1_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
         }
-    } else if ((bm == 32 || bm == 64) && (K == 256 || (K == 512 && bm == 64 && a_fp8)) &&
+    } else if ((bm == 32 || bm == 64) && (K == 256 || K == 512) &&
                !(s.kernel_name && std::string(s.kernel_name).find("flat") != std::string::npos)) {
         // short K: the streaming kernel (A in registers, a group of N tiles per
-        // workgroup, about 2048 workgroups in all).  Enabled where it is
-        // parity-tested: K = 256, and K = 512 for MXFP8 A with 64-row blocks.
-        // K = 512 with 32-row blocks (MXFP4 or MXFP8 A) gave wrong results on
-        // the GPU although a CPU emulation of its addressing matches the
-        // oracle; K = 512 with MXFP4 A and 64-row blocks was never validated.
-        // Those shapes take the flat kernel, and launch_s2_kw refuses them.
+        // workgroup, about 2048 workgroups in all); "_flat" names keep the
+        // flat tile kernel
         MoeS2Params sp{};
         const int64_t total_tiles = used * tiles_n;
         sp.tiles_per_group = (int)std::min<int64_t>(tiles_n, std::max<int64_t>(1, (total_tiles + 2047) / 2048));

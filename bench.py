@@ -136,11 +136,18 @@ def bench_prefill(steps, warmup, dev):
 _CEIL = {}
 
 
-def read_ceiling(dev, nbytes, grid=1024):
-    """Seconds per call of the calibration streaming read (`hbm_stream_read`,
-    nothing but 16-byte loads) over ``nbytes``, cold: the buffers rotate
-    through > 512 MiB.  The attainable HBM read time at that byte count,
-    launch and ramp included, that a bandwidth-bound GEMM is compared to."""
+# launch shapes of the calibration read (grid, threads per workgroup, loads
+# in flight per thread): the fastest ones of a sweep over unroll 1-8, block
+# 256-1024, grid 256-4096 and the cache policies, at 7.8, 29 and 125 MB
+CEILING_SHAPES = ((2048, 256, 1), (4096, 512, 1), (512, 1024, 1), (1024, 256, 4))
+
+
+def read_ceiling(dev, nbytes):
+    """Seconds per call of the fastest calibration streaming read
+    (`hbm_stream_read_cfg`, nothing but 16-byte loads) over ``nbytes``, cold:
+    the buffers rotate through > 512 MiB.  The attainable HBM read time at
+    that byte count, launch and ramp included, that a bandwidth-bound GEMM is
+    compared to (the minimum over CEILING_SHAPES)."""
     from aiter_amd._lib import call
 
     n = (nbytes + 15) // 16 * 16
@@ -148,16 +155,30 @@ def read_ceiling(dev, nbytes, grid=1024):
         copies = max(2, -(-(600 << 20) // n))
         bufs = [torch.ones(n, dtype=torch.uint8, device=dev) for _ in range(copies)]
         sink = torch.zeros(1, dtype=torch.int32, device=dev)
-        it = {"i": 0}
+        best = None
+        for grid, block, unroll in CEILING_SHAPES:
+            it = {"i": 0}
 
-        def run():
-            b = bufs[it["i"] % copies]
-            it["i"] += 1
-            call("hbm_stream_read", b, sink, grid)
+            def run():
+                b = bufs[it["i"] % copies]
+                it["i"] += 1
+                call("hbm_stream_read_cfg", b, sink, grid, block, unroll, -1)
 
-        _CEIL[n] = time_graph(run, copies * (4 if copies <= 100 else 1), 3)
+            t = time_graph(run, copies * (4 if copies <= 100 else 1), 3)
+            best = t if best is None else min(best, t)
+        _CEIL[n] = best
         del bufs
     return _CEIL[n]
+
+
+def launch_floor(dev):
+    """Seconds per graph-replayed launch of an empty grid of 1024 workgroups
+    (hbm_stream_read_cfg policy -2): the floor under any single-launch call."""
+    from aiter_amd._lib import call
+
+    src = torch.ones(1 << 20, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    return time_graph(lambda: call("hbm_stream_read_cfg", src, sink, 1024, 256, 1, -2), 100, 3)
 
 
 def bench_decode(dev, steps=50):
@@ -197,6 +218,7 @@ def bench_decode(dev, steps=50):
         t_warm = time_graph(warm, steps, 3)
         byts = a4w4_bytes(m, n, k)
         t_ceil = read_ceiling(dev, byts)
+        t_floor = launch_floor(dev) if not res else res[0]["launch_floor_us"] * 1e-6
         ref_bw = (m * k / 2 + n * k / 2 + 2 * m * n)  # reference `bw` formula (scales excluded)
         res.append({
             "M": m, "N": n, "K": k, "kernel": kname or "heuristic",
@@ -205,6 +227,7 @@ def bench_decode(dev, steps=50):
             "hbm_frac_cold": round(byts / t_cold / 1e9 / PEAK_HBM, 4),
             "ref_formula_GBps_cold": round(ref_bw / t_cold / 1e9, 1),
             "read_ceiling_us": round(t_ceil * 1e6, 3), "frac_of_read_ceiling": round(t_ceil / t_cold, 4),
+            "launch_floor_us": round(t_floor * 1e6, 3),
         })
         log(f"decode M={m}: cold {t_cold*1e6:.2f} us ({byts/t_cold/1e9:.0f} GB/s), warm {t_warm*1e6:.2f} us")
     return res
@@ -690,6 +713,23 @@ def profile_workload(dev, name):
     elif name == "fused_rms_mxfp4_8192":
         x, w = bf16(8192, 8192), bf16(1, 8192).view(-1)
         fn = lambda: aiter_amd.fused_rms_mxfp4_quant(x, w, 1e-6, shuffle=True)
+    elif name.startswith("moe_deepseek_"):
+        # fused_moe at the DeepSeek shape with "moe_deepseek_<tokens>" tokens
+        m = int(name.rsplit("_", 1)[1])
+        E, topk, dim, inter = 257, 9, 7168, 256
+        w1 = aiter_amd.shuffle_weight(torch.randint(0, 256, (E * 2 * inter, dim // 2), dtype=torch.uint8,
+                                                    device=dev, generator=g)).view(E, 2 * inter, dim // 2)
+        w2 = aiter_amd.shuffle_weight(torch.randint(0, 256, (E * dim, inter // 2), dtype=torch.uint8, device=dev,
+                                                    generator=g)).view(E, dim, inter // 2)
+        w1s = aiter_amd.shuffle_scale(torch.randint(119, 123, (E * 2 * inter, dim // 32), dtype=torch.uint8,
+                                                    device=dev, generator=g))
+        w2s = aiter_amd.shuffle_scale(torch.randint(119, 123, (E * dim, inter // 32), dtype=torch.uint8, device=dev,
+                                                    generator=g))
+        x = bf16(m, dim)
+        tw, ti = torch.topk(torch.softmax(torch.randn(m, E, device=dev, generator=g), -1), topk, -1)
+        tw, ti = (tw / tw.sum(-1, keepdim=True)).float(), ti.to(torch.int32)
+        fn = lambda: aiter_amd.fused_moe(x, w1, w2, tw, ti, quant_type=aiter_amd.QuantType.per_1x32, w1_scale=w1s,
+                                         w2_scale=w2s)
     elif _shape_workload(name):
         # "<a4w4|bf16|a8w4>_<M>x<N>x<K>": that GEMM through its public entry
         fam, (m, n, k) = _shape_workload(name)

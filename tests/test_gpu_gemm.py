@@ -267,6 +267,40 @@ def test_gemm_a16w16_every_instance(cuda, name):
     assert ok, msg
 
 
+def _split_f32_names():
+    try:
+        return [r[1] for r in _kernels("a16w16", out_f32=True) + _kernels("a16w16", b_pre=False, out_f32=True)
+                if r[3] and r[6]]
+    except RuntimeError:
+        return []
+
+
+@pytest.mark.parametrize("name", _split_f32_names())
+def test_gemm_a16w16_f32_split_sums_into_output(cuda, name):
+    """f32 output, no bias, split over K: the partials add straight into the
+    output, which the call clears first (NaN before the call, then a second
+    call on the first call's result)."""
+    import aiter_amd
+    from aiter_amd._lib import kernel_table
+
+    row = [r for r in kernel_table() if r[1] == name][0]
+    bm, b_pre = row[4], row[8]
+    m, n, k = max(1, bm - 3), 544, 2048
+    announce(f"a16w16 f32 split {name} {m}x{n}x{k}")
+    a = bf16_operand(m, k, 15)
+    b = bf16_operand(n, k, 16)
+    ref = O.bf16_bits_to_f32(a) @ O.bf16_bits_to_f32(b).T
+    bt_np = O.shuffle_weight(b) if b_pre else b
+    at = _dev(a.view(np.int16), cuda).view(torch.bfloat16)
+    bt = _dev(bt_np.view(np.int16), cuda).view(torch.bfloat16)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device=cuda)
+    for _ in range(2):
+        aiter_amd.gemm_a16w16_asm(at, bt, out, splitK=4, kernelName=name, bpreshuffle=b_pre)
+        torch.cuda.synchronize()
+        ok, msg = allclose_report(out.cpu().numpy(), ref)
+        assert ok, msg
+
+
 def _persistent_a16w16():
     try:
         from aiter_amd._lib import kernel_table

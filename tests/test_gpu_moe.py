@@ -246,14 +246,19 @@ def _accept(got, ref, max_diff=1e-4, min_close=0.98):
     assert d <= max_diff and close >= min_close, f"logits_diff {d:.3g}, within 1e-2: {close:.4f}"
 
 
-@pytest.mark.parametrize("inter,bs,tile", [(512, 32, ""), (512, 64, ""), (512, 64, "moe_m64_flat"), (768, 32, "")])
+@pytest.mark.parametrize("inter,bs,tile", [(512, 32, ""), (512, 64, ""), (512, 128, "moe_m32"),
+                                           (512, 64, "moe_m64_flat"), (768, 32, "")])
 @pytest.mark.parametrize("fp8", [False, True])
-def test_stage2_longer_k(cuda, inter, bs, tile, fp8):
-    """inter_dim 512: the streaming kernel's two-window form (MXFP8 A with
-    64-row blocks) or the flat kernel (32-row blocks, MXFP4 A, or named
-    _flat); 768: the flat kernel."""
-    announce(f"moe stage2 inter={inter} bs={bs} tile={tile} fp8={fp8}")
-    got, ref = _stage2_run(cuda, 40, 8, 1, 512, inter, bs, fp8, 260 + inter + bs, tile=tile)
+@pytest.mark.parametrize("per_pair", [False, True])
+def test_stage2_longer_k(cuda, inter, bs, tile, fp8, per_pair):
+    """inter_dim 512: the streaming kernel's two-window form (32- and 64-row
+    blocks, MXFP4 and MXFP8 A), or the flat kernel when named _flat; 768: the
+    flat kernel.  Atomic token rows (topk 1) and per-pair rows (topk 3)."""
+    announce(f"moe stage2 inter={inter} bs={bs} tile={tile} fp8={fp8} per_pair={per_pair}")
+    topk = 3 if per_pair else 1
+    got, ref = _stage2_run(cuda, 40, 8, topk, 512, inter, bs, fp8, 260 + inter + bs, tile=tile, per_pair=per_pair)
+    if per_pair:
+        got = got.float().cpu().numpy()
     ok, msg = allclose_report(got, ref)
     assert ok, msg
 

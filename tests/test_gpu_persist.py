@@ -43,6 +43,9 @@ def _shapes(row):
         (bm * 20 - 40, 256 * 16 - 16, 5 * ks),  # 320 tiles (more than the CUs), 5 stages -> 8
         (bm * 3, 256 * 2, 10 * ks),              # 6 tiles, 10 stages -> 12
         (bm * 32, 256 * 16, 8 * ks),             # 512 tiles: two per workgroup
+        (bm * 20 - 40, 256 * 16 - 16, 3 * ks),   # 320 tiles, 3 stages -> one 4-stage tile each
+        (bm * 32, 256 * 16, 4 * ks),             # 512 tiles of 4 stages: two per workgroup
+        (bm * 3, 256 * 2, 1 * ks),               # 6 tiles of 1 stage -> 4
     ]
 
 
@@ -128,6 +131,26 @@ def test_persist_against_oracle_a4w4(cuda):
                             out, kernelName="a4w4_tile_256x256_persist")
     torch.cuda.synchronize()
     ok, msg = allclose_report(out.float().cpu().numpy(), ref)
+    assert ok, msg
+
+
+def test_persist_four_stage_tiles_against_oracle(cuda):
+    """K = 1024 (4 stages: the tile's first four stages are its last four) with
+    more tiles than workgroups, each workgroup walking several tiles."""
+    import aiter_amd
+
+    m, n, k = 4096 + 200, 4096 - 16, 1024
+    announce(f"persist a4w4 4-stage tiles vs oracle {m}x{n}x{k}")
+    a_q, a_s, a_ss = mxfp4_operand(m, k, 64, "triton")
+    b_q, b_s, b_ss = mxfp4_operand(n, k, 65, "triton")
+    rows = np.unique(np.concatenate([np.arange(0, m, 97), [m - 1]]))
+    ref = O.bf16_bits_to_f32(O.gemm_a4w4_ref(a_q[rows], b_q, a_s[rows], b_s))
+    out = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.gemm_a4w4_asm(_dev(a_q, cuda), _dev(O.shuffle_weight(b_q), cuda), _dev(a_ss, cuda), _dev(b_ss, cuda),
+                            out, kernelName="a4w4_tile_256x256_persist")
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "output left unwritten"
+    ok, msg = allclose_report(out[torch.from_numpy(rows).to(cuda)].float().cpu().numpy(), ref)
     assert ok, msg
 
 

@@ -157,7 +157,7 @@ def run_persist(ndma, nb, nst, nstages, tiles):
     wait_n = loads_iter + ndma + 3 * nb
     wait_t = min(63, wait_n + nst)
     wait_p = min(63, 2 * ndma + 2 * nbl + nst)
-    nst4 = 8 if nstages <= 8 else (nstages + 3) & ~3
+    nst4 = 4 if nstages <= 4 else (8 if nstages <= 8 else (nstages + 3) & ~3)
     w = Wave()
     for t in range(2):
         w.issue(("A", 0, t), ndma)
@@ -231,7 +231,7 @@ def test_t32_kernel_waits(ns, ndma):
 
 @pytest.mark.parametrize("ka,bm", [("fp4", 256), ("fp4", 128), ("fp8", 256), ("bf16", 256)])
 @pytest.mark.parametrize("eb2", [1, 4, 8])
-@pytest.mark.parametrize("nstages", [2, 8, 9, 32])
+@pytest.mark.parametrize("nstages", [1, 2, 4, 5, 8, 9, 32])
 def test_persistent_kernel_waits(ka, bm, eb2, nstages):
     fa = 2 if ka == "fp8" else 1
     ndma = bm // 8 * fa // 4 + (0 if ka == "bf16" else 1)
