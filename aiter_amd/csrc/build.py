@@ -7,6 +7,7 @@ travels with the source tree.
 from __future__ import annotations
 
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -34,20 +35,44 @@ FLAGS = [
 ]
 
 
-def _compile(src: str, out_dir: str) -> str:
+# the compiler's per-kernel resource remarks (registers, spills, LDS)
+USAGE_FLAG = "-Rpass-analysis=kernel-resource-usage"
+
+
+def vgpr_spills(remarks: str) -> dict:
+    """{kernel symbol: spilled VGPRs} for every kernel that spills, from the
+    remarks of USAGE_FLAG."""
+    out, fn = {}, None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            fn = m.group(1)
+            continue
+        m = re.search(r"VGPRs Spill: (\d+)", line)
+        if m and fn and int(m.group(1)) > 0:
+            out[fn] = int(m.group(1))
+    return out
+
+
+def _compile(src: str, out_dir: str, extra=()) -> tuple:
     obj = os.path.join(out_dir, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, USAGE_FLAG, *extra, "-c", os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")
-    return obj
+    return obj, vgpr_spills(r.stderr)
 
 
 def build(verbose: bool = True) -> str:
     out_dir = os.path.join(PKG, "_build")
     os.makedirs(out_dir, exist_ok=True)
     with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, out_dir), SOURCES))
+        res = list(ex.map(lambda s: _compile(s, out_dir), SOURCES))
+    objs = [o for o, _ in res]
+    spills = {k: v for _, sp in res for k, v in sp.items()}
+    with open(os.path.join(out_dir, "vgpr_spills.txt"), "w") as f:
+        for k, v in sorted(spills.items()):
+            f.write(f"{v}\t{k}\n")
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -56,6 +81,8 @@ def build(verbose: bool = True) -> str:
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
+        if spills:
+            print(f"note: {len(spills)} kernel(s) spill VGPRs (list in {out_dir}/vgpr_spills.txt)")
     return LIB
 
 

@@ -41,7 +41,10 @@ struct FlatPersistCfg {
 
 // BPRE = false: row-major B, loaded straight into VGPRs as in gemm_flat_kernel.
 // SCALED = false: alpha == 1 (the epilogue skips the multiply).
-template <int KA, int BM, bool OUT_F32, bool BPRE = true, bool OUT_FP4 = false, bool SCALED = true>
+// SHORT4 = true: every tile is one 4-stage group (K <= 4 stages), so its first
+// four stages are its last four.  A separate instance: one body carrying both
+// stage sequences spills hundreds of VGPRs on the 256-row tiles.
+template <int KA, int BM, bool OUT_F32, bool BPRE = true, bool OUT_FP4 = false, bool SCALED = true, bool SHORT4 = false>
 __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p) {
     using Cfg = FlatPersistCfg<KA, BM>;
     constexpr int NS = 4;
@@ -78,8 +81,8 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
     const int G = gridDim.x, blk = blockIdx.x;
     const int my_tiles = (n_tiles - blk + G - 1) / G;
     const int nstages = p.K / Cfg::K_STAGE;
-    // stages per tile: a multiple of 4 (zero stages past K); 4 or at least 8
-    const int nst4 = nstages <= 4 ? 4 : (nstages <= 8 ? 8 : (nstages + 3) & ~3);
+    // stages per tile: a multiple of 4 (zero stages past K); 4 (SHORT4) or at least 8
+    const int nst4 = SHORT4 ? 4 : (nstages <= 8 ? 8 : (nstages + 3) & ~3);
 
     // tile-independent lane offsets; the tile origin is added per tile
     int a_off[NA];
@@ -363,7 +366,7 @@ __global__ __launch_bounds__(256, 1) void gemm_flat_persist_kernel(GemmParams p)
 
         read_scales(L0{}, sa_pk, sb_pk);
         read_a(L0{}, 0, 0);
-        if (nst4 == 4) {
+        if constexpr (SHORT4) {
             // a 4-stage tile (K <= 4 stages): its first four stages are its
             // last four; the waits of stages 0 and 1 span the previous
             // epilogue's stores, the look-ahead moves on to the next tile

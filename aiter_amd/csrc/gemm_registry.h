@@ -57,10 +57,18 @@ void launch_flat(const GemmParams& p, dim3 grid, hipStream_t s) {
 
 template <int KA, int BM, bool OF = false, bool BP = true>
 void launch_flat_persist(const GemmParams& p, dim3 grid, hipStream_t s) {
-    if (p.alpha == 1.0f)
-        gemm_flat_persist_kernel<KA, BM, OF, BP, false, false><<<grid, 256, 0, s>>>(p);
-    else
-        gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
+    const bool short4 = p.K / FlatPersistCfg<KA, BM>::K_STAGE <= 4;
+    if (p.alpha == 1.0f) {
+        if (short4)
+            gemm_flat_persist_kernel<KA, BM, OF, BP, false, false, true><<<grid, 256, 0, s>>>(p);
+        else
+            gemm_flat_persist_kernel<KA, BM, OF, BP, false, false><<<grid, 256, 0, s>>>(p);
+    } else {
+        if (short4)
+            gemm_flat_persist_kernel<KA, BM, OF, BP, false, true, true><<<grid, 256, 0, s>>>(p);
+        else
+            gemm_flat_persist_kernel<KA, BM, OF, BP><<<grid, 256, 0, s>>>(p);
+    }
 }
 
 template <bool BP>
