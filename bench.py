@@ -526,6 +526,14 @@ REF_MOE_STAGES = {1: (11.3537, 7.5406), 16: (40.5338, 24.9519), 128: (87.5346, 5
                   1024: (106.2571, 107.529), 4096: (191.9986, 283.9092)}
 
 
+def fused_moe_module():
+    """The aiter_amd.fused_moe module (the package attribute of that name is
+    the fused_moe function)."""
+    import importlib
+
+    return importlib.import_module("aiter_amd.fused_moe")
+
+
 def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter):
     """Each launch group of fused_moe timed on its own (graph-replayed, inputs
     from an eager run of the steps before it): the routing sort, the two
@@ -534,7 +542,8 @@ def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter
     like comparison with the reference's tuned us1 / us2 (stage kernels
     only)."""
     from aiter_amd import dtypes
-    from aiter_amd import fused_moe as FM
+
+    FM = fused_moe_module()
 
     m = x.shape[0]
     bm = FM.get_block_size_M(m, topk, E, inter)
