@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 ROOT = os.path.dirname(PKG)
 SOURCES = ["gemm.hip", "gemm_reg_mx.hip", "gemm_reg_bf16.hip", "gemm_reg_bf16_f32.hip", "gemm_reg_split.hip",
-           "gemm_reg_rest.hip", "gemm_reg_direct.hip", "quant.hip", "fused_quant.hip", "moe_sorting.hip", "moe_gemm.hip", "calib.hip"]
+           "gemm_reg_rest.hip", "gemm_reg_direct.hip", "gemm_reg_late.hip", "quant.hip", "fused_quant.hip", "moe_sorting.hip", "moe_gemm.hip", "calib.hip"]
 LIB = os.path.join(PKG, "libaiter_amd.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

@@ -52,6 +52,7 @@ std::vector<Instance>& registry() {
         b.part_persist_split();
         b.part_rest();
         b.part_direct();
+        b.part_late();
     });
     return reg;
 }

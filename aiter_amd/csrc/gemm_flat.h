@@ -591,7 +591,10 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     // ---- epilogue through LDS (the ring is free once every copy has landed)
     constexpr int EB = OUT_F32 ? 4 : 2;
     constexpr int WAVE_SCRATCH = NS * STAGE_BYTES / 4;
-    constexpr int EP_MP = (MA * 32 * 64 * EB <= WAVE_SCRATCH) ? MA : MA / 2;
+    // row tiles per epilogue pass: the most whose bytes fit the wave's scratch
+    constexpr int EP_MP = (MA * 32 * 64 * EB <= WAVE_SCRATCH)         ? MA
+                          : ((MA / 2) * 32 * 64 * EB <= WAVE_SCRATCH) ? MA / 2
+                                                                      : MA / 4;
     static_assert(MA % EP_MP == 0 && EP_MP * 32 * 64 * EB <= WAVE_SCRATCH, "epilogue pass fits the ring");
     wait_vmcnt<0>();
     if constexpr (MOE == kMoeStage1) {

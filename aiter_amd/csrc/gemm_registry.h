@@ -5,7 +5,7 @@
 // Every kernel instance has a stable name and integer id (the `kernelName` /
 // `kernelId` the tuned CSVs refer to); ids are assigned in registration
 // order, which the parts keep: part_mx, part_bf16<false>, part_bf16<true>,
-// part_persist_split, part_rest, part_direct.
+// part_persist_split, part_rest, part_direct, part_late.
 #pragma once
 
 #include <string>
@@ -177,6 +177,7 @@ struct RegBuilder {
     void part_persist_split();         // gemm_reg_split.hip
     void part_rest();                  // gemm_reg_rest.hip
     void part_direct();                // gemm_reg_direct.hip
+    void part_late();                  // gemm_reg_late.hip
 };
 
 constexpr Variant kPre{false, true, false}, kPlain{false, false, false}, kPre32{false, true, true};
