@@ -567,7 +567,8 @@ def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter
         s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, per_pair, topk, "", w2s, a2s, bm, sw, qt)
         s2()
         res["stage2_us"] = time_graph(s2, 10, 2)
-        res["moe_sum_us"] = time_graph(lambda: FM.moe_sum(per_pair, moe_buf), 10, 2)
+        moe_out = torch.empty((m, dim), dtype=torch.bfloat16, device=x.device)   # moe_buf is empty here
+        res["moe_sum_us"] = time_graph(lambda: FM.moe_sum(per_pair, moe_out), 10, 2)
     else:
         s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, moe_buf, topk, "", w2s, a2s, bm, sw, qt)
         res["stage2_us"] = time_graph(s2, 10, 2)
@@ -753,7 +754,8 @@ def profile_workload(dev, name):
             fn = lambda: aiter_amd.gemm_a8w4_mxfp8(xq, wq, xs, ws, a_preshuffle=False)
         else:
             a, b = bf16(m, k), bf16(n, k)
-            fn = lambda: aiter_amd.gemm_a16w16(a, b)
+            ot = torch.float32 if fam == "bf16f32" else None
+            fn = lambda: aiter_amd.gemm_a16w16(a, b, otype=ot)
     else:
         raise SystemExit(f"unknown workload {name}")
     fn()
@@ -767,11 +769,11 @@ def profile_workload(dev, name):
 
 
 def _shape_workload(name):
-    """("a4w4" | "bf16" | "a8w4", (M, N, K)) for a workload named
-    "<family>_<M>x<N>x<K>", else None."""
+    """("a4w4" | "bf16" | "bf16f32" | "a8w4", (M, N, K)) for a workload named
+    "<family>_<M>x<N>x<K>" (bf16f32: bf16 inputs, f32 output), else None."""
     fam, _, dims = name.partition("_")
     parts = dims.split("x")
-    if fam not in ("a4w4", "bf16", "a8w4") or len(parts) != 3 or not all(p.isdigit() for p in parts):
+    if fam not in ("a4w4", "bf16", "bf16f32", "a8w4") or len(parts) != 3 or not all(p.isdigit() for p in parts):
         return None
     return fam, tuple(int(p) for p in parts)
 

@@ -209,11 +209,12 @@ def test_fused_split_cat_epilogue_paths(cuda, monkeypatch, tmp_path, path, m, n,
 
 @pytest.mark.parametrize("bias", [False, True])
 @pytest.mark.parametrize("preshuffled", [True, False])
-@pytest.mark.parametrize("m,n4,n16", [(1, 1024, 256), (16, 1024, 256), (33, 1040, 272), (64, 1024, 256),
-                                      (300, 1024, 256)])
+@pytest.mark.parametrize("m,n4,n16", [(1, 1024, 256), (16, 1024, 256), (17, 1040, 272), (32, 1024, 256),
+                                      (33, 1040, 272), (64, 1024, 256), (300, 1024, 256)])
 def test_fused_gemm_afp4wfp4_a16w16(cuda, m, n4, n16, preshuffled, bias):
-    """M <= 64: both GEMMs in one grid (skinny_pair_kernel; ragged column
-    block counts at M = 33); M = 300: two launches."""
+    """M <= 32 (K short enough that neither GEMM splits): both GEMMs in one
+    grid (skinny_pair_kernel; ragged column block counts at M = 17); larger
+    M: two launches."""
     import aiter_amd
 
     k = 512
