@@ -118,6 +118,8 @@ SIGNATURES = {
     "mxfp4_moe_sort_hip": ([_T] * 4 + [ctypes.c_int] * 2 + [_S], ctypes.c_int),
     "ck_moe_stage1": ([_T] * 7 + [ctypes.c_int, ctypes.c_char_p, _T, _T, ctypes.c_int, _T] + [ctypes.c_int] * 4
                       + [ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
+    "ck_moe_stage1_fuse_quant": ([_T] * 7 + [ctypes.c_int, ctypes.c_char_p, _T, _T, ctypes.c_int, _T, _T,
+                                  ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
     "ck_moe_stage2": ([_T] * 7 + [ctypes.c_int, ctypes.c_char_p, _T, _T, ctypes.c_int, _T] + [ctypes.c_int] * 4
                       + [ctypes.c_char_p, ctypes.c_int, _S], ctypes.c_int),
     "moe_sum": ([_T, _T, _S], ctypes.c_int),

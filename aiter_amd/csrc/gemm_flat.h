@@ -75,7 +75,31 @@ struct MoeParams {
     int sort_bs;                // row block of the sort (a multiple of BM): expert of row r = sorted_eids[r / sort_bs]
     int k_splits;               // stage 1 split-K: > 1 -> raw f32 gate/up partials into GemmParams::ws
     int64_t ws_rows;            //   rows per split slice of ws (grid row blocks * BM)
+    // stage 1 with its output quantised in the epilogue (q_out null: bf16
+    // rows into `out`): each act(gate) * up row, rounded to bf16 as the plain
+    // store would, goes out as MXFP4 (RoundUp e8m0 from a running max of
+    // 1e-10): 16 code bytes per 32-column block into row token * topk + slot
+    // of q_out, the scale byte at the row's sorted position of the sorted,
+    // shuffled scale layout; a zero q_w (sorted routing weight) gives a zero
+    // block and byte, an invalid entry byte 0 (the sorted quantiser's rules)
+    uint8_t* q_out;
+    uint8_t* q_scale;
+    const float* q_w;
+    int64_t q_stride;           // bytes per q_out row
+    int q_scale_n_pad;          // scale columns of the sorted layout (pad8 of inter / 32)
 };
+
+// The MXFP4 block of 32 bf16 values given as 16 element pairs (RoundUp,
+// running max from 1e-10, the sorted quantiser's constants).
+AA_DEV uint32_t moe_quant_block(const uint32_t (&raw)[16], i32x4_t& o) {
+    float v[32];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        v[2 * i] = __builtin_bit_cast(float, raw[i] << 16);
+        v[2 * i + 1] = __builtin_bit_cast(float, raw[i] & 0xffff0000u);
+    }
+    return mx::quant32_fp4<uint16_t, mx::kRoundUp>(v, raw, 1e-10f, 1.0f / 6.0f, 0.25f, 0u, 2u, o);
+}
 
 AA_DEV void atomic_add_bf16x2(uint16_t* addr, uint32_t v) {
     asm volatile("global_atomic_pk_add_bf16 %0, %1, off" : : "v"(addr), "v"(v) : "memory");
@@ -659,6 +683,37 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
         }
         __syncthreads();
         if constexpr (MOE == kMoeStage1) {
+            if (mq.q_out) {
+                // fused output quant: (row, 32-column block) items of the tile
+                for (int it = threadIdx.x; it < BM * 4; it += 256) {
+                    const int row = it >> 2, yb = it & 3;
+                    const int pos = m0 + row;
+                    if (pos >= mq.sorted_len) continue;
+                    const int id = mq.sorted_ids[pos];
+                    const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+                    const int y = n0 / 32 + yb;
+                    uint8_t* sc = mq.q_scale + mx::scale_shuffle_idx(mq.q_scale_n_pad, pos, y);
+                    if (tok >= mq.token_num || slot >= mq.topk) {
+                        *sc = 0;
+                        continue;
+                    }
+                    i32x4_t o = {0, 0, 0, 0};
+                    uint32_t byte = 0;
+                    if (!(mq.q_w && mq.q_w[pos] == 0.0f)) {
+                        uint32_t raw[16];
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            const uint2 c = *chunk(row, 8 * yb + k);
+                            raw[2 * k] = c.x;
+                            raw[2 * k + 1] = c.y;
+                        }
+                        byte = moe_quant_block(raw, o);
+                    }
+                    *reinterpret_cast<i32x4_t*>(mq.q_out + ((int64_t)tok * mq.topk + slot) * mq.q_stride + y * 16) = o;
+                    *sc = (uint8_t)byte;
+                }
+                return;
+            }
             // lane l: row r0 + l/32, columns 4(l%32) .. +3
             for (int r0 = 2 * wave; r0 < BM; r0 += 8) {
                 const int row = r0 + (lane >> 5);

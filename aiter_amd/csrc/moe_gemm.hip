@@ -42,11 +42,79 @@ __global__ __launch_bounds__(256) void moe_stage1_reduce_kernel(const float* ws,
         uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 
+// the same with the fused output quant (MoeParams::q_out), laid out like the
+// plain reduce (thread: 4 columns of one sorted position) so that it runs as
+// many threads: the 8 threads of a 32-column block (consecutive lanes) take
+// the block's amax by lane exchange; each converts its 4 bf16-rounded values
+// with the block's scale into 2 code bytes (the bytes quant32_fp4 gives) and
+// the first writes the scale byte
+__global__ __launch_bounds__(256) void moe_stage1_reduce_quant_kernel(const float* ws, int splits, MoeParams mq) {
+    const int per_row = mq.inter / 4;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t pos = gid / per_row;
+    const int c = (int)(gid % per_row) * 4;
+    const int y = c / 32, sub = (c % 32) / 4;
+    // the 8 lanes of a block share pos (per_row is a multiple of 8), so
+    // every exit below is taken by all 8 or none of them
+    if (pos >= mq.ws_rows || pos >= *mq.num_valid || pos >= mq.sorted_len) return;
+    const int id = mq.sorted_ids[pos];
+    const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+    uint8_t* sc = mq.q_scale + mx::scale_shuffle_idx(mq.q_scale_n_pad, (int)pos, y);
+    if (tok >= mq.token_num || slot >= mq.topk) {
+        if (sub == 0) *sc = 0;
+        return;
+    }
+    uint8_t* dst = mq.q_out + ((int64_t)tok * mq.topk + slot) * mq.q_stride + y * 16 + 2 * sub;
+    if (mq.q_w && mq.q_w[pos] == 0.0f) {
+        *reinterpret_cast<uint16_t*>(dst) = 0;
+        if (sub == 0) *sc = 0;
+        return;
+    }
+    const float w = mq.sorted_w ? mq.sorted_w[pos] : 1.0f;
+    f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    const int64_t slice = mq.ws_rows * 2 * mq.inter;
+    const float* src = ws + pos * 2 * mq.inter + c;
+    for (int sp = 0; sp < splits; ++sp) {
+        g += *reinterpret_cast<const f32x4_t*>(src + sp * slice);
+        u += *reinterpret_cast<const f32x4_t*>(src + sp * slice + mq.inter);
+    }
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = moe_act(g[r] * w, mq.act) * (u[r] * w);
+    const uint32_t raw0 = pack_bf16x2(v[0], v[1]), raw1 = pack_bf16x2(v[2], v[3]);
+    // the bf16 values the plain path stores, as f32
+    const float b[4] = {__builtin_bit_cast(float, raw0 << 16), __builtin_bit_cast(float, raw0 & 0xffff0000u),
+                        __builtin_bit_cast(float, raw1 << 16), __builtin_bit_cast(float, raw1 & 0xffff0000u)};
+    float amax = 1e-10f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) amax = __builtin_fmaxf(amax, __builtin_fabsf(b[r]));
+#pragma unroll
+    for (int d = 1; d < 8; d <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, d));
+    const uint32_t byte = mx::e8m0_byte<mx::kRoundUp>(amax, 1.0f / 6.0f, 0.25f, 0u, 2u);
+    uint32_t wq = 0;
+    if (byte != 0u && byte != 255u) {
+        const float ds = __builtin_bit_cast(float, byte << 23);
+        wq = mx::cvt_fp4_pair<uint16_t>(wq, raw0, 0.f, 0.f, ds, 0);
+        wq = mx::cvt_fp4_pair<uint16_t>(wq, raw1, 0.f, 0.f, ds, 1);
+    } else {
+        const float inv = mx::inv_scale_from_byte(byte);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wq |= mx::f32_to_e2m1(b[r] * inv) << (4 * r);
+    }
+    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)wq;
+    if (sub == 0) *sc = (uint8_t)byte;
+}
+
 struct StageArgs {
     aiter_tensor_t *a, *w, *a_scale, *w_scale, *sorted_ids, *sorted_eids, *num_valid, *out, *sorted_w;
     int topk, block_m, activation, stage, splitk;
     int tile_m;   // GEMM row block (divides block_m; 0 = block_m)
     const char* kernel_name;
+    // stage 1 with the fused MXFP4 output quant: `out` holds the e2m1 codes
+    // [token_num * topk, inter / 2], q_scale the sorted shuffled scale bytes,
+    // q_w the sorted routing weights of the zero-row rule (optional)
+    aiter_tensor_t* q_scale = nullptr;
+    aiter_tensor_t* q_w = nullptr;
 };
 
 template <int KA, int MOE>
@@ -100,7 +168,12 @@ void run_stage(const StageArgs& s, hipStream_t st) {
     AA_CHECK(s.sorted_ids->dtype == AITER_DTYPE_i32 && s.sorted_eids->dtype == AITER_DTYPE_i32 &&
                  s.num_valid->dtype == AITER_DTYPE_i32,
              "sorted ids must be int32");
-    AA_CHECK(s.out->dtype == AITER_DTYPE_bf16, fn, ": bf16 output only, got ", dtype_name(s.out->dtype));
+    const bool fq = s.q_scale != nullptr;
+    if (fq)
+        AA_CHECK(s.stage == 1 && (s.out->dtype == AITER_DTYPE_fp4x2 || s.out->dtype == AITER_DTYPE_u8), fn,
+                 ": the fused-quant output must be fp4x2");
+    else
+        AA_CHECK(s.out->dtype == AITER_DTYPE_bf16, fn, ": bf16 output only, got ", dtype_name(s.out->dtype));
     AA_CHECK(s.w->dtype == AITER_DTYPE_fp4x2 || s.w->dtype == AITER_DTYPE_u8, fn, ": MXFP4 (fp4x2) weights only");
     const bool a_fp8 = s.a->dtype == AITER_DTYPE_fp8;
     AA_CHECK(a_fp8 || s.a->dtype == AITER_DTYPE_fp4x2 || s.a->dtype == AITER_DTYPE_u8,
@@ -159,9 +232,35 @@ void run_stage(const StageArgs& s, hipStream_t st) {
         AA_CHECK(s.activation == kActSilu || s.activation == kActGelu, "activation must be Silu (0) or Gelu (1)");
         AA_CHECK(arows >= 1, "empty input");
         token_num = arows;
-        AA_CHECK(rows_2d(s.out) == token_num * s.topk && cols_2d(s.out) == inter && s.out->strides[s.out->ndim - 1] == 1,
-                 "ck_moe_stage1: out must be [token_num, topk, inter_dim] bf16");
-        mq.out_stride = s.out->ndim >= 2 ? s.out->strides[s.out->ndim - 2] : inter;
+        if (fq) {
+            AA_CHECK(inter % 256 == 0, "ck_moe_stage1_fuse_quant: inter_dim = ", inter,
+                     " must be a multiple of 256 (whole 8-byte rows of scale bytes)");
+            AA_CHECK(rows_2d(s.out) == token_num * s.topk && cols_2d(s.out) == inter / 2 &&
+                         s.out->strides[s.out->ndim - 1] == 1,
+                     "ck_moe_stage1_fuse_quant: out must be [token_num, topk, inter_dim / 2] fp4x2");
+            mq.q_stride = s.out->ndim >= 2 ? s.out->strides[s.out->ndim - 2] : inter / 2;
+            AA_CHECK(mq.q_stride % 16 == 0 && ((uintptr_t)s.out->ptr & 15) == 0, "out rows must be 16-byte aligned");
+            check_tensor(s.q_scale, "out_scale");
+            mq.q_scale_n_pad = (int)(inter / 32);
+            const int64_t sorted_rows_q = ((int64_t)s.sorted_ids->numel + 31) / 32 * 32;
+            AA_CHECK(is_byte_type(s.q_scale->dtype) && (int64_t)s.q_scale->numel >= sorted_rows_q * mq.q_scale_n_pad,
+                     "out_scale must hold the sorted shuffled scales [", sorted_rows_q, ", ", mq.q_scale_n_pad, "]");
+            mq.q_out = static_cast<uint8_t*>(s.out->ptr);
+            mq.q_scale = static_cast<uint8_t*>(s.q_scale->ptr);
+            if (s.q_w) {
+                check_tensor(s.q_w, "quant_weights");
+                AA_CHECK(s.q_w->dtype == AITER_DTYPE_fp32 && (int64_t)s.q_w->numel >= (int64_t)s.sorted_ids->numel,
+                         "quant_weights must be float32 with len(sorted_token_ids) entries");
+                mq.q_w = static_cast<const float*>(s.q_w->ptr);
+            }
+            mq.out = nullptr;
+            mq.out_stride = 4;   // unused: no bf16 rows
+        } else {
+            AA_CHECK(rows_2d(s.out) == token_num * s.topk && cols_2d(s.out) == inter &&
+                         s.out->strides[s.out->ndim - 1] == 1,
+                     "ck_moe_stage1: out must be [token_num, topk, inter_dim] bf16");
+            mq.out_stride = s.out->ndim >= 2 ? s.out->strides[s.out->ndim - 2] : inter;
+        }
         mq.token_num = (int)token_num;
         mq.inter = (int)inter;
         tiles_n = (int)(inter / 128);
@@ -243,7 +342,10 @@ void run_stage(const StageArgs& s, hipStream_t st) {
         if (splits > 1) {
             AA_HIP(hipGetLastError());
             const int64_t n = mq.ws_rows * (mq.inter / 4);
-            moe_stage1_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
+            if (mq.q_out)
+                moe_stage1_reduce_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
+            else
+                moe_stage1_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
         }
     } else if ((bm == 32 || bm == 64) && (K == 256 || K == 512) &&
                !(s.kernel_name && std::string(s.kernel_name).find("flat") != std::string::npos)) {
@@ -341,6 +443,21 @@ int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tenso
         StageArgs s{hidden_states, w1, a1_scale, w1_scale, sorted_token_ids, sorted_expert_ids, num_valid_ids, out,
                     sorted_weights, topk, block_m, activation, 1, splitk, tile_from_name(kernelName, 1, block_m),
                     kernelName};
+        run_stage(s, reinterpret_cast<hipStream_t>(stream));
+    });
+}
+
+int ck_moe_stage1_fuse_quant(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* sorted_token_ids,
+                             aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids, aiter_tensor_t* out,
+                             aiter_tensor_t* out_scale, int topk, const char* kernelName, aiter_tensor_t* w1_scale,
+                             aiter_tensor_t* a1_scale, int block_m, aiter_tensor_t* sorted_weights,
+                             aiter_tensor_t* quant_weights, int activation, int splitk, aiter_stream_t stream) {
+    return safe_call([&] {
+        AA_CHECK(out_scale, "ck_moe_stage1_fuse_quant: out_scale must be given");
+        DeviceGuard g(hidden_states ? hidden_states->device_id : -1);
+        StageArgs s{hidden_states, w1, a1_scale, w1_scale, sorted_token_ids, sorted_expert_ids, num_valid_ids, out,
+                    sorted_weights, topk, block_m, activation, 1, splitk, tile_from_name(kernelName, 1, block_m),
+                    kernelName, out_scale, quant_weights};
         run_stage(s, reinterpret_cast<hipStream_t>(stream));
     });
 }

@@ -121,6 +121,48 @@ AA_DEV uint32_t cvt_fp8_pair(uint32_t old, uint32_t pair, float a, float b, floa
     return __builtin_bit_cast(uint32_t, r);
 }
 
+// e2m1 codes of one 32-element block held in registers: v = the 32 values
+// as f32, raw = the 16 element pairs as loaded (16-bit InT; unused for f32).
+// Returns the e8m0 byte (MODE, with the running max starting at amax_floor)
+// and the 16 code bytes in o (even element in the low nibble).  Bytes 1..254
+// take gfx950's scaled pair conversion (value / 2^(byte-127), RNE,
+// saturating), 0 and 255 the integer conversion of value * 2^(127-byte):
+// the same codes either way.
+template <typename InT, int MODE>
+AA_DEV uint32_t quant32_fp4(const float (&v)[32], const uint32_t (&raw)[16], float amax_floor, float inv_max_pos,
+                            float inv_max_pow2, uint32_t even_add, uint32_t emax, i32x4_t& o) {
+    float amax = amax_floor;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+    const uint32_t byte = e8m0_byte<MODE>(amax, inv_max_pos, inv_max_pow2, even_add, emax);
+    const float inv = inv_scale_from_byte(byte);
+    if (byte != 0u && byte != 255u) {
+        const float ds = __builtin_bit_cast(float, byte << 23);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if constexpr (sizeof(InT) == 2)
+                    w = cvt_fp4_pair<InT>(w, raw[i * 4 + j], 0.f, 0.f, ds, j);
+                else
+                    w = cvt_fp4_pair<float>(w, 0u, v[i * 8 + 2 * j], v[i * 8 + 2 * j + 1], ds, j);
+            }
+            o[i] = (int)w;
+        }
+    } else {
+        // scale byte 0 (2^-127, a subnormal f32) or 255 (NaN)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            uint32_t w = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) w |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
+            o[i] = (int)w;
+        }
+    }
+    return byte;
+}
+
 AA_DEV int scale_shuffle_idx(int scale_n_pad, int x, int y) {
     // csrc/include/mx_quant_utils.h:212-216
     return (x / 32 * scale_n_pad) * 32 + (y / 8) * 256 + (y % 4) * 64 + (x % 16) * 4 +

@@ -51,7 +51,7 @@ template <typename InT, bool OUT_FP8, int MODE>
 AA_DEV uint32_t quant_block32(const QuantParams& p, const InT* src, i32x4_t (&o)[2]) {
     constexpr int kVec = 16 / sizeof(InT);  // elements per 16-byte load
     float v[32];
-    uint32_t raw[sizeof(InT) == 2 ? 16 : 1];   // 16-bit inputs: the loaded element pairs
+    uint32_t raw[16];   // 16-bit inputs: the loaded element pairs (unused for f32)
 #pragma unroll
     for (int i = 0; i < 32 / kVec; ++i) {
         const i32x4_t w = *reinterpret_cast<const i32x4_t*>(src + i * kVec);
@@ -81,14 +81,15 @@ AA_DEV uint32_t quant_block32(const QuantParams& p, const InT* src, i32x4_t (&o)
             }
         }
     }
-    float amax = p.amax_floor;
+    if constexpr (!OUT_FP8) {
+        return quant32_fp4<InT, MODE>(v, raw, p.amax_floor, p.inv_max_pos, p.inv_max_pow2, p.even_add, p.emax,
+                                      o[0]);
+    } else {
+        float amax = p.amax_floor;
 #pragma unroll
-    for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
-
-    const uint32_t byte = e8m0_byte<MODE>(amax, p.inv_max_pos, p.inv_max_pow2, p.even_add, p.emax);
-    const float inv = inv_scale_from_byte(byte);
-
-    if constexpr (OUT_FP8) {
+        for (int i = 0; i < 32; ++i) amax = __builtin_fmaxf(amax, __builtin_fabsf(v[i]));
+        const uint32_t byte = e8m0_byte<MODE>(amax, p.inv_max_pos, p.inv_max_pow2, p.even_add, p.emax);
+        const float inv = inv_scale_from_byte(byte);
         if (byte != 0u && byte != 255u) {
             const float ds = __builtin_bit_cast(float, byte << 23);
 #pragma unroll
@@ -112,41 +113,8 @@ AA_DEV uint32_t quant_block32(const QuantParams& p, const InT* src, i32x4_t (&o)
                 o[i / 4][i % 4] = (int)w;
             }
         }
-    } else {
-        if (byte != 0u && byte != 255u) {
-            // gfx950 v_cvt_scalef32_pk_fp4_*: two values / 2^(byte-127) -> two
-            // e2m1 nibbles (RNE, saturating at 6; the even element in the low
-            // nibble), placed in byte `sel` of the destination: the same
-            // codes as f32_to_e2m1(x * 2^(127-byte)) below for every finite
-            // input, in one instruction per pair
-            const float ds = __builtin_bit_cast(float, byte << 23);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if constexpr (std::is_same<InT, _Float16>::value)
-                        w = cvt_fp4_pair<_Float16>(w, raw[i * 4 + j], 0.f, 0.f, ds, j);
-                    else if constexpr (sizeof(InT) == 2)
-                        w = cvt_fp4_pair<uint16_t>(w, raw[i * 4 + j], 0.f, 0.f, ds, j);
-                    else
-                        w = cvt_fp4_pair<float>(w, 0u, v[i * 8 + 2 * j], v[i * 8 + 2 * j + 1], ds, j);
-                }
-                o[0][i] = (int)w;
-            }
-        } else {
-            // scale byte 0 (2^-127, a subnormal f32) or 255 (NaN): the
-            // integer conversion
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                uint32_t w = 0;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) w |= f32_to_e2m1(v[i * 8 + j] * inv) << (4 * j);
-                o[0][i] = (int)w;
-            }
-        }
+        return byte;
     }
-    return byte;
 }
 
 template <typename InT, bool OUT_FP8, int MODE>

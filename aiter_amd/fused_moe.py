@@ -9,6 +9,8 @@ Mirrors the reference's entry points with their arguments and return values:
   fused_dynamic_mxfp8_quant_moe_sort  aiter/ops/quant.py:1183-1215
   mxfp4_moe_sort_fwd                  aiter/ops/quant.py:874-892
   ck_moe_stage1 / ck_moe_stage2       aiter/ops/moe_op.py:350-394
+  ck_moe_stage1_fuse_quant            the stage-1 call of a fuse_quant == "fp4"
+                                      configuration, aiter/fused_moe.py:3125-3171
   fused_moe                           aiter/fused_moe.py:454-558 (the
                                       per_1x32 path of fused_moe_2stages,
                                       aiter/fused_moe.py:2892-3276)
@@ -190,6 +192,26 @@ def ck_moe_stage1(hidden_states, w1, w2, sorted_token_ids, sorted_expert_ids, nu
          dst_type, int(bool(is_shuffled)))
 
 
+def ck_moe_stage1_fuse_quant(hidden_states, w1, sorted_token_ids, sorted_expert_ids, num_valid_ids, token_num: int,
+                             topk: int, block_m: int, w1_scale, a1_scale, sorted_weights=None, quant_weights=None,
+                             activation: int = 0, splitk: int = 0, kernelName: str | None = None):
+    """Stage 1 of a fuse_quant == "fp4" configuration (aiter/fused_moe.py:3125-3171):
+    the GEMM of ck_moe_stage1 with its act(gate) * up rows quantised to MXFP4
+    in the same launch.  Returns (a2 fp4x2 [token_num, topk, inter_dim / 2],
+    a2_scale in the sorted, shuffled layout), the bytes that
+    fused_dynamic_mx_quant_moe_sort(<ck_moe_stage1's bf16 output>, ...,
+    sorted_weights=quant_weights) returns.  ``sorted_weights`` (doweight_stage1)
+    scales gate and up before the activation, as in ck_moe_stage1."""
+    inter_dim = w1.shape[1] // 2
+    a2 = torch.empty((token_num, topk, inter_dim // 2), dtype=dtypes.fp4x2, device=hidden_states.device)
+    a2_scale = _sorted_scale(sorted_token_ids, inter_dim, hidden_states.device)
+    a = hidden_states if hidden_states.dtype == dtypes.fp8 else _u8(hidden_states)
+    call("ck_moe_stage1_fuse_quant", a, _u8(w1), sorted_token_ids, sorted_expert_ids, num_valid_ids,
+         _u8(a2.view(-1, a2.shape[-1])), _u8(a2_scale), int(topk), kernelName or "", _u8(w1_scale), _u8(a1_scale),
+         int(block_m), sorted_weights, quant_weights, int(activation), int(splitk))
+    return a2, a2_scale
+
+
 def ck_moe_stage2(inter_states, w1, w2, sorted_token_ids, sorted_expert_ids, num_valid_ids, out, topk: int,
                   kernelName: str | None = None, w2_scale=None, a2_scale=None, block_m: int | None = 32,
                   sorted_weights=None, quant_type: int = 0, activation: int = 0, splitk: int = 1,
@@ -252,11 +274,21 @@ def fused_moe_2stages(hidden_states, w1, w2, topk, sorted_ids, sorted_weights, s
     a1, a1_scale = fused_dynamic_mx_quant_moe_sort(hidden_states, sorted_ids, num_valid_ids, token_num, topk,
                                                    block_size_M, q_dtype_a, num_rows=num_local_tokens,
                                                    sorted_weights=sorted_weights)
-    a2 = torch.empty((token_num, topk, inter_dim), dtype=dtypes.bf16, device=hidden_states.device)
-    ck_moe_stage1(a1, w1, w2, sorted_ids, sorted_expert_ids, num_valid_ids, a2, topk, "", w1_scale, a1_scale,
-                  block_size_M, sorted_weights if doweight_stage1 else None, int(quant_type), int(activation), splitk=0)
-    a2q, a2_scale = fused_dynamic_mx_quant_moe_sort(a2.view(-1, inter_dim), sorted_ids, num_valid_ids, token_num,
-                                                    topk, block_size_M, q_dtype_a, sorted_weights=sorted_weights)
+    if q_dtype_a == dtypes.fp4x2 and inter_dim % 256 == 0 and expert_mask is None and num_local_tokens is None:
+        # fuse_quant "fp4": stage 1 writes its output already quantised (one
+        # launch and one pass over the stage-1 output less)
+        a2q, a2_scale = ck_moe_stage1_fuse_quant(a1, w1, sorted_ids, sorted_expert_ids, num_valid_ids, token_num,
+                                                 topk, block_size_M, w1_scale, a1_scale,
+                                                 sorted_weights if doweight_stage1 else None, sorted_weights,
+                                                 int(activation))
+    else:
+        a2 = torch.empty((token_num, topk, inter_dim), dtype=dtypes.bf16, device=hidden_states.device)
+        ck_moe_stage1(a1, w1, w2, sorted_ids, sorted_expert_ids, num_valid_ids, a2, topk, "", w1_scale, a1_scale,
+                      block_size_M, sorted_weights if doweight_stage1 else None, int(quant_type), int(activation),
+                      splitk=0)
+        a2q, a2_scale = fused_dynamic_mx_quant_moe_sort(a2.view(-1, inter_dim), sorted_ids, num_valid_ids,
+                                                        token_num, topk, block_size_M, q_dtype_a,
+                                                        sorted_weights=sorted_weights)
     if reduce:
         # one row per routed pair, then a fixed-order sum over the slots: device-
         # wide atomics cost one memory-side operation per 4 bytes, which

@@ -536,11 +536,12 @@ def fused_moe_module():
 
 def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter):
     """Each launch group of fused_moe timed on its own (graph-replayed, inputs
-    from an eager run of the steps before it): the routing sort, the two
-    sorted activation quants, stage 1 (with its split-K reduce) and stage 2
-    (with moe_sum when the per-pair rows are reduced by slot), for a like-for-
-    like comparison with the reference's tuned us1 / us2 (stage kernels
-    only)."""
+    from an eager run of the steps before it): the routing sort, the sorted
+    activation quant, stage 1 with its fused output quant (and its split-K
+    reduce) and stage 2 (with moe_sum when the per-pair rows are reduced by
+    slot), for a like-for-like comparison with the reference's tuned us1 /
+    us2 (stage kernels only; its decode rows' stage 1 also quantises its
+    output, the "_fp4" kernels of dsv3_fp4_tuned_fmoe.csv)."""
     from aiter_amd import dtypes
 
     FM = fused_moe_module()
@@ -553,15 +554,13 @@ def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter
     sids, sw, seids, nv, moe_buf = sort()
     q1 = lambda: FM.fused_dynamic_mx_quant_moe_sort(x, sids, nv, m, topk, bm, dtypes.fp4x2, sorted_weights=sw)
     a1, a1s = q1()
-    a2 = torch.empty((m, topk, inter), dtype=torch.bfloat16, device=x.device)
-    s1 = lambda: FM.ck_moe_stage1(a1, w1, w2, sids, seids, nv, a2, topk, "", w1s, a1s, bm, None, qt,
-                                  int(FM.ActivationType.Silu), splitk=0)
-    s1()
-    q2 = lambda: FM.fused_dynamic_mx_quant_moe_sort(a2.view(-1, inter), sids, nv, m, topk, bm, dtypes.fp4x2,
-                                                    sorted_weights=sw)
-    a2q, a2s = q2()
+    # stage 1 with its output quantised in the same launch (the flow fused_moe
+    # takes here; the reference's fuse_quant "fp4" stage 1)
+    s1 = lambda: FM.ck_moe_stage1_fuse_quant(a1, w1, sids, seids, nv, m, topk, bm, w1s, a1s, None, sw,
+                                             int(FM.ActivationType.Silu))
+    a2q, a2s = s1()
     res = {"sort_us": time_graph(sort, 10, 2), "quant1_us": time_graph(q1, 10, 2), "stage1_us": time_graph(s1, 10, 2),
-           "quant2_us": time_graph(q2, 10, 2)}
+           "quant2_us": 0.0}
     if reduce:
         per_pair = torch.empty((m, topk, dim), dtype=torch.bfloat16, device=x.device)
         s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, per_pair, topk, "", w2s, a2s, bm, sw, qt)

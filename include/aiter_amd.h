@@ -291,6 +291,21 @@ int ck_moe_stage1(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tenso
                   aiter_tensor_t* a1_scale, int block_m, aiter_tensor_t* sorted_weights, int quant_type,
                   int activation, int splitk, int use_non_temporal_load, const char* dst_type, int is_shuffled,
                   aiter_stream_t stream);
+/* Stage 1 with its output quantised in the same launch: replaces the stage-1
+ * call of a fuse_quant == "fp4" configuration (aiter/fused_moe.py:3125-3171:
+ * stage 1 returns (a2, a2_scale) and the separate
+ * fused_dynamic_mx_quant_moe_sort of the stage-1 output is skipped).  Same
+ * GEMM as ck_moe_stage1 (a4w4 or a8w4 input, per_1x32, preshuffled w1);
+ * out fp4x2 [token_num, topk, inter_dim / 2] and out_scale e8m0
+ * [pad32(len(sorted_token_ids)), inter_dim / 32] get exactly the bytes
+ * fused_dynamic_mx_quant_moe_sort_hip(out, out_scale, <ck_moe_stage1's bf16
+ * out>, sorted_token_ids, num_valid_ids, token_num, block_m, 32,
+ * quant_weights) would write.  inter_dim must be a multiple of 256. */
+int ck_moe_stage1_fuse_quant(aiter_tensor_t* hidden_states, aiter_tensor_t* w1, aiter_tensor_t* sorted_token_ids,
+                             aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids, aiter_tensor_t* out,
+                             aiter_tensor_t* out_scale, int topk, const char* kernelName, aiter_tensor_t* w1_scale,
+                             aiter_tensor_t* a1_scale, int block_m, aiter_tensor_t* sorted_weights,
+                             aiter_tensor_t* quant_weights, int activation, int splitk, aiter_stream_t stream);
 int ck_moe_stage2(aiter_tensor_t* inter_states, aiter_tensor_t* w1, aiter_tensor_t* w2,
                   aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids,
                   aiter_tensor_t* out, int topk, const char* kernelName, aiter_tensor_t* w2_scale,

@@ -195,6 +195,54 @@ def test_stage1_split_k(cuda, m, splitk, fp8):
     _stage1_check(cuda, m, 16, 9, 7168, 256, 32, fp8, 0, True, splitk, 900 + m + splitk)
 
 
+# (tokens, model_dim, inter_dim, block_m, splitk, MXFP8 input, activation,
+# doweight_stage1, zero routing weights): one-pass tiles (model_dim 512 /
+# 1024) and split K (model_dim 7168: 10 and 5 splits) through the reduce
+# kernel; Silu and Gelu; inter_dim 256 and 512 (one and two 128-column tiles
+# per 256-column scale row)
+FQ_CASES = [(5, 512, 256, 32, 1, False, 0, False, False), (200, 512, 256, 64, 1, True, 1, True, False),
+            (300, 1024, 512, 128, 1, False, 0, False, False), (40, 512, 256, 32, 1, False, 0, True, True),
+            (1, 7168, 256, 32, 0, False, 0, True, False), (4, 7168, 512, 32, 5, False, 1, False, True)]
+
+
+@pytest.mark.parametrize("m,dim,inter,bs,splitk,fp8,act,doweight,zero_w", FQ_CASES)
+def test_stage1_fuse_quant_matches_two_launches(cuda, m, dim, inter, bs, splitk, fp8, act, doweight, zero_w):
+    """ck_moe_stage1_fuse_quant writes exactly the bytes of ck_moe_stage1
+    followed by the sorted MXFP4 quant of its bf16 output: the e2m1 codes of
+    every routed (token, slot) row and the sorted scale rows below
+    num_valid_ids[0]; zero routing weights give zero blocks and bytes."""
+    import aiter_amd
+    from aiter_amd import dtypes
+
+    e, topk = 16, 3
+    announce(f"moe stage1 fuse_quant m={m} dim={dim} inter={inter} bs={bs} splitk={splitk} fp8={fp8} "
+             f"act={act} doweight={doweight} zero_w={zero_w}")
+    rng = np.random.default_rng(7000 + m + dim + inter)
+    ids, w = _routing(m, e, topk, rng)
+    if zero_w:
+        w[rng.random(w.shape) < 0.2] = 0.0
+    s, sw, se, nv, _ = _sort_dev(ids, w, e, bs, cuda, model_dim=dim)
+    x = to_bf16_f32(rng.standard_normal((m, dim)).astype(np.float32))
+    qfn = O.quant_mxfp8 if fp8 else O.quant_mxfp4
+    aq, a_s = qfn(x, O.ROUND_UP, amax_floor=1e-10)
+    a_sorted = _dev(MO.sort_scale_ref(a_s, s.cpu().numpy(), int(nv[0].item()), m, 1), cuda)
+    w1q, w1s = _weights(e, 2 * inter, dim, rng)
+    w1d, w1sd = _w_dev(w1q, w1s, cuda)
+    a_dev = _dev(aq, cuda).view(torch.float8_e4m3fn) if fp8 else _dev(aq, cuda)
+    dw = sw if doweight else None
+    a2 = torch.empty((m, topk, inter), dtype=torch.bfloat16, device=cuda)
+    aiter_amd.ck_moe_stage1(a_dev, w1d, None, s, se, nv, a2, topk, "", w1sd, a_sorted, bs, dw, 3, act, splitk=splitk)
+    ref_q, ref_s = aiter_amd.fused_dynamic_mx_quant_moe_sort(a2.view(-1, inter), s, nv, m, topk, bs, dtypes.fp4x2,
+                                                             sorted_weights=sw)
+    q, sc = aiter_amd.ck_moe_stage1_fuse_quant(a_dev, w1d, s, se, nv, m, topk, bs, w1sd, a_sorted, dw, sw, act,
+                                               splitk)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy().reshape(m * topk, inter // 2),
+                                  ref_q.view(torch.uint8).cpu().numpy().reshape(m * topk, inter // 2))
+    n = int(nv[0].item())
+    np.testing.assert_array_equal(sc.view(torch.uint8).cpu().numpy()[:n], ref_s.view(torch.uint8).cpu().numpy()[:n])
+
+
 def _stage2_run(cuda, m, e, topk, dim, inter, bs, fp8, seed, per_pair=False, tile=""):
     import aiter_amd
 
