@@ -23,8 +23,8 @@ from .fused_gemm import (fused_gemm_afp4wfp4_a16w16, fused_gemm_afp4wfp4_mul_add
                          fused_gemm_afp4wfp4_split_cat)
 from .fused_moe import (ActivationType, ck_moe_stage1, ck_moe_stage1_fuse_quant, ck_moe_stage2,
                         fused_dynamic_mx_quant_moe_sort, fused_dynamic_mxfp4_quant_moe_sort, fused_dynamic_mxfp8_quant_moe_sort, fused_moe,
-                        fused_moe_2stages, get_block_size_M, moe_sorting, moe_sorting_fwd, moe_sum,
-                        mxfp4_moe_sort_fwd)
+                        fused_moe_2stages, get_block_size_M, moe_sorting, moe_sorting_fwd, moe_sorting_mx_quant,
+                        moe_sum, mxfp4_moe_sort_fwd)
 from .gemm_op_a8w4 import gemm_a8w4_mxfp8, gemm_a8w4_mxfp8_dynamic
 from .gemm_op_a16w16 import gemm_a16w16_asm
 from .opus import gemm_a16w16_opus, opus_gemm_a16w16_tune, opus_gemm_workspace_init

@@ -114,6 +114,7 @@ SIGNATURES = {
     "fused_gemm_afp4wfp4_a16w16": ([_T] * 6 + [ctypes.c_char_p] + [_T] * 4 + [ctypes.c_char_p, ctypes.c_int, _S],
                                    ctypes.c_int),
     "moe_sorting_fwd": ([_T] * 7 + [ctypes.c_int, ctypes.c_int, _T, _T, ctypes.c_int, _S], ctypes.c_int),
+    "moe_sorting_mx_quant": ([_T] * 10 + [ctypes.c_int, ctypes.c_int, _S], ctypes.c_int),
     "fused_dynamic_mx_quant_moe_sort_hip": ([_T] * 5 + [ctypes.c_int] * 3 + [_T, _S], ctypes.c_int),
     "mxfp4_moe_sort_hip": ([_T] * 4 + [ctypes.c_int] * 2 + [_S], ctypes.c_int),
     "ck_moe_stage1": ([_T] * 7 + [ctypes.c_int, ctypes.c_char_p, _T, _T, ctypes.c_int, _T] + [ctypes.c_int] * 4

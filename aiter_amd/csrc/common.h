@@ -129,6 +129,9 @@ int device_cu_count(int dev);
 // inside graph capture: that raises); shared by the split-K GEMMs and the
 // MoE sort, which are stream-ordered on one stream.
 void* lib_workspace(int dev, hipStream_t st, size_t bytes);
+// Zeroed int counters of (device, stream), grown on demand like the
+// workspace; whoever uses them leaves them at zero when its launch ends.
+int* lib_counters(int dev, hipStream_t st, size_t count);
 
 }  // namespace aiter_amd
 

@@ -287,11 +287,14 @@ __global__ __launch_bounds__(256) void fill_byte_kernel(uint8_t* p, int64_t n, i
 struct WsKey {
     int dev;
     hipStream_t st;
-    int slot;   // 0: split-K partials, 1: low-precision-output f32 tile, 2: unit scales
+    // 0: split-K partials, 1: low-precision-output f32 tile, 2: unit scales,
+    // 3 / 4: x / w scales of a fused call shuffled, 5: tile counters (kCounterSlot)
+    int slot;
     bool operator<(const WsKey& o) const {
         return dev != o.dev ? dev < o.dev : (st != o.st ? st < o.st : slot < o.slot);
     }
 };
+constexpr int kCounterSlot = 5;
 struct WsVal {
     float* ptr = nullptr;
     size_t bytes = 0;
@@ -322,6 +325,9 @@ float* workspace(int dev, hipStream_t st, size_t bytes, int slot = 0) {
         }
         AA_HIP(hipMalloc(&w.ptr, bytes));
         w.bytes = bytes;
+        // counters start at zero; their users set them back to zero (never
+        // during graph capture: allocation is refused there)
+        if (slot == kCounterSlot) AA_HIP(hipMemsetAsync(w.ptr, 0, bytes, st));
     }
     return w.ptr;
 }
@@ -808,6 +814,9 @@ void mul_add_operand(const aiter_tensor_t* t, int64_t M, int64_t N, const void**
 }  // namespace
 
 void* lib_workspace(int dev, hipStream_t st, size_t bytes) { return workspace(dev, st, bytes); }
+int* lib_counters(int dev, hipStream_t st, size_t count) {
+    return reinterpret_cast<int*>(workspace(dev, st, count * sizeof(int), kCounterSlot));
+}
 
 }  // namespace aiter_amd
 

@@ -75,6 +75,11 @@ struct MoeParams {
     int sort_bs;                // row block of the sort (a multiple of BM): expert of row r = sorted_eids[r / sort_bs]
     int k_splits;               // stage 1 split-K: > 1 -> raw f32 gate/up partials into GemmParams::ws
     int64_t ws_rows;            //   rows per split slice of ws (grid row blocks * BM)
+    // split-K arrival counters, one per tile (row block * tiles_n + N tile),
+    // zero before the launch (needed whenever k_splits > 1): the split that
+    // arrives last sums the tile's partials in split order, applies weight,
+    // activation (and the output quant) and sets its counter back to zero
+    int* tile_cnt;
     // stage 1 with its output quantised in the epilogue (q_out null: bf16
     // rows into `out`): each act(gate) * up row, rounded to bf16 as the plain
     // store would, goes out as MXFP4 (RoundUp e8m0 from a running max of
@@ -108,6 +113,96 @@ AA_DEV void atomic_add_bf16x2(uint16_t* addr, uint32_t v) {
 AA_DEV float moe_act(float g, int act) {
     if (act == kActGelu) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f));
     return g / (1.0f + __expf(-g));
+}
+
+// Stage-1 split-K sum of one item of a tile: sorted position pos (entry id,
+// routing weight w), output columns c .. c+3.  The f32 gate / up partials of
+// every split are loaded together (up to 8 splits in flight) and added in
+// split order; then weight and act(gate) * up, rounded to bf16, go to row
+// token * topk + slot, as bf16 or (q_out) as MXFP4.  With q_out the 8 items
+// of one 32-column block must be 8 consecutive lanes (same pos, c = 32y + 4
+// sub): they take the block's amax by lane exchange; each converts its 4
+// values with the block's scale into 2 code bytes (the bytes quant32_fp4
+// gives) and the first writes the scale byte.  Every exit is taken by all 8
+// lanes of a block or none.
+// Split-K partials are written and read in the agent-coherent form (cache
+// policy sc1: past the XCD-private L2, to and from memory), so the split that
+// sums a tile sees what splits on other XCDs wrote without an L2 writeback or
+// invalidate; ws_rsrc covers the partials (byte offsets below 2^31).
+constexpr int kAgentCoherent = 16;
+
+template <bool QUANT>
+AA_DEV void moe_fold_item(__amdgpu_buffer_rsrc_t ws_rsrc, int splits, const MoeParams& mq, int64_t pos, int id,
+                          float w, int c) {
+    const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+    const bool valid = tok < mq.token_num && slot < mq.topk;
+    const int y = c / 32, sub = (c % 32) / 4;
+    if constexpr (QUANT) {
+        uint8_t* sc = mq.q_scale + mx::scale_shuffle_idx(mq.q_scale_n_pad, (int)pos, y);
+        if (!valid) {
+            if (sub == 0) *sc = 0;
+            return;
+        }
+        if (mq.q_w && mq.q_w[pos] == 0.0f) {
+            *reinterpret_cast<uint16_t*>(mq.q_out + ((int64_t)tok * mq.topk + slot) * mq.q_stride + y * 16 + 2 * sub) =
+                0;
+            if (sub == 0) *sc = 0;
+            return;
+        }
+    } else {
+        if (!valid) return;
+    }
+    f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    const int slice = (int)(mq.ws_rows * 2 * mq.inter * 4);      // bytes per split
+    const int off = (int)((pos * 2 * mq.inter + c) * 4);
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        f32x4_t gb[8], ub[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (s0 + k < splits) {
+                const int o = off + (s0 + k) * slice;
+                gb[k] = __builtin_bit_cast(f32x4_t,
+                                           __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, o, 0, kAgentCoherent));
+                ub[k] = __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(ws_rsrc, o + mq.inter * 4,
+                                                                                          0, kAgentCoherent));
+            }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (s0 + k < splits) {
+                g += gb[k];
+                u += ub[k];
+            }
+    }
+    float v[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v[r] = moe_act(g[r] * w, mq.act) * (u[r] * w);
+    const uint32_t raw0 = pack_bf16x2(v[0], v[1]), raw1 = pack_bf16x2(v[2], v[3]);
+    if constexpr (!QUANT) {
+        *reinterpret_cast<uint2*>(mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + c) = uint2{raw0, raw1};
+    } else {
+        // the bf16 values the plain path stores, as f32
+        const float b[4] = {__builtin_bit_cast(float, raw0 << 16), __builtin_bit_cast(float, raw0 & 0xffff0000u),
+                            __builtin_bit_cast(float, raw1 << 16), __builtin_bit_cast(float, raw1 & 0xffff0000u)};
+        float amax = 1e-10f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) amax = __builtin_fmaxf(amax, __builtin_fabsf(b[r]));
+#pragma unroll
+        for (int d = 1; d < 8; d <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, d));
+        const uint32_t byte = mx::e8m0_byte<mx::kRoundUp>(amax, 1.0f / 6.0f, 0.25f, 0u, 2u);
+        uint32_t wq = 0;
+        if (byte != 0u && byte != 255u) {
+            const float ds = __builtin_bit_cast(float, byte << 23);
+            wq = mx::cvt_fp4_pair<uint16_t>(wq, raw0, 0.f, 0.f, ds, 0);
+            wq = mx::cvt_fp4_pair<uint16_t>(wq, raw1, 0.f, 0.f, ds, 1);
+        } else {
+            const float inv = mx::inv_scale_from_byte(byte);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) wq |= mx::f32_to_e2m1(b[r] * inv) << (4 * r);
+        }
+        *reinterpret_cast<uint16_t*>(mq.q_out + ((int64_t)tok * mq.topk + slot) * mq.q_stride + y * 16 + 2 * sub) =
+            (uint16_t)wq;
+        if (sub == 0) *(mq.q_scale + mx::scale_shuffle_idx(mq.q_scale_n_pad, (int)pos, y)) = (uint8_t)byte;
+    }
 }
 
 // BPRE = false: B row-major [N, K].  The 32x32 MFMA's B operand is then 16
@@ -623,21 +718,57 @@ AA_DEV void flat_body(GemmParams p, const MoeParams& mq) {
     wait_vmcnt<0>();
     if constexpr (MOE == kMoeStage1) {
         if (mq.k_splits > 1) {
-            // raw f32 gate / up partials [split][ws_rows][2 * inter]; the reduce
-            // kernel sums the splits and applies weight and activation
-            float* wsb = p.ws + (int64_t)(kt0 / p.k_steps_per_split) * mq.ws_rows * (2 * mq.inter);
+            // raw f32 gate / up partials [split][ws_rows][2 * inter]; the split
+            // that finishes the tile last sums them and applies weight and activation
+            // (rows of padding entries are never read: not stored)
+            const __amdgpu_buffer_rsrc_t ws_rsrc = make_rsrc(p.ws, 0x7ffffff0LL);
+            const int wsb = (int)((kt0 / p.k_steps_per_split) * mq.ws_rows * (2 * mq.inter));   // floats
+            auto entry_of = [&](int r) -> int {   // any lane pattern
+                const int lo = __shfl(ids_r[0], r & 63), hi = __shfl(ids_r[IDR - 1], r & 63);
+                return r < 64 ? lo : hi;
+            };
 #pragma unroll
             for (int i = 0; i < MA; ++i) {
-                float* wrow = wsb + (int64_t)(m0 + 32 * i + (lane & 31)) * (2 * mq.inter) + n0 + 32 * wave +
-                              4 * (lane >> 5);
+                const int id = entry_of(32 * i + (lane & 31));
+                const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+                if (tok >= mq.token_num || slot >= mq.topk) continue;
+                const int wrow = wsb + (m0 + 32 * i + (lane & 31)) * (2 * mq.inter) + n0 + 32 * wave + 4 * (lane >> 5);
 #pragma unroll
                 for (int j = 0; j < NB; ++j)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
                         const f32x16v_t& a = acc[i][j];
-                        *reinterpret_cast<f32x4_t*>(wrow + (j ? mq.inter : 0) + 8 * q) =
-                            f32x4_t{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(i32x4_t, f32x4_t{a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]}),
+                            ws_rsrc, (wrow + (j ? mq.inter : 0) + 8 * q) * 4, 0, kAgentCoherent);
                     }
+            }
+            // arrival: every thread's partial stores have reached memory before
+            // the tile's counter is incremented
+            wait_vmcnt<0>();
+            __syncthreads();
+            int* flag = reinterpret_cast<int*>(smem);   // the ring is idle
+            if (threadIdx.x == 0) {
+                int* cnt = mq.tile_cnt + (int64_t)tm * p.tiles_n + tn;
+                const int last = atomicAdd(cnt, 1) == mq.k_splits - 1;
+                if (last) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                *flag = last;
+            }
+            __syncthreads();
+            if (!*flag) return;
+            // the last split sums the tile: rows m0 .., output columns n0 .. n0 + BN/2
+            // (entries and weights from the registers loaded at the start)
+            constexpr int IPR = BN / 8;   // items per row, 4 columns each
+            for (int it = threadIdx.x; it < BM * IPR; it += 256) {
+                const int row = it / IPR;
+                const int id = entry_of(row);
+                const float wl = __shfl(w_r[0], row & 63), wh = __shfl(w_r[IDR - 1], row & 63);
+                const float wgt = row < 64 ? wl : wh;
+                const int c = n0 + 4 * (it % IPR);
+                if (mq.q_out)
+                    moe_fold_item<true>(ws_rsrc, mq.k_splits, mq, m0 + row, id, wgt, c);
+                else
+                    moe_fold_item<false>(ws_rsrc, mq.k_splits, mq, m0 + row, id, wgt, c);
             }
             return;
         }

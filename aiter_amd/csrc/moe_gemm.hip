@@ -16,95 +16,6 @@ namespace {
 
 using namespace aiter_amd;
 
-// stage-1 split-K: sum the f32 partials of every split, then weight and
-// act(gate) * up -> bf16 row token * topk + slot; 4 columns per thread
-__global__ __launch_bounds__(256) void moe_stage1_reduce_kernel(const float* ws, int splits, MoeParams mq) {
-    const int per_row = mq.inter / 4;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t pos = gid / per_row;
-    const int c = (int)(gid % per_row) * 4;
-    if (pos >= mq.ws_rows || pos >= *mq.num_valid || pos >= mq.sorted_len) return;
-    const int id = mq.sorted_ids[pos];
-    const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
-    if (tok >= mq.token_num || slot >= mq.topk) return;
-    const float w = mq.sorted_w ? mq.sorted_w[pos] : 1.0f;
-    f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
-    const int64_t slice = mq.ws_rows * 2 * mq.inter;
-    const float* src = ws + pos * 2 * mq.inter + c;
-    for (int sp = 0; sp < splits; ++sp) {
-        g += *reinterpret_cast<const f32x4_t*>(src + sp * slice);
-        u += *reinterpret_cast<const f32x4_t*>(src + sp * slice + mq.inter);
-    }
-    float v[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = moe_act(g[r] * w, mq.act) * (u[r] * w);
-    *reinterpret_cast<uint2*>(mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + c) =
-        uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-}
-
-// the same with the fused output quant (MoeParams::q_out), laid out like the
-// plain reduce (thread: 4 columns of one sorted position) so that it runs as
-// many threads: the 8 threads of a 32-column block (consecutive lanes) take
-// the block's amax by lane exchange; each converts its 4 bf16-rounded values
-// with the block's scale into 2 code bytes (the bytes quant32_fp4 gives) and
-// the first writes the scale byte
-__global__ __launch_bounds__(256) void moe_stage1_reduce_quant_kernel(const float* ws, int splits, MoeParams mq) {
-    const int per_row = mq.inter / 4;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t pos = gid / per_row;
-    const int c = (int)(gid % per_row) * 4;
-    const int y = c / 32, sub = (c % 32) / 4;
-    // the 8 lanes of a block share pos (per_row is a multiple of 8), so
-    // every exit below is taken by all 8 or none of them
-    if (pos >= mq.ws_rows || pos >= *mq.num_valid || pos >= mq.sorted_len) return;
-    const int id = mq.sorted_ids[pos];
-    const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
-    uint8_t* sc = mq.q_scale + mx::scale_shuffle_idx(mq.q_scale_n_pad, (int)pos, y);
-    if (tok >= mq.token_num || slot >= mq.topk) {
-        if (sub == 0) *sc = 0;
-        return;
-    }
-    uint8_t* dst = mq.q_out + ((int64_t)tok * mq.topk + slot) * mq.q_stride + y * 16 + 2 * sub;
-    if (mq.q_w && mq.q_w[pos] == 0.0f) {
-        *reinterpret_cast<uint16_t*>(dst) = 0;
-        if (sub == 0) *sc = 0;
-        return;
-    }
-    const float w = mq.sorted_w ? mq.sorted_w[pos] : 1.0f;
-    f32x4_t g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
-    const int64_t slice = mq.ws_rows * 2 * mq.inter;
-    const float* src = ws + pos * 2 * mq.inter + c;
-    for (int sp = 0; sp < splits; ++sp) {
-        g += *reinterpret_cast<const f32x4_t*>(src + sp * slice);
-        u += *reinterpret_cast<const f32x4_t*>(src + sp * slice + mq.inter);
-    }
-    float v[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = moe_act(g[r] * w, mq.act) * (u[r] * w);
-    const uint32_t raw0 = pack_bf16x2(v[0], v[1]), raw1 = pack_bf16x2(v[2], v[3]);
-    // the bf16 values the plain path stores, as f32
-    const float b[4] = {__builtin_bit_cast(float, raw0 << 16), __builtin_bit_cast(float, raw0 & 0xffff0000u),
-                        __builtin_bit_cast(float, raw1 << 16), __builtin_bit_cast(float, raw1 & 0xffff0000u)};
-    float amax = 1e-10f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) amax = __builtin_fmaxf(amax, __builtin_fabsf(b[r]));
-#pragma unroll
-    for (int d = 1; d < 8; d <<= 1) amax = __builtin_fmaxf(amax, __shfl_xor(amax, d));
-    const uint32_t byte = mx::e8m0_byte<mx::kRoundUp>(amax, 1.0f / 6.0f, 0.25f, 0u, 2u);
-    uint32_t wq = 0;
-    if (byte != 0u && byte != 255u) {
-        const float ds = __builtin_bit_cast(float, byte << 23);
-        wq = mx::cvt_fp4_pair<uint16_t>(wq, raw0, 0.f, 0.f, ds, 0);
-        wq = mx::cvt_fp4_pair<uint16_t>(wq, raw1, 0.f, 0.f, ds, 1);
-    } else {
-        const float inv = mx::inv_scale_from_byte(byte);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) wq |= mx::f32_to_e2m1(b[r] * inv) << (4 * r);
-    }
-    *reinterpret_cast<uint16_t*>(dst) = (uint16_t)wq;
-    if (sub == 0) *sc = (uint8_t)byte;
-}
-
 struct StageArgs {
     aiter_tensor_t *a, *w, *a_scale, *w_scale, *sorted_ids, *sorted_eids, *num_valid, *out, *sorted_w;
     int topk, block_m, activation, stage, splitk;
@@ -333,20 +244,16 @@ void run_stage(const StageArgs& s, hipStream_t st) {
     mq.ws_rows = used * bm;
     if (splits > 1) {
         const size_t bytes = (size_t)splits * mq.ws_rows * 2 * mq.inter * sizeof(float);
+        AA_CHECK(bytes <= 0x7ffffff0u, "stage-1 split-K partials need ", bytes,
+                 " bytes (at most 2 GiB): ask for fewer splits (splitk)");
         p.ws = static_cast<float*>(lib_workspace(s.out->device_id, st, bytes));
+        // the split that finishes a tile last sums it (no reduce launch)
+        mq.tile_cnt = lib_counters(s.out->device_id, st, (size_t)tiles);
     }
     const dim3 grid((unsigned)((tiles * splits + 7) / 8 * 8));   // multiple of 8: XCD-aware tile order
     if (s.stage == 1) {
         if (a_fp8) launch_bm<kFp8, kMoeStage1>(bm, grid, p, mq, st);
         else launch_bm<kFp4, kMoeStage1>(bm, grid, p, mq, st);
-        if (splits > 1) {
-            AA_HIP(hipGetLastError());
-            const int64_t n = mq.ws_rows * (mq.inter / 4);
-            if (mq.q_out)
-                moe_stage1_reduce_quant_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
-            else
-                moe_stage1_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(p.ws, splits, mq);
-        }
     } else if ((bm == 32 || bm == 64) && (K == 256 || K == 512) &&
                !(s.kernel_name && std::string(s.kernel_name).find("flat") != std::string::npos)) {
         // short K: the streaming kernel (A in registers, a group of N tiles per

@@ -20,6 +20,7 @@
 // (count, scan, place); more take three launches: per-chunk counts, one scan
 // over chunks and experts, and one placement workgroup per chunk.
 #include "common.h"
+#include "mx_quant.h"
 
 namespace {
 
@@ -264,7 +265,233 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(uint8_t* dst, int64_t by
     for (int64_t i = n16 * 16 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < bytes; i += stride) dst[i] = 0;
 }
 
+
+// ---- decode: routing sort and the stage-1 activation quant in one launch ----
+// (the fusion of aiter/ops/flydsl/kernels/moe_fused_route_quant_scatter.py,
+// route map + MX quant + scale scatter, for this library's sorted list.)
+// For at most kSQMaxEntries routed entries (one wave holds them all), every
+// workgroup ranks the entries itself with ballots over the distinct experts
+// (no cross-workgroup step), quantises all token rows (their loads are
+// issued before the ranking, so the kernel has one dependent global load
+// level), and writes sorted row group blockIdx.x (32 positions): sorted ids
+// and weights, and the shuffled 256-byte scale blocks of the group's rows.
+// Workgroup 0 writes the block -> expert table and num_valid_ids; the token
+// rows' MXFP4 codes and the moe_buf clear are split over the workgroups.
+// Outputs equal moe_sorting_fwd followed by fused_dynamic_mx_quant_moe_sort
+// (stage 1, RoundUp e8m0 from 1e-10, sorted weights given) at positions below
+// num_valid_ids[0] (plus the rest of its last 32-row group); later positions
+// of sorted_ids / sorted_weights and later scale groups are left unwritten
+// (no reader goes past num_valid_ids[0]).  Every token row is quantised,
+// also one whose entries were all dropped, and a zero routing weight gives
+// scale byte 0 at its position with the token row quantised as usual.
+constexpr int kSQMaxEntries = 64;
+
+struct SortQuantParams {
+    SortParams s;               // no expert mask, no device token count
+    const uint16_t* x;          // bf16 [M, K]
+    int64_t x_stride;           // elements per row
+    uint8_t* q;                 // fp4x2 [M, K / 2]
+    int64_t q_stride;           // bytes per row
+    uint8_t* q_scale;           // [pad32(max_padded), scale_n_pad], sorted and shuffled
+    int scale_n, scale_n_pad;   // K / 32 and its pad to 8
+    uint8_t* zero_buf;          // moe_buf (may be null)
+    int64_t zero_bytes;
+};
+
+__global__ __launch_bounds__(256) void moe_sort_quant_small(SortQuantParams p) {
+    extern __shared__ uint8_t tok_sc[];   // [M][scale_n_pad] e8m0 bytes of the token rows
+    __shared__ int row_id[32];            // sorted entry of each row of the group (padding: pad id)
+    __shared__ float row_w[32];
+    __shared__ int s_total;
+    const SortParams& s = p.s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = s.M * s.topk;
+    const int grp = blockIdx.x, ngrp = gridDim.x;
+    const int pad_id = (s.topk << 24) | s.M;
+
+    // wave 0: entry `lane` (expert -1: none or dropped)
+    int e = -1;
+    float w = 0.0f;
+    if (wave == 0) {
+        e = expert_of(s, lane, n);
+        if (lane < n) w = s.topk_w[(int64_t)(lane / s.topk) * s.w_stride + lane % s.topk];
+    }
+    // this workgroup's share of the moe_buf clear
+    if (p.zero_bytes > 0) {
+        const int64_t units = p.zero_bytes / 16, per = (units + ngrp - 1) / ngrp;
+        for (int64_t u = grp * per + tid; u < min(units, (int64_t)(grp + 1) * per); u += 256)
+            reinterpret_cast<i32x4_t*>(p.zero_buf)[u] = i32x4_t{0, 0, 0, 0};
+        if (grp == 0)
+            for (int64_t b = units * 16 + tid; b < p.zero_bytes; b += 256) p.zero_buf[b] = 0;
+    }
+    // token rows: item (token, block y), up to 4 per thread with their loads in flight together
+    const int items = s.M * p.scale_n;
+    for (int b0 = 0; b0 < items; b0 += 4 * 256) {
+        i32x4_t raw[4][4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int it = b0 + 256 * k + tid;
+            if (it < items) {
+                const int t = it / p.scale_n, y = it - t * p.scale_n;
+                const i32x4_t* src = reinterpret_cast<const i32x4_t*>(p.x + t * p.x_stride + (int64_t)y * 32);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) raw[k][c] = src[c];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int it = b0 + 256 * k + tid;
+            if (it >= items) continue;
+            const int t = it / p.scale_n, y = it - t * p.scale_n;
+            float v[32];
+            uint32_t pr[16];
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t d = (uint32_t)raw[k][c][j];
+                    pr[4 * c + j] = d;
+                    v[8 * c + 2 * j] = __builtin_bit_cast(float, d << 16);
+                    v[8 * c + 2 * j + 1] = __builtin_bit_cast(float, d & 0xffff0000u);
+                }
+            i32x4_t o;
+            const uint32_t byte =
+                aiter_amd::mx::quant32_fp4<uint16_t, aiter_amd::mx::kRoundUp>(v, pr, 1e-10f, 1.0f / 6.0f, 0.25f, 0u, 2u, o);
+            tok_sc[t * p.scale_n_pad + y] = (uint8_t)byte;
+            if (it % ngrp == grp) *reinterpret_cast<i32x4_t*>(p.q + t * p.q_stride + (int64_t)y * 16) = o;
+        }
+    }
+    for (int i = tid; i < s.M * (p.scale_n_pad - p.scale_n); i += 256) {
+        const int t = i / (p.scale_n_pad - p.scale_n);
+        tok_sc[t * p.scale_n_pad + p.scale_n + i % (p.scale_n_pad - p.scale_n)] = 0;
+    }
+    if (wave == 0) {
+        // rank: position = padded counts of the smaller experts + entries of
+        // the same expert on lower lanes (entry order = token, slot order)
+        uint64_t act = __ballot(e >= 0);
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        int before = 0, rank = 0, mine = 0, total = 0;
+        while (act) {
+            const int leader = __builtin_ctzll(act);
+            const int le = __builtin_amdgcn_readlane(e, leader);
+            const uint64_t m = __ballot(e == le);
+            const int pc = (__popcll(m) + s.bs - 1) / s.bs * s.bs;
+            if (e == le) {
+                rank = __popcll(m & below);
+                mine = pc;
+            }
+            if (e > le) before += pc;
+            total += pc;
+            act &= ~m;
+        }
+        const int pos = before + rank;
+        if (lane < 32) {
+            row_id[lane] = pad_id;
+            row_w[lane] = 0.0f;
+        }
+        if (e >= 0 && pos >= 32 * grp && pos < 32 * grp + 32) {
+            const int t = lane / s.topk;
+            row_id[pos - 32 * grp] = ((lane - t * s.topk) << 24) | t;
+            row_w[pos - 32 * grp] = w;
+        }
+        if (lane == 0) s_total = total;
+        if (grp == 0) {
+            // the expert's row blocks (the first entry of each expert writes them)
+            if (e >= 0 && rank == 0)
+                for (int b = before / s.bs; b < (before + mine) / s.bs && b < s.max_blocks; ++b) s.sorted_eids[b] = e;
+            if (lane == 0) {
+                s.num_valid[0] = total;
+                s.num_valid[1] = s.M;
+            }
+        }
+    }
+    __syncthreads();
+    const int total = s_total;
+    if (grp == 0)
+        for (int b = total / s.bs + tid; b < s.max_blocks; b += 256) s.sorted_eids[b] = -1;
+    if (32 * grp >= total) return;
+    if (tid < 32 && 32 * grp + tid < s.max_padded) {
+        s.sorted_ids[32 * grp + tid] = row_id[tid];
+        s.sorted_w[32 * grp + tid] = row_w[tid];
+    }
+    // the group's scale blocks: 16-byte piece w16 of column octet y8 holds
+    // rows 4(w16 % 4) + (b >> 2) + 16(b & 1), columns 8 y8 + w16 / 4 + 4((b >> 1) & 1)
+    // for its bytes b (the mx_scale_shuffle_idx layout)
+    for (int c = tid; c < 2 * p.scale_n_pad; c += 256) {
+        const int y8 = c >> 4, w16 = c & 15;
+        uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int xr = 4 * (w16 & 3) + (b >> 2) + 16 * (b & 1);
+            const int yy = (w16 >> 2) + 4 * ((b >> 1) & 1);
+            const int id = row_id[xr];
+            const int t = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+            const bool valid = 32 * grp + xr < total && t < s.M && slot < s.topk && row_w[xr] != 0.0f;
+            const uint32_t byte = valid ? tok_sc[t * p.scale_n_pad + 8 * y8 + yy] : 0u;
+            d[b >> 2] |= byte << (8 * (b & 3));
+        }
+        *reinterpret_cast<i32x4_t*>(p.q_scale + (int64_t)grp * 32 * p.scale_n_pad + y8 * 256 + w16 * 16) =
+            i32x4_t{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+    }
+}
 }  // namespace
+
+// Checks the routing inputs and sorted outputs of a sort (the moe_sorting_fwd
+// contract) and fills the kernel parameters.
+static SortParams sort_params(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights,
+                              aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_weights,
+                              aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids, int num_experts,
+                              int unit_size, aiter_tensor_t* local_expert_mask, aiter_tensor_t* num_local_tokens) {
+    using namespace aiter_amd;
+    check_tensor(topk_ids, "topk_ids", 2);
+    check_tensor(topk_weights, "topk_weights", 2);
+    check_tensor(sorted_token_ids, "sorted_token_ids", 1);
+    check_tensor(sorted_weights, "sorted_weights", 1);
+    check_tensor(sorted_expert_ids, "sorted_expert_ids", 1);
+    check_tensor(num_valid_ids, "num_valid_ids", 1);
+    AA_CHECK(topk_ids->dtype == AITER_DTYPE_i32, "topk_ids must be int32");
+    AA_CHECK(topk_weights->dtype == AITER_DTYPE_fp32, "topk_weights must be float32");
+    AA_CHECK(sorted_token_ids->dtype == AITER_DTYPE_i32 && sorted_expert_ids->dtype == AITER_DTYPE_i32 &&
+                 num_valid_ids->dtype == AITER_DTYPE_i32,
+             "sorted_token_ids, sorted_expert_ids and num_valid_ids must be int32");
+    AA_CHECK(sorted_weights->dtype == AITER_DTYPE_fp32, "sorted_weights must be float32");
+    AA_CHECK(topk_ids->strides[1] == 1 && topk_weights->strides[1] == 1, "topk tensors need unit column stride");
+    const int M = (int)topk_ids->shape[0], topk = (int)topk_ids->shape[1];
+    AA_CHECK(topk_weights->shape[0] == M && topk_weights->shape[1] == topk, "topk_weights shape != topk_ids shape");
+    AA_CHECK(num_experts >= 1 && num_experts <= kMaxE, "num_experts must be in [1, ", kMaxE, "], got ", num_experts);
+    AA_CHECK(unit_size >= 1, "unit_size must be positive");
+    AA_CHECK(topk >= 1 && topk < 128 && M < (1 << 24), "topk must be in [1, 127] and tokens < 2^24");
+    const int64_t max_padded = (int64_t)M * topk + (int64_t)num_experts * unit_size - topk;
+    const int64_t max_blocks = (max_padded + unit_size - 1) / unit_size;
+    AA_CHECK(sorted_token_ids->numel >= (size_t)max_padded && sorted_weights->numel >= (size_t)max_padded,
+             "sorted_token_ids / sorted_weights need ", max_padded, " entries");
+    AA_CHECK(sorted_expert_ids->numel >= (size_t)max_blocks, "sorted_expert_ids needs ", max_blocks, " entries");
+    AA_CHECK(num_valid_ids->numel >= 2, "num_valid_ids needs 2 entries");
+    if (local_expert_mask) {
+        AA_CHECK(local_expert_mask->dtype == AITER_DTYPE_i32 && local_expert_mask->numel >= (size_t)num_experts,
+                 "local_expert_mask must be int32 with num_experts entries");
+    }
+    if (num_local_tokens) AA_CHECK(num_local_tokens->dtype == AITER_DTYPE_i32, "num_local_tokens must be int32");
+
+    SortParams p{};
+    p.topk_ids = static_cast<const int*>(topk_ids->ptr);
+    p.topk_w = static_cast<const float*>(topk_weights->ptr);
+    p.sorted_ids = static_cast<int*>(sorted_token_ids->ptr);
+    p.sorted_w = static_cast<float*>(sorted_weights->ptr);
+    p.sorted_eids = static_cast<int*>(sorted_expert_ids->ptr);
+    p.num_valid = static_cast<int*>(num_valid_ids->ptr);
+    p.expert_mask = local_expert_mask ? static_cast<const int*>(local_expert_mask->ptr) : nullptr;
+    p.num_local = num_local_tokens ? static_cast<const int*>(num_local_tokens->ptr) : nullptr;
+    p.ids_stride = topk_ids->strides[0];
+    p.w_stride = topk_weights->strides[0];
+    p.M = M;
+    p.topk = topk;
+    p.E = num_experts;
+    p.bs = unit_size;
+    p.max_padded = (int)max_padded;
+    p.max_blocks = (int)max_blocks;
+    return p;
+}
 
 extern "C" {
 
@@ -275,56 +502,12 @@ int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aite
     using namespace aiter_amd;
     return safe_call([&] {
         check_tensor(topk_ids, "topk_ids", 2);
-        check_tensor(topk_weights, "topk_weights", 2);
-        check_tensor(sorted_token_ids, "sorted_token_ids", 1);
-        check_tensor(sorted_weights, "sorted_weights", 1);
-        check_tensor(sorted_expert_ids, "sorted_expert_ids", 1);
-        check_tensor(num_valid_ids, "num_valid_ids", 1);
         DeviceGuard g(topk_ids->device_id);
         hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-        AA_CHECK(topk_ids->dtype == AITER_DTYPE_i32, "topk_ids must be int32");
-        AA_CHECK(topk_weights->dtype == AITER_DTYPE_fp32, "topk_weights must be float32");
-        AA_CHECK(sorted_token_ids->dtype == AITER_DTYPE_i32 && sorted_expert_ids->dtype == AITER_DTYPE_i32 &&
-                     num_valid_ids->dtype == AITER_DTYPE_i32,
-                 "sorted_token_ids, sorted_expert_ids and num_valid_ids must be int32");
-        AA_CHECK(sorted_weights->dtype == AITER_DTYPE_fp32, "sorted_weights must be float32");
-        AA_CHECK(topk_ids->strides[1] == 1 && topk_weights->strides[1] == 1, "topk tensors need unit column stride");
-        const int M = (int)topk_ids->shape[0], topk = (int)topk_ids->shape[1];
-        AA_CHECK(topk_weights->shape[0] == M && topk_weights->shape[1] == topk, "topk_weights shape != topk_ids shape");
-        AA_CHECK(num_experts >= 1 && num_experts <= kMaxE, "num_experts must be in [1, ", kMaxE, "], got ",
-                 num_experts);
-        AA_CHECK(unit_size >= 1, "unit_size must be positive");
-        AA_CHECK(topk >= 1 && topk < 128 && M < (1 << 24), "topk must be in [1, 127] and tokens < 2^24");
         AA_CHECK(dispatch_policy == 0, "only dispatch_policy 0 is supported");
-        const int64_t max_padded = (int64_t)M * topk + (int64_t)num_experts * unit_size - topk;
-        const int64_t max_blocks = (max_padded + unit_size - 1) / unit_size;
-        AA_CHECK(sorted_token_ids->numel >= (size_t)max_padded && sorted_weights->numel >= (size_t)max_padded,
-                 "sorted_token_ids / sorted_weights need ", max_padded, " entries");
-        AA_CHECK(sorted_expert_ids->numel >= (size_t)max_blocks, "sorted_expert_ids needs ", max_blocks, " entries");
-        AA_CHECK(num_valid_ids->numel >= 2, "num_valid_ids needs 2 entries");
-        if (local_expert_mask) {
-            AA_CHECK(local_expert_mask->dtype == AITER_DTYPE_i32 && local_expert_mask->numel >= (size_t)num_experts,
-                     "local_expert_mask must be int32 with num_experts entries");
-        }
-        if (num_local_tokens) AA_CHECK(num_local_tokens->dtype == AITER_DTYPE_i32, "num_local_tokens must be int32");
-
-        SortParams p{};
-        p.topk_ids = static_cast<const int*>(topk_ids->ptr);
-        p.topk_w = static_cast<const float*>(topk_weights->ptr);
-        p.sorted_ids = static_cast<int*>(sorted_token_ids->ptr);
-        p.sorted_w = static_cast<float*>(sorted_weights->ptr);
-        p.sorted_eids = static_cast<int*>(sorted_expert_ids->ptr);
-        p.num_valid = static_cast<int*>(num_valid_ids->ptr);
-        p.expert_mask = local_expert_mask ? static_cast<const int*>(local_expert_mask->ptr) : nullptr;
-        p.num_local = num_local_tokens ? static_cast<const int*>(num_local_tokens->ptr) : nullptr;
-        p.ids_stride = topk_ids->strides[0];
-        p.w_stride = topk_weights->strides[0];
-        p.M = M;
-        p.topk = topk;
-        p.E = num_experts;
-        p.bs = unit_size;
-        p.max_padded = (int)max_padded;
-        p.max_blocks = (int)max_blocks;
+        SortParams p = sort_params(topk_ids, topk_weights, sorted_token_ids, sorted_weights, sorted_expert_ids,
+                                   num_valid_ids, num_experts, unit_size, local_expert_mask, num_local_tokens);
+        const int M = p.M, topk = p.topk;
         const int64_t entries = (int64_t)M * topk;
         p.nchunks = (int)((entries + kThreads - 1) / kThreads);
         const int64_t buf_bytes =
@@ -348,6 +531,68 @@ int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aite
             fill_zero_kernel<<<(unsigned)blocks, 256, 0, st>>>(static_cast<uint8_t*>(moe_buf->ptr), bytes);
             AA_HIP(hipGetLastError());
         }
+    });
+}
+
+int moe_sorting_mx_quant(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aiter_tensor_t* hidden_states,
+                         aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_weights,
+                         aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids, aiter_tensor_t* moe_buf,
+                         aiter_tensor_t* a_out, aiter_tensor_t* a_scale, int num_experts, int unit_size,
+                         aiter_stream_t stream) {
+    using namespace aiter_amd;
+    return safe_call([&] {
+        check_tensor(topk_ids, "topk_ids", 2);
+        check_tensor(hidden_states, "hidden_states", 2);
+        check_tensor(a_out, "a_out", 2);
+        check_tensor(a_scale, "a_scale");
+        DeviceGuard g(topk_ids->device_id);
+        hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+        SortQuantParams q{};
+        q.s = sort_params(topk_ids, topk_weights, sorted_token_ids, sorted_weights, sorted_expert_ids, num_valid_ids,
+                          num_experts, unit_size, nullptr, nullptr);
+        const int M = q.s.M;
+        const int64_t n = (int64_t)M * q.s.topk;
+        AA_CHECK(n <= kSQMaxEntries, "moe_sorting_mx_quant: at most ", kSQMaxEntries, " routed entries, got ", n);
+        AA_CHECK(hidden_states->dtype == AITER_DTYPE_bf16, "hidden_states must be bf16");
+        const int64_t K = cols_2d(hidden_states);
+        AA_CHECK(hidden_states->shape[0] == M, "hidden_states must have ", M, " rows");
+        AA_CHECK(K > 0 && K % 32 == 0, "hidden_states columns must be a positive multiple of 32");
+        AA_CHECK(hidden_states->strides[1] == 1 && hidden_states->strides[0] % 8 == 0 &&
+                     ((uintptr_t)hidden_states->ptr & 15) == 0,
+                 "hidden_states rows must be contiguous and 16-byte aligned");
+        AA_CHECK(is_byte_type(a_out->dtype) && a_out->shape[0] == M && a_out->shape[1] == K / 2 &&
+                     a_out->strides[1] == 1 && a_out->strides[0] % 16 == 0 && ((uintptr_t)a_out->ptr & 15) == 0,
+                 "a_out must be fp4x2 [", M, ", ", K / 2, "] with 16-byte aligned rows");
+        const int scale_n = (int)(K / 32), scale_n_pad = (scale_n + 7) / 8 * 8;
+        const int64_t sorted_rows = ((int64_t)q.s.max_padded + 31) / 32 * 32;
+        AA_CHECK(is_byte_type(a_scale->dtype) && (int64_t)a_scale->numel >= sorted_rows * scale_n_pad &&
+                     ((uintptr_t)a_scale->ptr & 15) == 0,
+                 "a_scale needs [pad32(len(sorted_token_ids)), ", scale_n_pad, "] bytes, 16-byte aligned");
+        const int64_t lds = (int64_t)M * scale_n_pad;
+        AA_CHECK(lds <= 32768, "moe_sorting_mx_quant: tokens * pad8(K / 32) must be at most 32768");
+        q.x = static_cast<const uint16_t*>(hidden_states->ptr);
+        q.x_stride = hidden_states->strides[0];
+        q.q = static_cast<uint8_t*>(a_out->ptr);
+        q.q_stride = a_out->strides[0];
+        q.q_scale = static_cast<uint8_t*>(a_scale->ptr);
+        q.scale_n = scale_n;
+        q.scale_n_pad = scale_n_pad;
+        if (moe_buf && moe_buf->numel > 0) {
+            AA_CHECK(((uintptr_t)moe_buf->ptr & 15) == 0, "moe_buf must be 16-byte aligned");
+            q.zero_buf = static_cast<uint8_t*>(moe_buf->ptr);
+            q.zero_bytes = (int64_t)moe_buf->numel * (int64_t)dtype_size(moe_buf->dtype);
+        }
+        if (M == 0) {
+            moe_sort_single<<<1, kThreads, 0, st>>>(q.s, q.zero_buf, q.zero_bytes);
+            AA_HIP(hipGetLastError());
+            return;
+        }
+        // every sorted position below num_valid_ids[0] is in one of these groups:
+        // the padded count is at most entries * unit_size (and the list length)
+        const int64_t bound = std::min<int64_t>(n * unit_size, q.s.max_padded);
+        const unsigned groups = (unsigned)std::max<int64_t>(1, (bound + 31) / 32);
+        moe_sort_quant_small<<<groups, 256, (size_t)lds, st>>>(q);
+        AA_HIP(hipGetLastError());
     });
 }
 

@@ -11,6 +11,10 @@ Mirrors the reference's entry points with their arguments and return values:
   ck_moe_stage1 / ck_moe_stage2       aiter/ops/moe_op.py:350-394
   ck_moe_stage1_fuse_quant            the stage-1 call of a fuse_quant == "fp4"
                                       configuration, aiter/fused_moe.py:3125-3171
+  moe_sorting_mx_quant                moe_sorting + the stage-1 quant in one
+                                      launch for decode-sized routing (the
+                                      fusion of aiter/ops/flydsl/kernels/
+                                      moe_fused_route_quant_scatter.py)
   fused_moe                           aiter/fused_moe.py:454-558 (the
                                       per_1x32 path of fused_moe_2stages,
                                       aiter/fused_moe.py:2892-3276)
@@ -96,6 +100,62 @@ def moe_sorting(topk_ids, topk_weights, num_experts, model_dim, moebuf_dtype, bl
                     num_valid_ids, moe_buf, num_experts, int(block_size), expert_mask, num_local_tokens,
                     dispatch_policy)
     return sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf
+
+
+SORT_QUANT_MAX_ENTRIES = 64
+
+
+def moe_sorting_mx_quant_fwd(topk_ids, topk_weights, hidden_states, sorted_token_ids, sorted_weights,
+                             sorted_expert_ids, num_valid_ids, moe_buf, a_out, a_scale, num_experts: int,
+                             unit_size: int) -> None:
+    """C entry: the routing sort and the stage-1 MXFP4 activation quant in one
+    launch (decode-sized routing; the fusion of
+    aiter/ops/flydsl/kernels/moe_fused_route_quant_scatter.py)."""
+    call("moe_sorting_mx_quant", topk_ids, topk_weights, hidden_states, sorted_token_ids, sorted_weights,
+         sorted_expert_ids, num_valid_ids, moe_buf, _u8(a_out), _u8(a_scale), int(num_experts), int(unit_size))
+
+
+def can_sort_quant(hidden_states, topk_ids, expert_mask=None, num_local_tokens=None, dispatch_policy=0) -> bool:
+    """Whether moe_sorting_mx_quant takes this call: at most
+    SORT_QUANT_MAX_ENTRIES routed entries, bf16 rows, no expert mask or
+    device token count."""
+    M, topk = topk_ids.shape
+    K = hidden_states.shape[-1]
+    return (expert_mask is None and num_local_tokens is None and dispatch_policy == 0 and
+            M * topk <= SORT_QUANT_MAX_ENTRIES and hidden_states.dtype == dtypes.bf16 and hidden_states.dim() == 2 and
+            K % 32 == 0 and M * ((K // 32 + 7) // 8 * 8) <= 32768)
+
+
+def moe_sorting_mx_quant(topk_ids, topk_weights, hidden_states, num_experts, block_size=BLOCK_SIZE_M,
+                         accumulate=True):
+    """-> (sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf,
+    a1, a1_scale): moe_sorting followed by fused_dynamic_mx_quant_moe_sort of
+    ``hidden_states`` (fp4x2, sorted weights given) in one launch.  Sorted
+    positions past num_valid_ids[0] (beyond its 32-row group) stay unwritten.
+    Raises unless can_sort_quant holds."""
+    if not can_sort_quant(hidden_states, topk_ids):
+        raise ValueError("moe_sorting_mx_quant: needs at most %d routed entries, bf16 [M, K] rows with K %% 32 == 0 "
+                         "and M * pad8(K / 32) <= 32768" % SORT_QUANT_MAX_ENTRIES)
+    device = topk_ids.device
+    M, topk = topk_ids.shape
+    if topk_ids.dtype != torch.int32:
+        topk_ids = topk_ids.to(torch.int32)
+    if topk_weights.dtype != torch.float32:
+        topk_weights = topk_weights.float()
+    model_dim = hidden_states.shape[-1]
+    max_num_tokens_padded = int(topk_ids.numel() + num_experts * block_size - topk)
+    max_num_m_blocks = int((max_num_tokens_padded + block_size - 1) // block_size)
+    sorted_ids = torch.empty(max_num_tokens_padded, dtype=torch.int32, device=device)
+    sorted_weights = torch.empty(max_num_tokens_padded, dtype=torch.float32, device=device)
+    sorted_expert_ids = torch.empty(max_num_m_blocks, dtype=torch.int32, device=device)
+    num_valid_ids = torch.empty(2, dtype=torch.int32, device=device)
+    moe_buf = torch.empty((M, model_dim) if accumulate else (0, 0), dtype=dtypes.bf16, device=device)
+    a1 = torch.empty((M, model_dim // 2), dtype=dtypes.fp4x2, device=device)
+    a1_scale = _sorted_scale(sorted_ids, model_dim, device)
+    moe_sorting_mx_quant_fwd(topk_ids.contiguous(), topk_weights.contiguous(), hidden_states.contiguous(), sorted_ids,
+                             sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf, a1, a1_scale, num_experts,
+                             int(block_size))
+    return sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf, a1, a1_scale
 
 
 # ------------------------------------------------------------- sorted quant
@@ -260,10 +320,11 @@ def get_inter_dim(w1_shape, w2_shape):
 def fused_moe_2stages(hidden_states, w1, w2, topk, sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids,
                       moe_out, block_size_M, activation=ActivationType.Silu, quant_type=QuantType.per_1x32,
                       doweight_stage1=False, q_dtype_a=dtypes.fp4x2, w1_scale=None, w2_scale=None,
-                      num_local_tokens=None, expert_mask=None):
+                      num_local_tokens=None, expert_mask=None, a1=None, a1_scale=None):
     """The per_1x32 two-stage flow of aiter/fused_moe.py:2892-3276: quant +
     sort of the tokens, stage 1, quant + sort of the stage-1 output, stage 2
-    accumulating into ``moe_out``."""
+    accumulating into ``moe_out``.  ``a1`` / ``a1_scale``: the tokens already
+    quantised with their scales in sorted order (moe_sorting_mx_quant)."""
     token_num = hidden_states.shape[0]
     E, model_dim, inter_dim = get_inter_dim(w1.shape, w2.shape)
     # per-pair rows miss the pairs routed to masked experts or past
@@ -271,9 +332,10 @@ def fused_moe_2stages(hidden_states, w1, w2, topk, sorted_ids, sorted_weights, s
     reduce = expert_mask is None and num_local_tokens is None and _use_reduce(token_num, topk)
     if moe_out.numel() == 0:
         moe_out = torch.empty((token_num, model_dim), dtype=dtypes.bf16, device=hidden_states.device)
-    a1, a1_scale = fused_dynamic_mx_quant_moe_sort(hidden_states, sorted_ids, num_valid_ids, token_num, topk,
-                                                   block_size_M, q_dtype_a, num_rows=num_local_tokens,
-                                                   sorted_weights=sorted_weights)
+    if a1 is None:
+        a1, a1_scale = fused_dynamic_mx_quant_moe_sort(hidden_states, sorted_ids, num_valid_ids, token_num, topk,
+                                                       block_size_M, q_dtype_a, num_rows=num_local_tokens,
+                                                       sorted_weights=sorted_weights)
     if q_dtype_a == dtypes.fp4x2 and inter_dim % 256 == 0 and expert_mask is None and num_local_tokens is None:
         # fuse_quant "fp4": stage 1 writes its output already quantised (one
         # launch and one pass over the stage-1 output less)
@@ -346,9 +408,15 @@ def fused_moe(hidden_states, w1, w2, topk_weight, topk_ids, expert_mask=None, ac
     bm = block_size_M if block_size_M and block_size_M > 0 else get_block_size_M(token_num, topk, global_E,
                                                                                  inter_dim)
     accumulate = not (expert_mask is None and num_local_tokens is None and _use_reduce(token_num, topk))
-    sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf = moe_sorting(
-        topk_ids, topk_weight, global_E, model_dim, dtype, bm, expert_mask, num_local_tokens,
-        moe_sorting_dispatch_policy, accumulate=accumulate)
+    a1 = a1_scale = None
+    if can_sort_quant(hidden_states, topk_ids, expert_mask, num_local_tokens, moe_sorting_dispatch_policy):
+        # decode: the sort and the token quant in one launch
+        sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf, a1, a1_scale = moe_sorting_mx_quant(
+            topk_ids, topk_weight, hidden_states, global_E, bm, accumulate=accumulate)
+    else:
+        sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf = moe_sorting(
+            topk_ids, topk_weight, global_E, model_dim, dtype, bm, expert_mask, num_local_tokens,
+            moe_sorting_dispatch_policy, accumulate=accumulate)
     return fused_moe_2stages(hidden_states, w1, w2, topk, sorted_ids, sorted_weights, sorted_expert_ids,
                              num_valid_ids, moe_buf, bm, activation, quant_type, doweight_stage1, dtypes.fp4x2,
-                             w1_scale, w2_scale, num_local_tokens, expert_mask)
+                             w1_scale, w2_scale, num_local_tokens, expert_mask, a1=a1, a1_scale=a1_scale)

@@ -559,8 +559,14 @@ def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter
     s1 = lambda: FM.ck_moe_stage1_fuse_quant(a1, w1, sids, seids, nv, m, topk, bm, w1s, a1s, None, sw,
                                              int(FM.ActivationType.Silu))
     a2q, a2s = s1()
-    res = {"sort_us": time_graph(sort, 10, 2), "quant1_us": time_graph(q1, 10, 2), "stage1_us": time_graph(s1, 10, 2),
-           "quant2_us": 0.0}
+    if FM.can_sort_quant(x, ti):
+        # decode: fused_moe sorts and quantises the tokens in one launch
+        sq = lambda: FM.moe_sorting_mx_quant(ti, tw, x, E, bm, accumulate=not reduce)
+        sq()
+        res = {"sort_us": time_graph(sq, 10, 2), "quant1_us": 0.0, "sort_quant_fused": True}
+    else:
+        res = {"sort_us": time_graph(sort, 10, 2), "quant1_us": time_graph(q1, 10, 2), "sort_quant_fused": False}
+    res.update({"stage1_us": time_graph(s1, 10, 2), "quant2_us": 0.0})
     if reduce:
         per_pair = torch.empty((m, topk, dim), dtype=torch.bfloat16, device=x.device)
         s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, per_pair, topk, "", w2s, a2s, bm, sw, qt)
@@ -572,7 +578,7 @@ def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter
         s2 = lambda: FM.ck_moe_stage2(a2q, w1, w2, sids, seids, nv, moe_buf, topk, "", w2s, a2s, bm, sw, qt)
         res["stage2_us"] = time_graph(s2, 10, 2)
         res["moe_sum_us"] = 0.0
-    res = {k: round(v * 1e6, 1) for k, v in res.items()}
+    res = {k: (round(v * 1e6, 1) if isinstance(v, float) else v) for k, v in res.items()}
     res["stages_us"] = round(res["stage1_us"] + res["stage2_us"] + res["moe_sum_us"], 1)
     if m in REF_MOE_STAGES:
         r1, r2 = REF_MOE_STAGES[m]

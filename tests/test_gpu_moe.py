@@ -115,6 +115,68 @@ def test_quant_sort_exact(cuda, fp8, m, topk, stage):
     np.testing.assert_array_equal(sc2.view(torch.uint8).cpu().numpy()[:n_valid], rsc[:n_valid])
 
 
+# ------------------------------------------------- sort + quant, one launch
+SQ_CASES = [(1, 257, 9, 32, 7168), (3, 257, 9, 64, 7168), (7, 257, 9, 32, 7168), (2, 257, 9, 128, 7168),
+            (8, 16, 8, 32, 256), (4, 8, 4, 16, 320), (64, 4, 1, 32, 64), (16, 16, 4, 64, 512)]
+
+
+@pytest.mark.parametrize("m,e,topk,bs,k", SQ_CASES)
+@pytest.mark.parametrize("edge", [False, True])
+def test_sort_quant_one_launch(cuda, m, e, topk, bs, k, edge):
+    """moe_sorting_mx_quant against the oracle sort + stage-1 sorted quant:
+    ids / weights below num_valid_ids[0], the whole block table, the counts,
+    every token row's MXFP4 codes and the sorted scale groups below
+    num_valid_ids[0], bit-exact; moe_buf zeroed.  edge: one entry routed to
+    an expert id past the last (dropped by the sort) and one zero routing
+    weight (scale byte 0 at its position only)."""
+    import aiter_amd
+
+    announce(f"sort_quant m={m} e={e} topk={topk} bs={bs} k={k} edge={edge}")
+    rng = np.random.default_rng(1000 * m + 7 * e + topk + bs + edge)
+    ids, w = _routing(m, e, topk, rng)
+    if edge:
+        ids[0, topk - 1] = e               # dropped entry
+        w[m - 1, 0] = 0.0                  # zero routing weight
+    x = to_bf16_f32(rng.standard_normal((m, k)).astype(np.float32) * 3)
+    x[0, :32] = 0.0                        # an all-zero block (running max 1e-10)
+    ids_d, w_d, x_d = _dev(ids, cuda), _dev(w, cuda), _bf16_dev(x, cuda)
+    fill = torch.full((m, k), 7.0, dtype=torch.bfloat16, device=cuda)   # moe_buf likely reuses this block
+    del fill
+    s, sw, se, nv, buf, q, sc = aiter_amd.moe_sorting_mx_quant(ids_d, w_d, x_d, e, bs, accumulate=True)
+    torch.cuda.synchronize()
+    rs, rsw, rse, rnv = MO.moe_sorting_ref(ids, w, e, bs)
+    assert nv.cpu().numpy().tolist() == rnv.tolist()
+    total = int(rnv[0])
+    np.testing.assert_array_equal(s.cpu().numpy()[:total], rs[:total])
+    np.testing.assert_array_equal(sw.cpu().numpy()[:total], rsw[:total])
+    np.testing.assert_array_equal(se.cpu().numpy(), rse)
+    assert buf.shape == (m, k) and torch.count_nonzero(buf).item() == 0
+    # every token row quantised (no zero-weight rule on the rows)
+    qr, sr = O.quant_mxfp4(x, O.ROUND_UP, amax_floor=1e-10)
+    np.testing.assert_array_equal(q.view(torch.uint8).cpu().numpy(), qr)
+    rsc = MO.sort_scale_ref(sr, rs, total, m, 1)
+    zero = np.flatnonzero((np.arange(len(rsw)) < total) & (rsw == 0) & ((rs & 0xFFFFFF) < m))
+    snp = rsc.shape[1]
+    for xpos in zero:                      # scale byte 0 at a zero-weight position
+        for y in range(snp):
+            rsc.reshape(-1)[(xpos // 32 * snp) * 32 + (y // 8) * 256 + (y % 4) * 64 + (xpos % 16) * 4 +
+                            (y % 8) // 4 * 2 + (xpos % 32) // 16] = 0
+    if edge:
+        assert len(zero) == 1
+    rows = (total + 31) // 32 * 32
+    np.testing.assert_array_equal(sc.view(torch.uint8).cpu().numpy()[:rows], rsc[:rows])
+
+
+def test_sort_quant_refuses_large_routing(cuda):
+    import aiter_amd
+
+    ids = torch.zeros((8, 9), dtype=torch.int32, device=cuda)
+    w = torch.ones((8, 9), dtype=torch.float32, device=cuda)
+    x = torch.zeros((8, 256), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(ValueError):
+        aiter_amd.moe_sorting_mx_quant(ids, w, x, 16, 32)
+
+
 # -------------------------------------------------------------------- stages
 def _weights(e, n, k, rng):
     """random fp4 bytes [e, n, k/2] and plain scales [e*n, k/32] near 2^-6"""
@@ -195,11 +257,37 @@ def test_stage1_split_k(cuda, m, splitk, fp8):
     _stage1_check(cuda, m, 16, 9, 7168, 256, 32, fp8, 0, True, splitk, 900 + m + splitk)
 
 
+def test_stage1_split_k_after_fused_gemm(cuda):
+    """A fused GEMM with plain scales stages them in library workspace of the
+    same stream; the split-K tile counters have a workspace of their own, so a
+    split stage 1 right after it still finds them at zero."""
+    import aiter_amd
+
+    announce("moe stage1 split-K after fused_gemm_afp4wfp4_mul_add")
+    g = torch.Generator(device=cuda).manual_seed(5)
+    m, n, k = 16, 256, 512
+    x = torch.randint(0, 256, (m, k // 2), dtype=torch.uint8, device=cuda, generator=g)
+    w = torch.randint(0, 256, (n, k // 2), dtype=torch.uint8, device=cuda, generator=g)
+    xs = torch.randint(118, 124, (m, k // 32), dtype=torch.uint8, device=cuda, generator=g)
+    wsc = torch.randint(118, 124, (n, k // 32), dtype=torch.uint8, device=cuda, generator=g)
+    aiter_amd.fused_gemm_afp4wfp4_mul_add(x, w, xs, wsc, 2.0, 1.0)
+    _stage1_check(cuda, 1, 16, 9, 7168, 256, 32, False, 0, True, 0, 940)
+
+
+def test_stage1_split_k_back_to_back(cuda):
+    """Split-K stage-1 calls in a row on one stream, of different sizes: the
+    split that finishes a tile last sums it, so each call must find its tile
+    counters back at zero (a stale counter leaves rows unwritten: NaN)."""
+    for i, (m, splitk) in enumerate([(1, 0), (4, 0), (1, 0), (4, 5), (2, 0)]):
+        announce(f"moe stage1 split-K back to back #{i} m={m} splitk={splitk}")
+        _stage1_check(cuda, m, 16, 9, 7168, 256, 32, False, 0, True, splitk, 950 + i)
+
+
 # (tokens, model_dim, inter_dim, block_m, splitk, MXFP8 input, activation,
 # doweight_stage1, zero routing weights): one-pass tiles (model_dim 512 /
-# 1024) and split K (model_dim 7168: 10 and 5 splits) through the reduce
-# kernel; Silu and Gelu; inter_dim 256 and 512 (one and two 128-column tiles
-# per 256-column scale row)
+# 1024) and split K (model_dim 7168: 10 and 5 splits, summed by the split
+# that finishes each tile last); Silu and Gelu; inter_dim 256 and 512 (one and
+# two 128-column tiles per 256-column scale row)
 FQ_CASES = [(5, 512, 256, 32, 1, False, 0, False, False), (200, 512, 256, 64, 1, True, 1, True, False),
             (300, 1024, 512, 128, 1, False, 0, False, False), (40, 512, 256, 32, 1, False, 0, True, True),
             (1, 7168, 256, 32, 0, False, 0, True, False), (4, 7168, 512, 32, 5, False, 1, False, True)]
