@@ -224,15 +224,25 @@ void run_stage(const StageArgs& s, hipStream_t st) {
     if (used == 0) return;
     p.tiles_m = (int)used;
     AA_CHECK((int64_t)tiles_n * used < ((int64_t)1 << 31), "grid too large");
-    // stage-1 split-K when the tiles cannot fill the chip (decode): about 256
-    // workgroups, at least 2 K stages each
+    // stage-1 split-K while the tiles leave the CUs short of weight loads in
+    // flight (decode and small batches; at least 2 K stages per split).  A
+    // workgroup keeps one K stage of B ahead, so a CU with one tile streams
+    // its weights far below its share of HBM.  Measured at the DeepSeek shape
+    // (model_dim 7168, 257 experts, topk 9; 256 CUs): 1 token (20 tiles) is
+    // fastest with ~120 workgroups (6 splits: 9.6 us, 10 splits 10.1, none
+    // 14.9); 16-64 tokens (300-550 tiles) with 2 splits (16 tokens 53.6 ->
+    // 42.7 us, 32 tokens 89.3 -> 74.5, 64 tokens 94.6 -> 90.1); from 128
+    // tokens (590 tiles) one pass is faster.
     const int nst = (int)(K / 256);
     const int64_t tiles = (int64_t)tiles_n * used;
     int splits = 1;
     if (s.stage == 1) {
         // splitk: 1 = one pass over K (the reference's default), > 1 = that
         // many K slices, 0 = chosen here
-        int want = s.splitk != 0 ? s.splitk : (tiles < 128 ? (int)std::max<int64_t>(1, 256 / tiles) : 1);
+        const int64_t cus = device_cu_count(s.out->device_id);
+        int want = s.splitk;
+        if (want == 0)
+            want = tiles < cus / 2 ? (int)std::max<int64_t>(2, cus / 2 / tiles) : (tiles * 4 < cus * 9 ? 2 : 1);
         want = std::min(want, std::max(1, nst / 2));
         if (want > 1) {
             const int per = (nst + want - 1) / want;

@@ -245,12 +245,13 @@ def test_stage1(cuda, bs, fp8, act, doweight, m, splitk):
     _stage1_check(cuda, m, 8, 3, 512, 256, bs, fp8, act, doweight, splitk, 100 + m + bs)
 
 
-# (tokens, splitk): model_dim 7168 = 28 K stages, 16 experts, topk 9.
-# splitk 0 at 1 token: 10 row blocks x 2 N tiles = 20 tiles -> 12 wanted ->
-# 3 stages per split -> 10 splits, the last with one stage.  splitk 0 at 4
-# tokens: 18 row blocks -> 36 tiles -> 7 wanted -> 4 stages x 7 splits.
-# splitk 5: 6 stages x 5 splits, the last with 4.  splitk 1: one pass.
-@pytest.mark.parametrize("m,splitk", [(1, 0), (4, 0), (4, 5), (1, 1)])
+# (tokens, splitk): model_dim 7168 = 28 K stages, 16 experts, topk 9 (256
+# CUs).  splitk 0 at 1 token: 10 row blocks x 2 N tiles = 20 tiles -> 6
+# wanted -> 5 stages x 6 splits, the last with 3.  splitk 0 at 4 tokens: 18
+# row blocks -> 36 tiles -> 3 wanted -> 10 stages x 3 splits, the last with 8.
+# splitk 5: 6 stages x 5 splits, the last with 4.  splitk 10: 3 stages x 10
+# splits, the last with one.  splitk 1: one pass.
+@pytest.mark.parametrize("m,splitk", [(1, 0), (4, 0), (4, 5), (1, 10), (1, 1)])
 @pytest.mark.parametrize("fp8", [False, True])
 def test_stage1_split_k(cuda, m, splitk, fp8):
     announce(f"moe stage1 split-K m={m} splitk={splitk} fp8={fp8} dim=7168")
