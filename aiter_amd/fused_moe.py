@@ -298,12 +298,13 @@ def moe_sum(input: torch.Tensor, output: torch.Tensor) -> None:
 @functools.lru_cache(maxsize=2048)
 def get_block_size_M(token: int, topk: int, expert: int, inter_dim: int) -> int:
     """Row block of the sorted list, from the average routed rows per expert:
-    32 up to 24 rows, 64 up to 512, 128 above (measured at the DeepSeek shape,
-    257 experts x topk 9: 64 is fastest from ~1000 to 8192 tokens, 32 below);
-    the reference picks from its tuned table with the same candidates
-    (aiter/fused_moe.py:1178-1193)."""
+    32 up to 16 rows, 64 up to 512, 128 above (measured end to end at the
+    DeepSeek shape, 257 experts x topk 9: 32 is fastest up to 256 tokens,
+    64 from 512 tokens (512: 232.5 against 238.3 us) to 8192, 128 slower
+    everywhere there); the reference picks from its tuned table with the
+    same candidates (aiter/fused_moe.py:1178-1193)."""
     per_expert = token * topk / max(expert, 1)
-    if per_expert <= 24:
+    if per_expert <= 16:
         return 32
     if per_expert <= 512:
         return 64
