@@ -269,22 +269,22 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(uint8_t* dst, int64_t by
 // ---- decode: routing sort and the stage-1 activation quant in one launch ----
 // (the fusion of aiter/ops/flydsl/kernels/moe_fused_route_quant_scatter.py,
 // route map + MX quant + scale scatter, for this library's sorted list.)
-// For at most kSQMaxEntries routed entries (one wave holds them all), every
-// workgroup ranks the entries itself with ballots over the distinct experts
-// (no cross-workgroup step), quantises all token rows (their loads are
-// issued before the ranking, so the kernel has one dependent global load
-// level), and writes sorted row group blockIdx.x (32 positions): sorted ids
-// and weights, and the shuffled 256-byte scale blocks of the group's rows.
-// Workgroup 0 writes the block -> expert table and num_valid_ids; the token
-// rows' MXFP4 codes and the moe_buf clear are split over the workgroups.
-// Outputs equal moe_sorting_fwd followed by fused_dynamic_mx_quant_moe_sort
-// (stage 1, RoundUp e8m0 from 1e-10, sorted weights given) at positions below
-// num_valid_ids[0] (plus the rest of its last 32-row group); later positions
-// of sorted_ids / sorted_weights and later scale groups are left unwritten
-// (no reader goes past num_valid_ids[0]).  Every token row is quantised,
-// also one whose entries were all dropped, and a zero routing weight gives
-// scale byte 0 at its position with the token row quantised as usual.
-constexpr int kSQMaxEntries = 64;
+// For at most kSQMaxEntries routed entries (one per thread of a workgroup),
+// every workgroup ranks all entries itself (no cross-workgroup step) and
+// then handles sorted row group blockIdx.x (32 positions): its sorted ids and
+// weights, the MXFP4 quant of the tokens its rows name, and the shuffled
+// 256-byte scale blocks of its rows.  A token's MXFP4 codes are written by
+// the workgroup holding the token's first sorted position (or, where every
+// workgroup quantises every token, split over the workgroups); workgroup 0
+// writes the block -> expert table and num_valid_ids; the moe_buf clear is
+// split over the workgroups.  Outputs equal moe_sorting_fwd followed by
+// fused_dynamic_mx_quant_moe_sort (stage 1, RoundUp e8m0 from 1e-10, sorted
+// weights given) at positions below num_valid_ids[0] (plus the rest of its
+// last 32-row group); later positions of sorted_ids / sorted_weights and
+// later scale groups are left unwritten, as is the row of a token whose
+// entries were all dropped (no reader goes there).  A zero routing weight
+// gives scale byte 0 at its position with the token row quantised as usual.
+constexpr int kSQMaxEntries = 256;
 
 struct SortQuantParams {
     SortParams s;               // no expert mask, no device token count
@@ -298,7 +298,28 @@ struct SortQuantParams {
     int64_t zero_bytes;
 };
 
-__global__ __launch_bounds__(256) void moe_sort_quant_small(SortQuantParams p) {
+// the MXFP4 block of 32 bf16 values given as 4 x 16 loaded bytes
+AA_DEV uint32_t sq_quant_block(const i32x4_t (&raw)[4], i32x4_t& o) {
+    float v[32];
+    uint32_t pr[16];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t d = (uint32_t)raw[q][j];
+            pr[4 * q + j] = d;
+            v[8 * q + 2 * j] = __builtin_bit_cast(float, d << 16);
+            v[8 * q + 2 * j + 1] = __builtin_bit_cast(float, d & 0xffff0000u);
+        }
+    return aiter_amd::mx::quant32_fp4<uint16_t, aiter_amd::mx::kRoundUp>(v, pr, 1e-10f, 1.0f / 6.0f, 0.25f, 0u, 2u, o);
+}
+
+// Up to 64 entries (one wave holds them all): wave 0 ranks the entries with a
+// ballot per distinct expert (no histogram, scan or extra barrier) while the
+// other waves quantise every token row, whose loads are issued first.
+constexpr int kSQWaveEntries = 64;
+
+__global__ __launch_bounds__(256) void moe_sort_quant_wave(SortQuantParams p) {
     extern __shared__ uint8_t tok_sc[];   // [M][scale_n_pad] e8m0 bytes of the token rows
     __shared__ int row_id[32];            // sorted entry of each row of the group (padding: pad id)
     __shared__ float row_w[32];
@@ -428,6 +449,232 @@ __global__ __launch_bounds__(256) void moe_sort_quant_small(SortQuantParams p) {
             const int t = id & 0xffffff, slot = (int)((unsigned)id >> 24);
             const bool valid = 32 * grp + xr < total && t < s.M && slot < s.topk && row_w[xr] != 0.0f;
             const uint32_t byte = valid ? tok_sc[t * p.scale_n_pad + 8 * y8 + yy] : 0u;
+            d[b >> 2] |= byte << (8 * (b & 3));
+        }
+        *reinterpret_cast<i32x4_t*>(p.q_scale + (int64_t)grp * 32 * p.scale_n_pad + y8 * 256 + w16 * 16) =
+            i32x4_t{(int)d[0], (int)d[1], (int)d[2], (int)d[3]};
+    }
+}
+
+// PRE: every workgroup loads and quantises all token rows, the loads issued
+// before the ranking (tokens * K/32 <= 1024: at most 4 blocks per thread);
+// otherwise a workgroup quantises the tokens of its rows after the ranking.
+template <bool PRE>
+__global__ __launch_bounds__(256) void moe_sort_quant_small(SortQuantParams p) {
+    // e8m0 bytes of the quantised tokens: [M] (PRE) or [32] (the group's tokens) x scale_n_pad
+    extern __shared__ uint8_t tok_sc[];
+    __shared__ __attribute__((aligned(16))) uint8_t wcnt[4][kMaxE];   // entries per (wave, expert)
+    __shared__ int off[kMaxE];                                        // padded start of each expert
+    __shared__ int scan_buf[4];
+    __shared__ int first_pos[kSQMaxEntries];                          // smallest sorted position of each token
+    __shared__ int row_id[32];                                        // entry of each row of the group (padding: pad id)
+    __shared__ float row_w[32];
+    __shared__ int row_tix[32];                                       // index of the row's token in gtok
+    __shared__ int gtok[32];                                          // distinct tokens of the group's rows
+    __shared__ int s_ntok;
+    const SortParams& s = p.s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = s.M * s.topk;
+    const int grp = blockIdx.x, ngrp = gridDim.x;
+    const int pad_id = (s.topk << 24) | s.M;
+
+    // entry `tid` (expert -1: none or dropped)
+    const int e = expert_of(s, tid, n);
+    const float w = tid < n ? s.topk_w[(int64_t)(tid / s.topk) * s.w_stride + tid % s.topk] : 0.0f;
+    // PRE: all token rows, item (token, block y) = tid + 256 k
+    i32x4_t raw[PRE ? 4 : 1][4];
+    const int pre_items = PRE ? s.M * p.scale_n : 0;
+    if constexpr (PRE) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int it = 256 * k + tid;
+            if (it < pre_items) {
+                const int t = it / p.scale_n, y = it - t * p.scale_n;
+                const i32x4_t* src = reinterpret_cast<const i32x4_t*>(p.x + t * p.x_stride + (int64_t)y * 32);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) raw[k][q] = src[q];
+            }
+        }
+    }
+    // this workgroup's share of the moe_buf clear
+    if (p.zero_bytes > 0) {
+        const int64_t units = p.zero_bytes / 16, per = (units + ngrp - 1) / ngrp;
+        for (int64_t u = grp * per + tid; u < min(units, (int64_t)(grp + 1) * per); u += 256)
+            reinterpret_cast<i32x4_t*>(p.zero_buf)[u] = i32x4_t{0, 0, 0, 0};
+        if (grp == 0)
+            for (int64_t b = units * 16 + tid; b < p.zero_bytes; b += 256) p.zero_buf[b] = 0;
+    }
+    static_assert(sizeof(wcnt) == 256 * 16, "one 16-byte clear per thread");
+    reinterpret_cast<i32x4_t*>(&wcnt[0][0])[tid] = i32x4_t{0, 0, 0, 0};
+    if (tid < s.M) first_pos[tid] = 0x7fffffff;
+    if (tid < 32) {
+        row_id[tid] = pad_id;
+        row_w[tid] = 0.0f;
+        row_tix[tid] = 0;
+    }
+    __syncthreads();
+    // in-wave rank among equal experts and per-wave counts: one ballot per
+    // distinct expert of the wave
+    int rank = 0;
+    {
+        uint64_t act = __ballot(e >= 0);
+        const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;
+        while (act) {
+            const int leader = __builtin_ctzll(act);
+            const int le = __builtin_amdgcn_readlane(e, leader);
+            const uint64_t m = __ballot(e == le);
+            if (e == le) rank = __popcll(m & below);
+            if (lane == leader) wcnt[wave][le] = (uint8_t)__popcll(m);
+            act &= ~m;
+        }
+    }
+    __syncthreads();
+    // padded count of experts 4 tid .. 4 tid + 3, exclusive scan over the
+    // workgroup -> each expert's padded start
+    int pc[4], sum = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int x = 4 * tid + k;
+        const int c = x < s.E ? wcnt[0][x] + wcnt[1][x] + wcnt[2][x] + wcnt[3][x] : 0;
+        pc[k] = (c + s.bs - 1) / s.bs * s.bs;
+        sum += pc[k];
+    }
+    int incl = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d);
+        if (lane >= d) incl += y;
+    }
+    if (lane == 63) scan_buf[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int v = 0; v < wave; ++v) base += scan_buf[v];
+    const int total = scan_buf[0] + scan_buf[1] + scan_buf[2] + scan_buf[3];
+    {
+        int o = base + incl - sum;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int x = 4 * tid + k;
+            if (x < s.E) off[x] = o;
+            // workgroup 0: the expert's row blocks
+            if (grp == 0 && x < s.E)
+                for (int b = o / s.bs; b < (o + pc[k]) / s.bs && b < s.max_blocks; ++b) s.sorted_eids[b] = x;
+            o += pc[k];
+        }
+    }
+    if (grp == 0) {
+        for (int b = total / s.bs + tid; b < s.max_blocks; b += 256) s.sorted_eids[b] = -1;
+        if (tid == 0) {
+            s.num_valid[0] = total;
+            s.num_valid[1] = s.M;
+        }
+    }
+    __syncthreads();
+    if (e >= 0) {
+        int pos = off[e] + rank;
+        for (int v = 0; v < wave; ++v) pos += wcnt[v][e];
+        atomicMin(&first_pos[tid / s.topk], pos);
+        if (pos >= 32 * grp && pos < 32 * grp + 32) {
+            const int t = tid / s.topk;
+            row_id[pos - 32 * grp] = ((tid - t * s.topk) << 24) | t;
+            row_w[pos - 32 * grp] = w;
+        }
+    }
+    if constexpr (PRE) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int it = 256 * k + tid;
+            if (it >= pre_items) continue;
+            const int t = it / p.scale_n, y = it - t * p.scale_n;
+            i32x4_t o;
+            tok_sc[t * p.scale_n_pad + y] = (uint8_t)sq_quant_block(raw[k], o);
+            if (it % ngrp == grp) *reinterpret_cast<i32x4_t*>(p.q + t * p.q_stride + (int64_t)y * 16) = o;
+        }
+        for (int i = tid; i < s.M * (p.scale_n_pad - p.scale_n); i += 256) {
+            const int t = i / (p.scale_n_pad - p.scale_n);
+            tok_sc[t * p.scale_n_pad + p.scale_n + i % (p.scale_n_pad - p.scale_n)] = 0;
+        }
+    }
+    __syncthreads();
+    if (32 * grp >= total) return;
+    if (tid < 32 && 32 * grp + tid < s.max_padded) {
+        s.sorted_ids[32 * grp + tid] = row_id[tid];
+        s.sorted_w[32 * grp + tid] = row_w[tid];
+    }
+    if constexpr (!PRE) {
+        // the group's distinct tokens (wave 0, lane = row): one ballot per
+        // distinct token numbers them in order of first appearance
+        if (wave == 0) {
+            int tok = -1;
+            if (lane < 32) {
+                const int id = row_id[lane];
+                const int t = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+                if (32 * grp + lane < total && t < s.M && slot < s.topk) tok = t;
+            }
+            uint64_t act = __ballot(tok >= 0);
+            int nt = 0;
+            while (act) {
+                const int leader = __builtin_ctzll(act);
+                const int lt = __builtin_amdgcn_readlane(tok, leader);
+                const uint64_t m = __ballot(tok == lt);
+                if (tok == lt) row_tix[lane] = nt;
+                if (lane == leader) gtok[nt] = lt;
+                ++nt;
+                act &= ~m;
+            }
+            if (lane == 0) s_ntok = nt;
+        }
+        __syncthreads();
+        // quantise the group's tokens: item (token index, block y), up to 4
+        // per thread with their loads in flight together; a token's codes
+        // come from the workgroup holding its first sorted position
+        const int ntok = s_ntok;
+        const int items = ntok * p.scale_n;
+        for (int b0 = 0; b0 < items; b0 += 4 * 256) {
+            i32x4_t rw[4][4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int it = b0 + 256 * k + tid;
+                if (it < items) {
+                    const int ti = it / p.scale_n, y = it - ti * p.scale_n;
+                    const i32x4_t* src =
+                        reinterpret_cast<const i32x4_t*>(p.x + gtok[ti] * p.x_stride + (int64_t)y * 32);
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) rw[k][q] = src[q];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int it = b0 + 256 * k + tid;
+                if (it >= items) continue;
+                const int ti = it / p.scale_n, y = it - ti * p.scale_n;
+                const int t = gtok[ti];
+                i32x4_t o;
+                tok_sc[ti * p.scale_n_pad + y] = (uint8_t)sq_quant_block(rw[k], o);
+                if (first_pos[t] / 32 == grp) *reinterpret_cast<i32x4_t*>(p.q + t * p.q_stride + (int64_t)y * 16) = o;
+            }
+        }
+        for (int i = tid; i < ntok * (p.scale_n_pad - p.scale_n); i += 256) {
+            const int ti = i / (p.scale_n_pad - p.scale_n);
+            tok_sc[ti * p.scale_n_pad + p.scale_n + i % (p.scale_n_pad - p.scale_n)] = 0;
+        }
+        __syncthreads();
+    }
+    // the group's scale blocks: 16-byte piece w16 of column octet y8 holds
+    // rows 4(w16 % 4) + (b >> 2) + 16(b & 1), columns 8 y8 + w16 / 4 + 4((b >> 1) & 1)
+    // for its bytes b (the mx_scale_shuffle_idx layout)
+    for (int c2 = tid; c2 < 2 * p.scale_n_pad; c2 += 256) {
+        const int y8 = c2 >> 4, w16 = c2 & 15;
+        uint32_t d[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int xr = 4 * (w16 & 3) + (b >> 2) + 16 * (b & 1);
+            const int yy = (w16 >> 2) + 4 * ((b >> 1) & 1);
+            const int id = row_id[xr];
+            const int t = id & 0xffffff, slot = (int)((unsigned)id >> 24);
+            const bool valid = 32 * grp + xr < total && t < s.M && slot < s.topk && row_w[xr] != 0.0f;
+            const int ti = PRE ? t : row_tix[xr];
+            const uint32_t byte = valid ? tok_sc[ti * p.scale_n_pad + 8 * y8 + yy] : 0u;
             d[b >> 2] |= byte << (8 * (b & 3));
         }
         *reinterpret_cast<i32x4_t*>(p.q_scale + (int64_t)grp * 32 * p.scale_n_pad + y8 * 256 + w16 * 16) =
@@ -568,8 +815,13 @@ int moe_sorting_mx_quant(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights,
         AA_CHECK(is_byte_type(a_scale->dtype) && (int64_t)a_scale->numel >= sorted_rows * scale_n_pad &&
                      ((uintptr_t)a_scale->ptr & 15) == 0,
                  "a_scale needs [pad32(len(sorted_token_ids)), ", scale_n_pad, "] bytes, 16-byte aligned");
-        const int64_t lds = (int64_t)M * scale_n_pad;
-        AA_CHECK(lds <= 32768, "moe_sorting_mx_quant: tokens * pad8(K / 32) must be at most 32768");
+        AA_CHECK(32 * (int64_t)scale_n_pad <= 65536, "moe_sorting_mx_quant: K must be at most 65536");
+        // up to 64 entries: one wave ranks them, every workgroup quantises
+        // all token rows; otherwise all token rows are loaded before the
+        // ranking when they are at most 4 32-element blocks per thread
+        const bool one_wave = n <= kSQWaveEntries && (int64_t)M * scale_n_pad <= 32768;
+        const bool pre = (int64_t)M * scale_n <= 1024;
+        const int64_t lds = (one_wave || pre ? M : 32) * (int64_t)scale_n_pad;
         q.x = static_cast<const uint16_t*>(hidden_states->ptr);
         q.x_stride = hidden_states->strides[0];
         q.q = static_cast<uint8_t*>(a_out->ptr);
@@ -591,7 +843,12 @@ int moe_sorting_mx_quant(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights,
         // the padded count is at most entries * unit_size (and the list length)
         const int64_t bound = std::min<int64_t>(n * unit_size, q.s.max_padded);
         const unsigned groups = (unsigned)std::max<int64_t>(1, (bound + 31) / 32);
-        moe_sort_quant_small<<<groups, 256, (size_t)lds, st>>>(q);
+        if (one_wave)
+            moe_sort_quant_wave<<<groups, 256, (size_t)lds, st>>>(q);
+        else if (pre)
+            moe_sort_quant_small<true><<<groups, 256, (size_t)lds, st>>>(q);
+        else
+            moe_sort_quant_small<false><<<groups, 256, (size_t)lds, st>>>(q);
         AA_HIP(hipGetLastError());
     });
 }

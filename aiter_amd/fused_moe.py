@@ -102,7 +102,7 @@ def moe_sorting(topk_ids, topk_weights, num_experts, model_dim, moebuf_dtype, bl
     return sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf
 
 
-SORT_QUANT_MAX_ENTRIES = 64
+SORT_QUANT_MAX_ENTRIES = 256
 
 
 def moe_sorting_mx_quant_fwd(topk_ids, topk_weights, hidden_states, sorted_token_ids, sorted_weights,
@@ -123,7 +123,7 @@ def can_sort_quant(hidden_states, topk_ids, expert_mask=None, num_local_tokens=N
     K = hidden_states.shape[-1]
     return (expert_mask is None and num_local_tokens is None and dispatch_policy == 0 and
             M * topk <= SORT_QUANT_MAX_ENTRIES and hidden_states.dtype == dtypes.bf16 and hidden_states.dim() == 2 and
-            K % 32 == 0 and M * ((K // 32 + 7) // 8 * 8) <= 32768)
+            K % 32 == 0 and K <= 65536)
 
 
 def moe_sorting_mx_quant(topk_ids, topk_weights, hidden_states, num_experts, block_size=BLOCK_SIZE_M,
@@ -131,11 +131,12 @@ def moe_sorting_mx_quant(topk_ids, topk_weights, hidden_states, num_experts, blo
     """-> (sorted_ids, sorted_weights, sorted_expert_ids, num_valid_ids, moe_buf,
     a1, a1_scale): moe_sorting followed by fused_dynamic_mx_quant_moe_sort of
     ``hidden_states`` (fp4x2, sorted weights given) in one launch.  Sorted
-    positions past num_valid_ids[0] (beyond its 32-row group) stay unwritten.
-    Raises unless can_sort_quant holds."""
+    positions past num_valid_ids[0] (beyond its 32-row group) and the rows of
+    tokens whose entries were all dropped stay unwritten.  Raises unless
+    can_sort_quant holds."""
     if not can_sort_quant(hidden_states, topk_ids):
         raise ValueError("moe_sorting_mx_quant: needs at most %d routed entries, bf16 [M, K] rows with K %% 32 == 0 "
-                         "and M * pad8(K / 32) <= 32768" % SORT_QUANT_MAX_ENTRIES)
+                         "and K <= 65536" % SORT_QUANT_MAX_ENTRIES)
     device = topk_ids.device
     M, topk = topk_ids.shape
     if topk_ids.dtype != torch.int32:

@@ -255,17 +255,17 @@ int moe_sorting_fwd(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aite
                     aiter_tensor_t* num_local_tokens, int dispatch_policy, aiter_stream_t stream);
 
 /* Routing sort + stage-1 activation quant in one launch, for decode-sized
- * routing (at most 64 entries M * topk; no expert mask, no device token
+ * routing (at most 256 entries M * topk; no expert mask, no device token
  * count): the fusion of route map, MX quant and scale scatter of
  * aiter/ops/flydsl/kernels/moe_fused_route_quant_scatter.py:1-50 for this
  * library's sorted list.  Same arguments and outputs as moe_sorting_fwd
  * (dispatch_policy 0) followed by fused_dynamic_mx_quant_moe_sort_hip(a_out,
  * a_scale, hidden_states, ..., sorted_weights) at stage 1: hidden_states bf16
- * [M, K], a_out fp4x2 [M, K/2] (every token row), a_scale u8
- * [pad32(len(sorted_token_ids)), pad8(K/32)] sorted and shuffled.  Positions
- * at or past num_valid_ids[0] (beyond the last 32-row group) are left
- * unwritten; a zero routing weight gives scale byte 0 at its position.
- * Needs M * pad8(K/32) <= 32768. */
+ * [M, K], a_out fp4x2 [M, K/2], a_scale u8 [pad32(len(sorted_token_ids)),
+ * pad8(K/32)] sorted and shuffled.  Positions at or past num_valid_ids[0]
+ * (beyond the last 32-row group) and the rows of tokens whose entries were
+ * all dropped are left unwritten; a zero routing weight gives scale byte 0
+ * at its position.  Needs K <= 65536. */
 int moe_sorting_mx_quant(aiter_tensor_t* topk_ids, aiter_tensor_t* topk_weights, aiter_tensor_t* hidden_states,
                          aiter_tensor_t* sorted_token_ids, aiter_tensor_t* sorted_weights,
                          aiter_tensor_t* sorted_expert_ids, aiter_tensor_t* num_valid_ids, aiter_tensor_t* moe_buf,
