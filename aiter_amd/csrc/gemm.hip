@@ -815,7 +815,9 @@ void mul_add_operand(const aiter_tensor_t* t, int64_t M, int64_t N, const void**
 
 void* lib_workspace(int dev, hipStream_t st, size_t bytes) { return workspace(dev, st, bytes); }
 int* lib_counters(int dev, hipStream_t st, size_t count) {
-    return reinterpret_cast<int*>(workspace(dev, st, count * sizeof(int), kCounterSlot));
+    // at least 64K counters (256 KiB), so that gemm_workspace_reserve covers
+    // the split-K calls of a later graph capture
+    return reinterpret_cast<int*>(workspace(dev, st, std::max<size_t>(count, 65536) * sizeof(int), kCounterSlot));
 }
 
 }  // namespace aiter_amd
@@ -1366,6 +1368,7 @@ int gemm_workspace_reserve(int device, aiter_stream_t stream, size_t bytes) {
     return safe_call([&] {
         DeviceGuard g(device);
         (void)workspace(device, reinterpret_cast<hipStream_t>(stream), bytes);
+        (void)lib_counters(device, reinterpret_cast<hipStream_t>(stream), 0);   // the split-K tile counters
     });
 }
 

@@ -125,12 +125,9 @@ AA_DEV float moe_act(float g, int act) {
 // values with the block's scale into 2 code bytes (the bytes quant32_fp4
 // gives) and the first writes the scale byte.  Every exit is taken by all 8
 // lanes of a block or none.
-// Split-K partials are written and read in the agent-coherent form (cache
-// policy sc1: past the XCD-private L2, to and from memory), so the split that
-// sums a tile sees what splits on other XCDs wrote without an L2 writeback or
-// invalidate; ws_rsrc covers the partials (byte offsets below 2^31).
-constexpr int kAgentCoherent = 16;
-
+// Split-K partials are written and read in the agent-coherent form
+// (kAgentCoherent), so the split that sums a tile sees what splits on other
+// XCDs wrote; ws_rsrc covers the partials (byte offsets below 2^31).
 template <bool QUANT>
 AA_DEV void moe_fold_item(__amdgpu_buffer_rsrc_t ws_rsrc, int splits, const MoeParams& mq, int64_t pos, int id,
                           float w, int c) {

@@ -115,6 +115,12 @@ AA_DEV f32x16v_t mma32x(const i32x4_t& b, const i32x4_t& a0, const i32x4_t& a1, 
     }
 }
 
+// Buffer cache policy of split-K partials that one workgroup writes and the
+// last-arriving split of the same tile (on any XCD) reads back: sc1, the
+// agent-coherent form (past the XCD-private L2, to and from memory), so no
+// L2 writeback or invalidate is needed between them (the MoE stage-1 split).
+constexpr int kAgentCoherent = 16;
+
 // Epilogue of a wave's (32*MA) x (32*NB) block of 32x32 MFMA accumulators
 // (lane l holds C[m = l%32][n = 8q + 4(l/32) + r] of each tile) written as
 // bf16 or f32, D = alpha*acc + beta*bias.  Stored directly, each global store

@@ -360,7 +360,8 @@ int aiter_amd_resolve_kernel_name(const char* name, int family, int a_pre, int b
 int aiter_amd_resolve_opus_kid(int kid, int out_f32, int64_t M);
 
 /* Pre-sizes the split-K fp32 workspace owned by (device, stream) to at least
- * `bytes`, so that a later HIP-graph capture never needs to allocate.  The
+ * `bytes` (and allocates its split-K tile counters, 64K of them), so that a
+ * later HIP-graph capture never needs to allocate.  The
  * reference's counterpart is the caller-provided semaphore / workspace
  * tensor of csrc/py_itfs_cu/asm_gemm_a16w16.cu:192-205 and
  * aiter/ops/opus/gemm_op_opus.py (opus_gemm_workspace_init). */
