@@ -155,8 +155,11 @@ __global__ __launch_bounds__(256, 2) void moe_stage2_stream_kernel(GemmParams p,
         });
         // ---- epilogue: lane holds rows 32i + l%32, columns 64 wave + 32 j + 8 q + 4 h + r.
         // Per-pair rows go through the wave's own LDS tile [BM][64] bf16
-        // (16-byte granules XOR-swizzled by row) so that each store writes
-        // 8 rows x 128 contiguous bytes; atomics (decode) are stored directly.
+        // (16-byte granules XOR-swizzled by row bits 1-3: two 128-byte rows
+        // share a 256-byte bank line, so 32 rows of one granule spread over
+        // all 16 granule positions, two rows each, the floor for 512 bytes)
+        // so that each store writes 8 rows x 128 contiguous bytes; atomics
+        // (decode) are stored directly.
         const int n0 = 256 * tn + 64 * wave;
         if (mq.per_pair) {
 #pragma unroll
@@ -169,7 +172,7 @@ __global__ __launch_bounds__(256, 2) void moe_stage2_stream_kernel(GemmParams p,
                     for (int q = 0; q < 4; ++q) {
                         const f32x16v_t& a = acc[i][j];
                         const int cc = 8 * j + 2 * q + h;   // 8-byte chunk of the 128-byte row
-                        *reinterpret_cast<uint2*>(ep + r * 128 + (((cc >> 1) ^ (r & 7)) * 16) + (cc & 1) * 8) =
+                        *reinterpret_cast<uint2*>(ep + r * 128 + (((cc >> 1) ^ ((r >> 1) & 7)) * 16) + (cc & 1) * 8) =
                             uint2{pack_bf16x2(a[4 * q] * wgt, a[4 * q + 1] * wgt),
                                   pack_bf16x2(a[4 * q + 2] * wgt, a[4 * q + 3] * wgt)};
                     }
@@ -178,7 +181,7 @@ __global__ __launch_bounds__(256, 2) void moe_stage2_stream_kernel(GemmParams p,
             for (int r0 = 0; r0 < BM; r0 += 8) {
                 const int r = r0 + (lane >> 3);
                 const int id = __shfl(ids_r[r0 / 64], r & 63);
-                const i32x4_t v = *reinterpret_cast<const i32x4_t*>(ep + r * 128 + (((lane & 7) ^ (r & 7)) * 16));
+                const i32x4_t v = *reinterpret_cast<const i32x4_t*>(ep + r * 128 + (((lane & 7) ^ ((r >> 1) & 7)) * 16));
                 const int tok = id & 0xffffff, slot = (int)((unsigned)id >> 24);
                 if (tok >= mq.token_num || slot >= mq.topk) continue;
                 *reinterpret_cast<i32x4_t*>(mq.out + ((int64_t)tok * mq.topk + slot) * mq.out_stride + n0 +

@@ -449,20 +449,32 @@ def test_moe_stage2_needs_no_ring_waits():
     loads and uses) and uses LDS only for a wave-private epilogue tile that the
     same wave writes and then reads back: LDS operations of one wave complete
     in issue order, so no wait or barrier publishes anything.  The model of
-    that tile: every read follows the wave's own write of the same bytes."""
+    that tile: every read follows the wave's own write of the same bytes.
+    The granule swizzle uses row bits 1-3, so each 8-byte store instruction
+    (32 rows of 16 bytes) puts at most two rows on one 16-byte granule of the
+    256-byte bank line (the floor for 512 bytes)."""
     bm = 32
+
+    def swz(r):
+        return (r >> 1) & 7
+
     written = set()
     for i in range(bm // 32):
-        for lane in range(64):
-            r = 32 * i + (lane & 31)
-            for j in range(2):
-                for q in range(4):
+        for j in range(2):
+            for q in range(4):
+                hits = {}
+                for lane in range(64):
+                    r = 32 * i + (lane & 31)
                     cc = 8 * j + 2 * q + (lane >> 5)
-                    written.add((r, (((cc >> 1) ^ (r & 7)) * 16) + (cc & 1) * 8))
-                    written.add((r, (((cc >> 1) ^ (r & 7)) * 16) + (cc & 1) * 8 + 4))
+                    off = ((cc >> 1) ^ swz(r)) * 16 + (cc & 1) * 8
+                    written.add((r, off))
+                    written.add((r, off + 4))
+                    g = ((r * 128 + off) % 256) // 16
+                    hits.setdefault(g, set()).add(r)
+                assert max(len(v) for v in hits.values()) <= 2
     for r0 in range(0, bm, 8):
         for lane in range(64):
             r = r0 + (lane >> 3)
-            base = ((lane & 7) ^ (r & 7)) * 16
+            base = ((lane & 7) ^ swz(r)) * 16
             for b in range(0, 16, 4):
                 assert (r, base + b) in written
