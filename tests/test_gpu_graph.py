@@ -3,9 +3,11 @@ stream whose library workspace an eager call has already sized, then the graph
 is replayed several times with the program's own eager work and
 synchronisations between replays; every replay must equal the eager result
 (bit-exact; the end-to-end MoE path, whose stage 2 adds the slots with
-packed-bf16 atomics in any order, within 4 bf16 ulps of the largest output:
+packed-bf16 atomics in any order, within 8 bf16 ulps of the largest output:
 a sum of bf16-rounded adds in another order moves by a few ulps of its
-largest partial sum, also where the terms cancel to a small result)."""
+largest partial sum, which can exceed the result where terms cancel; a
+missing or doubled contribution moves an element by the size of the
+outputs)."""
 import importlib
 
 import numpy as np
@@ -47,7 +49,7 @@ def _replay_check(fn, cuda, exact=True):
             if exact:
                 assert torch.equal(o.view(torch.uint8), e.view(torch.uint8)), f"replay {rep} differs"
             else:
-                tol = 2.0 ** -6 * e.float().abs().max().item() + 1e-2
+                tol = 2.0 ** -5 * e.float().abs().max().item() + 1e-2
                 err = (o.float() - e.float()).abs().max().item()
                 assert err <= tol, f"replay {rep}: max difference {err} > {tol}"
 
