@@ -549,7 +549,8 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     const int req_splits = c.split_count > 0 ? c.split_count : (c.log2_split >= 0 ? 1 << std::min(c.log2_split, 16) : 0);
     if (inst->skinny && inst->split && req_splits > 0) splits = req_splits;
     if (inst->skinny) AA_CHECK(M <= inst->bm, "skinny kernel ", inst->name, " covers M <= ", inst->bm);
-    AA_CHECK(!c.capture || (inst->skinny && !inst->split && !batched), "planned calls take non-split skinny kernels");
+    AA_CHECK(!c.capture || (inst->skinny && !inst->split && !inst->stream_k && !batched),
+             "planned calls take non-split skinny kernels");
 
     if (!inst->skinny) {
         p.tiles_m = (int)((M + inst->bm - 1) / inst->bm);
@@ -611,6 +612,21 @@ void run_gemm(const GemmCall& c, hipStream_t stream) {
     } else {
         // the skinny kernels split K in k-pairs (one scale dword each)
         const int kpairs = ksteps / 2;
+        if (inst->stream_k) {
+            // up to one workgroup per CU over the (column block, k-pair)
+            // units, and about 8 ranges per block at most (the range that sums
+            // a block loads the others' partials 8 at a time); two partial
+            // slots per workgroup, one arrival counter per block
+            AA_CHECK(!batched && !c.scratch, "stream-K skinny kernel ", inst->name, ": no batch, no caller scratch");
+            const int64_t nblk = (N + inst->bn - 1) / inst->bn;
+            const int grid = (int)std::min<int64_t>(std::min<int64_t>(cus, nblk * 8), nblk * kpairs);
+            p.k_steps_per_split = kpairs;
+            p.ws = split_buffer(c, dev, stream, (size_t)2 * grid * inst->bm * inst->bn * sizeof(float));
+            p.cnt = lib_counters(dev, stream, (size_t)nblk);
+            inst->fn(p, dim3((unsigned)grid), stream);
+            AA_HIP(hipGetLastError());
+            return;
+        }
         splits = batched ? 1 : std::max(1, std::min(splits, kpairs));
         p.k_steps_per_split = (kpairs + splits - 1) / splits;
         splits = (kpairs + p.k_steps_per_split - 1) / p.k_steps_per_split;

@@ -98,6 +98,7 @@ struct GemmParams {
     void* D;
     const float* bias;
     float* ws;           // split-K f32 partial sums: [M, N] (skinny), [splits][M][N] (tiles)
+    int* cnt;            // stream-K: one zeroed arrival counter per column block
     int64_t lda, ldb;    // bytes per row (row-major) / per row of the preshuffled matrix
     int64_t ldd;         // elements per output row
     int64_t ld_bias;     // elements per bias row (0 = broadcast one row)

@@ -40,6 +40,7 @@ struct Instance {
     LaunchFn fn;
     bool persistent = false;   // grid of min(tiles, CUs) workgroups walking the tiles
     int rank = 0;              // among skinny forms of one shape the heuristic takes the highest
+    bool stream_k = false;     // skinny stream-K form: one workgroup per CU, partial blocks summed in place
 };
 
 template <int KA, int KB, int BM, int BN, bool AP, bool BP, bool OF>
@@ -112,6 +113,20 @@ void launch_skinny_alds(const GemmParams& p, dim3 grid, hipStream_t s) {
         gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, true><<<grid, 64 * NW, 0, s>>>(p);
     else
         gemm_skinny_alds_kernel<KA, MF, NW, BP, false, false, NB, S, BL, false><<<grid, 64 * NW, 0, s>>>(p);
+}
+
+// stream-K skinny kernel (row-major bf16 B): grid = workgroups sharing the
+// units; p.ws holds 2 * grid.x partial slots, p.cnt the block counters
+template <int MF, int NB, int NW, int S = 2, bool OF = false>
+void launch_skinny_sk(const GemmParams& p, dim3 grid, hipStream_t s) {
+    AA_CHECK(p.ws && p.cnt, "stream-K skinny kernel: no workspace");
+    // lane offsets reach the rows of the last block past N
+    AA_CHECK((int64_t)p.M * p.lda < (1LL << 31) && (int64_t)(p.N + 32) * p.ldb < (1LL << 31),
+             "stream-K skinny kernel: A or B larger than 2 GiB");
+    if (b_streams<kBf16>(p))
+        gemm_skinny_sk_kernel<MF, NW, OF, NB, S, true><<<grid, 64 * NW, 0, s>>>(p);
+    else
+        gemm_skinny_sk_kernel<MF, NW, OF, NB, S, false><<<grid, 64 * NW, 0, s>>>(p);
 }
 
 // the short-K direct skinny kernel: KP k-pairs at most (K <= KP * 256 for

@@ -292,4 +292,285 @@ __global__ __launch_bounds__(64 * NW) void gemm_skinny_alds_kernel(GemmParams p)
     }
 }
 
+// Stream-K form of the row-major bf16 staged kernel (A and B through LDS).
+// A decode shape with fewer 32-column blocks than CUs leaves CUs idle (N =
+// 7168: 224 blocks on 256 CUs), and splitting every block in two leaves the
+// same longest share per CU.  Here gridDim.x workgroups (one per CU) share
+// the U = blocks x k-pairs units evenly: workgroup g takes units
+// [g*U/G, (g+1)*U/G).  It walks its range in windows of at most two column
+// blocks; the waves take the window's units in turn (wave w: units w, w+NW,
+// ...), each accumulating the units of the window's first block, then
+// those of its second, in two register sets.  A block whose units all lie in
+// one range is stored directly.  A block split over ranges leaves one f32
+// partial per range in that range's slot (workgroup g, slot 0 for the
+// range's first segment, 1 for its last), written with agent-coherent
+// stores (past the XCD-private L2); after they have landed one thread
+// increments the block's arrival counter, and the range that arrives last
+// loads the block's slots with agent-coherent loads, adds them in range
+// order (the result does not depend on the arrival order), stores the block
+// and sets the counter back to zero.  p.ws: 2 * G slots of 16*MF x 16*NB
+// floats; p.cnt: one zeroed counter per column block.  The host caps G at
+// 8 workgroups per block: each range beyond that adds one more partial to
+// load for the range that sums the block.
+template <int MF, int NW, bool OUT_F32, int NB, int S, bool NT>
+__global__ __launch_bounds__(64 * NW) void gemm_skinny_sk_kernel(GemmParams p) {
+    static_assert(NB == 1 || NB == 2, "one or two column blocks per workgroup");
+    using C = SkinnyLdsCfg<kBf16, MF, NW, false, false, OUT_F32, NB, S, true>;
+    using St = SkinnyLdsStage<kBf16, MF, NB, true>;
+    constexpr int ITEMS = MF * NB * 64;                    // f32x4 items of one block's sum
+    constexpr int LDS = C::LDS > 2 * NW * ITEMS * 16 ? C::LDS : 2 * NW * ITEMS * 16;
+    static_assert(LDS <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[LDS];
+    __shared__ int last_flag[2];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    constexpr int BW = 16 * NB;   // columns per block
+    const int T = p.K / C::KPAIR;
+    const int nblk = (p.N + BW - 1) / BW;
+    const int64_t U = (int64_t)nblk * T, G = gridDim.x, g = blockIdx.x;
+    const int64_t lo0 = g * U / G, hi = (g + 1) * U / G;
+    // the range that holds unit x: the largest g with g*U/G <= x
+    auto owner = [&](int64_t x) -> int64_t { return ((x + 1) * G - 1) / U; };
+
+    const __amdgpu_buffer_rsrc_t ar = make_rsrc(p.A, (int64_t)p.M * p.lda);
+    // the whole of B: rows past N read as zeros, their columns are never stored
+    const __amdgpu_buffer_rsrc_t br = make_rsrc(p.B, (int64_t)p.N * p.ldb);
+    const __amdgpu_buffer_rsrc_t wr = make_rsrc(p.ws, 2 * G * ITEMS * 16);
+    int a_voff[C::NCP];
+#pragma unroll
+    for (int c = 0; c < C::NCP; ++c) {
+        const int r = c * C::RPI + lane / C::PPR;
+        a_voff[c] = r * (int)p.lda + ((lane % C::PPR) ^ C::swz(r)) * 16;
+    }
+    int b_voff[2 * NB];
+#pragma unroll
+    for (int c = 0; c < 2 * NB; ++c) {
+        const int r = c * 8 + lane / 8;
+        b_voff[c] = r * (int)p.ldb + ((lane % 8) ^ ((r >> 1) & 7)) * 16;
+    }
+    uint8_t* const abase = smem + wave * S * C::SET;
+    const int rd_rowb = (lane & 15) * 128;
+    const int rd_swb = ((lane & 15) >> 1) & 7;
+    const int rd_row = (lane & 15) * C::ROWB;
+    const int rd_sw = C::swz(lane & 15);
+    const int rd_q = lane >> 4;
+    auto fence = [] { __builtin_amdgcn_sched_barrier(0); };
+
+    for (int64_t x = lo0; x < hi;) {
+        const int b0 = (int)(x / T);
+        const int64_t xe = min(hi, (int64_t)(b0 + 2) * T);   // window [x, xe): blocks b0 and b0 + 1
+        const int64_t xb = min(xe, (int64_t)(b0 + 1) * T);   // first unit of block b0 + 1
+        const int64_t ubase = x + wave;                       // unit t of this wave: ubase + t*NW
+        const int npairs = ubase < xe ? (int)((xe - ubase + NW - 1) / NW) : 0;
+        // consumed units before tsw are block b0's
+        const int tsw = xb > ubase ? (int)((xb - ubase + NW - 1) / NW) : 0;
+
+        f32x4_t acc[MF][NB], acc0[MF][NB];
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                acc0[i][j] = acc[i][j];
+            }
+
+        auto issue = [&](int t, int buf) {
+            const int64_t u = ubase + (int64_t)t * NW;
+            const int blk = u < xb ? b0 : b0 + 1;
+            const int pr = (int)(u - (int64_t)blk * T);
+            uint8_t* dst = abase + buf * C::SET;
+#pragma unroll
+            for (int c = 0; c < C::NCP; ++c) dma16(ar, dst + c * 1024, a_voff[c], pr * C::ROWB);
+            // the block's row offset goes into the range-checked lane offset
+            const int brow = blk * BW * (int)p.ldb;
+#pragma unroll
+            for (int c = 0; c < 2 * NB; ++c)
+                dma16<NT ? kLoadNt : 0>(br, dst + C::ABUF + c * 1024, b_voff[c] + brow, pr * 128);
+        };
+        auto mma = [&](int buf) {
+            const uint8_t* src = abase + buf * C::SET + rd_row;
+            const uint8_t* bsl = abase + buf * C::SET + C::ABUF + rd_rowb;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                i32x4_t a[MF][C::FA];
+#pragma unroll
+                for (int i = 0; i < MF; ++i)
+#pragma unroll
+                    for (int f = 0; f < C::FA; ++f) {
+                        const int q = (h * C::A_STEP + f * 64) / 16 + rd_q;
+                        a[i][f] = *reinterpret_cast<const i32x4_t*>(src + i * 16 * C::ROWB + ((q ^ rd_sw) * 16));
+                    }
+                i32x4_t bl[NB];
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+                    bl[j] = *reinterpret_cast<const i32x4_t*>(bsl + j * 16 * 128 + (((h * 4 + rd_q) ^ rd_swb) * 16));
+#pragma unroll
+                for (int i = 0; i < MF; ++i)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) acc[i][j] = mma_step<kBf16, kBf16>(&bl[j], a[i], acc[i][j], 0, 0, 0, 0);
+            }
+        };
+        // unit t (consumed in order): the first unit of block b0 + 1 moves
+        // the first block's sum aside
+        auto consume = [&](int t, auto set, auto after) {
+            fence();
+            wait_vmcnt<decltype(after)::value * (C::NCP + 2 * NB)>();
+            fence();
+            if (t == tsw) {
+#pragma unroll
+                for (int i = 0; i < MF; ++i)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        acc0[i][j] = acc[i][j];
+                        acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                    }
+            }
+            mma(decltype(set)::value);
+        };
+        if (npairs > 0 && npairs < S) {
+            static_for<S - 1>([&](auto nn) {
+                constexpr int N = decltype(nn)::value + 1;
+                if (npairs == N) {
+                    static_for<N>([&](auto u) { issue(decltype(u)::value, decltype(u)::value); });
+                    static_for<N>([&](auto u) {
+                        constexpr int UU = decltype(u)::value;
+                        consume(UU, u, std::integral_constant<int, N - 1 - UU>{});
+                    });
+                }
+            });
+        } else if (npairs >= S) {
+            static_for<S - 1>([&](auto u) { issue(decltype(u)::value, decltype(u)::value); });
+            int t = 0;   // units consumed; t % S == 0 at the top of the loop
+            for (; t + 2 * S - 2 < npairs; t += S) {
+                static_for<S>([&](auto u) {
+                    constexpr int UU = decltype(u)::value, I = (UU + S - 1) % S;
+                    fence();
+                    issue(t + UU + S - 1, I);
+                    consume(t + UU, u, std::integral_constant<int, S - 1>{});
+                });
+            }
+            const int rem = npairs - t - (S - 1);
+            static_for<S>([&](auto rr) {
+                constexpr int R = decltype(rr)::value;
+                if (rem == R) {
+                    static_for<S - 1 + R>([&](auto u) {
+                        constexpr int UU = decltype(u)::value;
+                        if constexpr (UU < R) {
+                            constexpr int I = (UU + S - 1) % S;
+                            fence();
+                            issue(t + UU + S - 1, I);
+                            consume(t + UU, std::integral_constant<int, UU % S>{}, std::integral_constant<int, S - 1>{});
+                        } else {
+                            consume(t + UU, std::integral_constant<int, UU % S>{},
+                                    std::integral_constant<int, S - 2 + R - UU>{});
+                        }
+                    });
+                }
+            });
+        }
+        // register set of each block: a wave that switched holds block b0's
+        // sum in acc0 and block b0 + 1's in acc; one that did not, b0's in acc
+        const bool switched = tsw < npairs;
+
+        // every copy has landed; the reduction reuses the buffers once all
+        // waves have read theirs
+        __syncthreads();
+        f32x4_t* red = reinterpret_cast<f32x4_t*>(smem);   // [2][NW][MF*NB][64]
+#pragma unroll
+        for (int i = 0; i < MF; ++i)
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int ij = i * NB + j;
+                red[(wave * MF * NB + ij) * 64 + lane] = switched ? acc0[i][j] : acc[i][j];
+                red[((NW + wave) * MF * NB + ij) * 64 + lane] = switched ? acc[i][j] : f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+        __syncthreads();
+        // segment of each set in this window: [s_lo, s_hi) within its block
+        auto seg_lo = [&](int st) { return st ? xb : x; };
+        auto seg_hi = [&](int st) { return st ? xe : xb; };
+        bool any_partial = false;
+        constexpr int PER = 2 * ITEMS / (64 * NW) > 0 ? 2 * ITEMS / (64 * NW) : 1;
+        static_assert(2 * ITEMS % (64 * NW) == 0 || 2 * ITEMS < 64 * NW, "items per thread");
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+            const int it = threadIdx.x + k * 64 * NW;
+            if (it >= 2 * ITEMS) continue;
+            const int st = it / ITEMS, ij = (it % ITEMS) / 64, l = it % 64;
+            f32x4_t s = red[(st * NW * MF * NB + ij) * 64 + l];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) s += red[((st * NW + w) * MF * NB + ij) * 64 + l];
+            const int64_t slo = seg_lo(st), shi = seg_hi(st);
+            if (slo >= shi) continue;   // no second block in this window
+            const int blk = b0 + st;
+            const bool whole = slo == (int64_t)blk * T && shi == (int64_t)(blk + 1) * T;
+            if (whole) {
+                const int i = ij / NB, j = ij % NB;
+                store_frag<OUT_F32>(p, s, i * 16 + (l & 15), blk * BW + 16 * j + 4 * (l >> 4));
+            } else {
+                const int which = slo == lo0 ? 0 : 1;
+                const int off = (int)(((g * 2 + which) * ITEMS + (it % ITEMS)) * 16);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4_t, s), wr, off, 0, kAgentCoherent);
+            }
+        }
+        // arrival of the partial blocks (uniform: depends on the window only)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            const int64_t slo = seg_lo(st), shi = seg_hi(st);
+            const int blk = b0 + st;
+            if (slo < shi && !(slo == (int64_t)blk * T && shi == (int64_t)(blk + 1) * T)) any_partial = true;
+        }
+        if (any_partial) {
+            wait_vmcnt<0>();
+            __syncthreads();
+            if (threadIdx.x < 2) {
+                const int st = threadIdx.x;
+                const int64_t slo = seg_lo(st), shi = seg_hi(st);
+                const int blk = b0 + st;
+                int last = 0;
+                if (slo < shi && !(slo == (int64_t)blk * T && shi == (int64_t)(blk + 1) * T)) {
+                    const int np = (int)(owner((int64_t)(blk + 1) * T - 1) - owner((int64_t)blk * T) + 1);
+                    last = atomicAdd(p.cnt + blk, 1) == np - 1;
+                    if (last) __hip_atomic_store(p.cnt + blk, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
+                last_flag[st] = last;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int it = threadIdx.x + k * 64 * NW;
+                if (it >= 2 * ITEMS) continue;
+                const int st = it / ITEMS;
+                if (!last_flag[st]) continue;
+                const int blk = b0 + st, ij = (it % ITEMS) / 64, l = it % 64;
+                const int64_t x0 = (int64_t)blk * T;
+                const int64_t gf = owner(x0), gl = owner(x0 + T - 1);
+                // up to 8 slots in flight; slots past the last range read as
+                // zeros (an offset past the descriptor) and add nothing
+                f32x4_t s = f32x4_t{0.f, 0.f, 0.f, 0.f};
+                for (int64_t g0 = gf; g0 <= gl; g0 += 8) {
+                    f32x4_t v[8];
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const int64_t gg = g0 + q;
+                        const int which = gg * U / G < x0 ? 1 : 0;
+                        const int off = gg <= gl ? (int)(((gg * 2 + which) * ITEMS + (it % ITEMS)) * 16) : 0x7ffffff0;
+                        v[q] = __builtin_bit_cast(f32x4_t,
+                                                  __builtin_amdgcn_raw_buffer_load_b128(wr, off, 0, kAgentCoherent));
+                    }
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) s += v[q];
+                }
+                const int i = ij / NB, j = ij % NB;
+                store_frag<OUT_F32>(p, s, i * 16 + (l & 15), blk * BW + 16 * j + 4 * (l >> 4));
+            }
+        }
+        x = xe;
+        // the next window's waits count its own loads only; the buffers and
+        // flags are reused by it
+        wait_vmcnt<0>();
+        __syncthreads();
+    }
+}
+
 }  // namespace aiter_amd
