@@ -19,7 +19,7 @@ its issue orders: B operand loads spread over the k-steps, and the BLDS order
 of row-major bf16 B, A copies before the wait and B copies after it),
 gemm_t32.h ``gemm_t32_kernel``, gemm_flat_persist.h (prologue, tile
 transitions), gemm_skinny_lds.h (S pairs in flight, its up-front, steady and
-tail phases, buffer refills), gemm_lds_persist.h (two stage buffers, the
+tail phases, buffer refills; the stream-K form's windows), gemm_lds_persist.h (two stage buffers, the
 epilogue's use of a stage buffer, tile transitions), and moe_stage2.h (no
 ring: its wave-private epilogue tile).  A wrong count here (the flat
 kernel's former prologue wait of (NS - 2) * NDMA) lets the first stage read a
@@ -287,8 +287,8 @@ def skinny_lds_lp(ka, mf, nb, bl):
     return ncp + b_ops + scales
 
 
-def run_skinny_lds(s, lp, npairs):
-    w = Wave()
+def run_skinny_lds(s, lp, npairs, w=None, tag=0):
+    w = Wave() if w is None else w
     bad = []
     held = {}
     consumed = []
@@ -297,12 +297,12 @@ def run_skinny_lds(s, lp, npairs):
         if buf in held and held[buf] not in consumed:
             bad.append(("refilled before use", pair, buf))
         held[buf] = pair
-        w.issue(("P", pair), lp)
+        w.issue(("P", tag, pair), lp)
 
     def consume(buf, after):
         pair = held[buf]
         w.wait(after * lp)
-        if not w.complete(("P", pair)):
+        if not w.complete(("P", tag, pair)):
             bad.append(("wait misses", pair))
         consumed.append(pair)
 
@@ -345,6 +345,25 @@ def test_skinny_lds_waits(ka, mf, nb, s, bl, npairs):
     lp = skinny_lds_lp(ka, mf, nb, bl)
     assert (s - 1) * lp < 64          # the kernel's static_assert: vmcnt range
     assert run_skinny_lds(s, lp, npairs) == []
+
+
+# gemm_skinny_sk_kernel (the stream-K form, row-major bf16 B): each window of
+# a workgroup's range runs the same per-wave schedule over the wave's units
+# of that window; between windows the wave issues the window's output stores
+# (a whole block's stores, or a partial's agent-coherent stores) and waits
+# for vmcnt(0), so the next window's waits count its own copies only.
+SKINNY_SK = [("bf16", 1, 2, 2, True), ("bf16", 2, 2, 2, True), ("bf16", 4, 2, 2, True)]
+
+
+@pytest.mark.parametrize("ka,mf,nb,s,bl", SKINNY_SK)
+@pytest.mark.parametrize("windows", [[1], [4], [2, 5], [1, 1, 4], [33, 2], [0, 3], [3, 0, 1]])
+def test_skinny_sk_waits(ka, mf, nb, s, bl, windows):
+    lp = skinny_lds_lp(ka, mf, nb, bl)
+    w = Wave()
+    for i, npairs in enumerate(windows):
+        assert run_skinny_lds(s, lp, npairs, w, tag=i) == []
+        w.issue(("store", i), 2)   # the window's output (or partial) stores
+        w.wait(0)
 
 
 def test_skinny_lds_model_catches_a_short_tail_wait():
