@@ -178,14 +178,21 @@ __global__ __launch_bounds__(kThreads) void moe_sort_single(SortParams p, uint8_
     __shared__ SortSmem sm;
     const int nt = local_tokens(p);
     const int n = nt * p.topk;
-    // the first chunk's entries stay in registers from one load (expert id
-    // and weight issued together); later chunks reload theirs
+    // every chunk's entries stay in registers from one round of loads
+    // (expert ids and weights of all chunks issued together), so neither the
+    // count nor the placement of a later chunk waits on another load
     const int tid = threadIdx.x;
-    const int e0 = expert_of(p, tid, n);
-    float w0 = 0.0f;
-    if (tid < n) {
-        const int t = tid / p.topk, s = tid - t * p.topk;
-        w0 = p.topk_w[(int64_t)t * p.w_stride + s];
+    int ev[kSingleChunks];
+    float wv[kSingleChunks];
+#pragma unroll
+    for (int k = 0; k < kSingleChunks; ++k) {
+        const int i = tid + k * kThreads;
+        ev[k] = expert_of(p, i, n);
+        wv[k] = 0.0f;
+        if (i < n) {
+            const int t = i / p.topk, s = i - t * p.topk;
+            wv[k] = p.topk_w[(int64_t)t * p.w_stride + s];
+        }
     }
     // a small moe_buf is cleared here rather than by a second launch
     for (int64_t b = (int64_t)tid * 16; b + 16 <= zero_bytes; b += kThreads * 16)
@@ -194,17 +201,16 @@ __global__ __launch_bounds__(kThreads) void moe_sort_single(SortParams p, uint8_
     fill_padding(p, 0, p.max_padded, tid, kThreads);   // ordered before placement by the barriers below
     for (int x = tid; x < kMaxE; x += kThreads) sm.cnt[x] = 0;
     __syncthreads();
-    if (e0 >= 0) atomicAdd(&sm.cnt[e0], 1);
-    for (int i = tid + kThreads; i < n; i += kThreads) {
-        const int e = expert_of(p, i, n);
-        if (e >= 0) atomicAdd(&sm.cnt[e], 1);
-    }
+#pragma unroll
+    for (int k = 0; k < kSingleChunks; ++k)
+        if (ev[k] >= 0) atomicAdd(&sm.cnt[ev[k]], 1);
     __syncthreads();
     scan_experts(p, sm, nt);
     for (int x = tid; x < p.E; x += kThreads) sm.base[x] = sm.off[x];
     __syncthreads();
-    place_chunk(p, sm, 0, n, e0, w0);
-    for (int c0 = kThreads; c0 < n; c0 += kThreads) place_chunk(p, sm, c0, n);
+#pragma unroll
+    for (int k = 0; k < kSingleChunks; ++k)
+        if (k == 0 || k * kThreads < n) place_chunk(p, sm, k * kThreads, n, ev[k], wv[k]);
 }
 
 __global__ __launch_bounds__(kThreads) void moe_sort_count(SortParams p) {
