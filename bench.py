@@ -478,7 +478,7 @@ def bench_fused_a16w16(dev, ms=(1, 16, 64), n4=4096, n16=256, k=7168):
     return res
 
 
-def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
+def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096), model="deepseek"):
     """fused_moe A4W4 at the reference test's DeepSeek shape (op_tests/test_moe_2stage.py
     defaults: model_dim 7168, inter_dim 256, 257 experts, topk 9), graph-captured
     so that host time is excluded.  Weights are random fp4 bytes with scale
@@ -488,7 +488,7 @@ def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
     dense MXFP4 peak."""
     import aiter_amd
 
-    E, topk, dim, inter = 257, 9, 7168, 256
+    E, topk, dim, inter = MOE_MODELS[model]
     g = torch.Generator(device=dev).manual_seed(11)
     w1 = torch.randint(0, 256, (E * 2 * inter, dim // 2), dtype=torch.uint8, device=dev, generator=g)
     w2 = torch.randint(0, 256, (E * dim, inter // 2), dtype=torch.uint8, device=dev, generator=g)
@@ -508,7 +508,7 @@ def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
         fn = lambda: aiter_amd.fused_moe(x, w1, w2, tw, ti, quant_type=aiter_amd.QuantType.per_1x32, w1_scale=w1s,
                                          w2_scale=w2s)
         t = time_graph(fn, 10, 2)
-        stages = _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter)
+        stages = _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter, REF_MOE[model])
         touched = int(torch.unique(ti).numel())
         nbytes = touched * per_expert + m * dim * 2 * 2
         flop = 2 * m * topk * (2 * inter * dim + dim * inter)
@@ -516,7 +516,7 @@ def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
                     "frac_mxfp4_peak": round(flop / t / 1e12 / PEAK_MXFP4, 4), "experts_touched": touched,
                     "GBps": round(nbytes / t / 1e9, 1), "frac_hbm": round(nbytes / t / 1e9 / PEAK_HBM, 4),
                     "block_m": aiter_amd.get_block_size_M(m, topk, E, inter), **stages})
-        log(f"fused_moe tokens={m}: {out[-1]}")
+        log(f"fused_moe {model} tokens={m}: {out[-1]}")
     return out
 
 
@@ -524,6 +524,28 @@ def bench_moe(dev, tokens=(1, 16, 128, 1024, 4096)):
 # 257 experts, topk 9: aiter/configs/model_configs/dsv3_fp4_tuned_fmoe.csv:2,6,9,12,14
 REF_MOE_STAGES = {1: (11.3537, 7.5406), 16: (40.5338, 24.9519), 128: (87.5346, 54.4124),
                   1024: (106.2571, 107.529), 4096: (191.9986, 283.9092)}
+
+# (experts, topk, model_dim, inter_dim) of the models whose MXFP4 fused-MoE
+# rows the reference tunes, and their tuned (us1, us2) at 1/16/128/1024/4096
+# tokens (rows 2, 6, 9, 12, 14 of each file; Qwen3.5's 1- and 16-token rows
+# are one-stage kernels: us2 0, us1 the whole call)
+MOE_MODELS = {"deepseek": (257, 9, 7168, 256), "glm5": (257, 9, 6144, 2048), "kimik2": (384, 8, 7168, 256),
+              "minimax_m25": (256, 8, 3072, 256), "qwen3_5_397b": (512, 10, 4096, 256)}
+REF_MOE = {
+    "deepseek": REF_MOE_STAGES,
+    # aiter/configs/model_configs/glm5_fp4_tuned_fmoe.csv:2,6,9,12,14
+    "glm5": {1: (23.1763, 16.8433), 16: (233.4281, 127.2874), 128: (513.8856, 276.6438),
+             1024: (544.8517, 320.5397), 4096: (978.5945, 784.0105)},
+    # aiter/configs/model_configs/kimik2_fp4_tuned_fmoe.csv:2,6,9,12,14
+    "kimik2": {1: (13.6475, 7.7145), 16: (35.9287, 23.6549), 128: (108.3724, 66.6968),
+               1024: (121.0563, 106.3806), 4096: (158.9084, 270.351)},
+    # aiter/configs/model_configs/minimax_m25_fp4_tuned_fmoe.csv:2,6,9,12,14
+    "minimax_m25": {1: (12.6929, 6.4582), 16: (19.2822, 15.3136), 128: (41.3453, 26.5566),
+                    1024: (45.8141, 47.6451), 4096: (82.4129, 126.4326)},
+    # aiter/configs/model_configs/qwen3_5_397b_fp4_tuned_fmoe.csv:2,6,9,12,14
+    "qwen3_5_397b": {1: (19.3721, 0.0), 16: (55.31, 0.0), 128: (87.4931, 53.1125), 1024: (110.6725, 81.2088),
+                     4096: (149.0609, 201.2182)},
+}
 
 
 def fused_moe_module():
@@ -534,7 +556,7 @@ def fused_moe_module():
     return importlib.import_module("aiter_amd.fused_moe")
 
 
-def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter):
+def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter, ref=None):
     """Each launch group of fused_moe timed on its own (graph-replayed, inputs
     from an eager run of the steps before it): the routing sort, the sorted
     activation quant, stage 1 with its fused output quant (and its split-K
@@ -580,8 +602,9 @@ def _moe_stage_times(aiter_amd, x, w1, w2, w1s, w2s, tw, ti, E, topk, dim, inter
         res["moe_sum_us"] = 0.0
     res = {k: (round(v * 1e6, 1) if isinstance(v, float) else v) for k, v in res.items()}
     res["stages_us"] = round(res["stage1_us"] + res["stage2_us"] + res["moe_sum_us"], 1)
-    if m in REF_MOE_STAGES:
-        r1, r2 = REF_MOE_STAGES[m]
+    ref = REF_MOE_STAGES if ref is None else ref
+    if m in ref:
+        r1, r2 = ref[m]
         res["ref_stage1_us"], res["ref_stage2_us"] = r1, r2
         res["stages_vs_ref"] = round((r1 + r2) / res["stages_us"], 3)
     return res
@@ -799,6 +822,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--quick", action="store_true", help="headline only")
     ap.add_argument("--moe", action="store_true", help="only the fused-MoE workloads (for profiling)")
+    ap.add_argument("--moe-models", action="store_true",
+                    help="fused MoE at each MOE_MODELS shape against the reference's tuned stage times")
     ap.add_argument("--decode", action="store_true", help="only the decode workloads (configs[1] and configs[4])")
     ap.add_argument("--sweep", action="store_true", help="only the prefill sweep (configs[4]) and configs[3]")
     ap.add_argument("--cpu", action="store_true", help="only the CPU baseline")
@@ -819,6 +844,13 @@ def main():
         return
     if args.moe:
         print(json.dumps({"fused_moe_a4w4_deepseek": bench_moe(dev)}), flush=True)
+        return
+    if args.moe_models:
+        res = {}
+        for name in MOE_MODELS:
+            res[name] = bench_moe(dev, model=name)
+            torch.cuda.empty_cache()
+        print(json.dumps({"fused_moe_models": res}), flush=True)
         return
     if args.decode:
         print(json.dumps({"decode": bench_decode(dev), "decode_sweep": bench_decode_sweep(dev)}), flush=True)

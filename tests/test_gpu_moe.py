@@ -464,16 +464,24 @@ def test_fused_moe(cuda, m, e, topk, act, doweight, use_mask):
     _accept(out.float().cpu().numpy(), ref, min_close=0.9)
 
 
+# (experts, topk, model_dim, inter_dim) of the models whose MXFP4 fused-MoE
+# rows the reference tunes (aiter/configs/model_configs/*_fp4_tuned_fmoe.csv):
+# DeepSeek-V3, GLM-5, Kimi-K2, MiniMax-M2.5, Qwen3.5-397B
+MOE_MODELS = {"deepseek": (257, 9, 7168, 256), "glm5": (257, 9, 6144, 2048), "kimik2": (384, 8, 7168, 256),
+              "minimax_m25": (256, 8, 3072, 256), "qwen3_5_397b": (512, 10, 4096, 256)}
+
+
+@pytest.mark.parametrize("model", list(MOE_MODELS))
 @pytest.mark.parametrize("m", [64, 1])
-def test_fused_moe_deepseek_shape(cuda, m):
-    """model_dim 7168, inter_dim 256, 257 experts, topk 9, 64 tokens (one
-    pass over K) and 1 token (decode: stage 1 splits K over 10 workgroups
-    per tile); the oracle recomputes up to 4 tokens from the experts they
-    route to."""
+def test_fused_moe_model_shapes(cuda, m, model):
+    """The models' shapes (DeepSeek: model_dim 7168, inter_dim 256, 257
+    experts, topk 9), 64 tokens (one pass over K) and 1 token (decode: stage
+    1 splits K over several workgroups per tile); the oracle recomputes a few
+    tokens from the experts they route to."""
     import aiter_amd
 
-    e, topk, dim, inter = 257, 9, 7168, 256
-    announce(f"fused_moe deepseek m={m}")
+    e, topk, dim, inter = MOE_MODELS[model]
+    announce(f"fused_moe {model} m={m}")
     rng = np.random.default_rng(500)
     ids, w = _routing(m, e, topk, rng)
     x = to_bf16_f32(rng.standard_normal((m, dim)).astype(np.float32))
@@ -488,7 +496,7 @@ def test_fused_moe_deepseek_shape(cuda, m):
                               quant_type=aiter_amd.QuantType.per_1x32, w1_scale=aiter_amd.shuffle_scale(w1s),
                               w2_scale=aiter_amd.shuffle_scale(w2s))
     torch.cuda.synchronize()
-    toks = [0, 17, 40, 63] if m > 63 else [0]
+    toks = ([0, 17, 40, 63] if inter <= 256 else [0, 40]) if m > 63 else [0]
     experts = sorted(set(ids[toks].reshape(-1).tolist()))
     remap = {ex: i for i, ex in enumerate(experts)}
     sub_ids = np.vectorize(remap.get)(ids[toks]).astype(np.int32)
@@ -500,4 +508,9 @@ def test_fused_moe_deepseek_shape(cuda, m):
     w2sq = w2s.view(e, n2, -1)[sel].reshape(len(experts) * n2, -1).cpu().numpy()
     ref = O.bf16_bits_to_f32(MO.fused_moe_ref(x[toks], MO.dequant_experts(w1q, w1sq), MO.dequant_experts(w2q, w2sq),
                                               sub_ids, w[toks]))
-    _accept(out.float().cpu().numpy()[toks], ref, min_close=0.9)
+    # every output sums 9 x inter_dim requantised MXFP4 intermediates; one
+    # whose bf16 value sits on an fp4 rounding boundary (stage 1's f32 sums
+    # run in another order than the oracle's, split over K at decode) moves
+    # by one fp4 step, so with inter_dim 2048 more outputs leave 1e-2 while
+    # logits_diff stays far below its bound (1.1e-5 for GLM-5 at one token)
+    _accept(out.float().cpu().numpy()[toks], ref, min_close=0.9 if inter <= 256 else 0.85)
